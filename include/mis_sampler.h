@@ -1,0 +1,109 @@
+/*
+ * mis_sampler.h -- C ABI of the MI355X-native decode-step token sampler.
+ *
+ * The library (libmis_sampler.so, built from vllm_mps_amd/csrc/) replaces the
+ * per-row Python sampler of the reference engine with one batched,
+ * stream-ordered call over a [B, V] logits tensor resident in HBM.
+ *
+ * Reference interfaces replaced:
+ *   - Sampler.sample(logits[V], SamplingParams) -> int
+ *       model/sampler.py:18-60 (greedy / temperature / top-k / top-p / draw)
+ *   - Sampler.sample_batch(logits[B, V], SamplingParams) -> list[int]
+ *       model/sampler.py:62-79
+ *   - the engine's per-row dispatch loop over _seq_to_params
+ *       engine/llm_engine.py:339-345, engine/model_runner.py:124-129
+ *   - SamplingParams fields temperature / top_k / top_p
+ *       core/sequence.py:23-39 (validation :41-61 is mirrored per row as
+ *       MIS_ROW_BAD_PARAM instead of a Python ValueError)
+ *
+ * All pointers except the workspace size are device pointers.  No exceptions,
+ * no host synchronisation and no allocation happen inside mis_sample(); every
+ * launch goes on `stream` (a hipStream_t; NULL = the legacy default stream).
+ */
+#ifndef MIS_SAMPLER_H
+#define MIS_SAMPLER_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MIS_ABI_VERSION 1
+
+/* logits element type */
+enum { MIS_DTYPE_F32 = 0, MIS_DTYPE_F16 = 1, MIS_DTYPE_BF16 = 2 };
+
+/* return codes of the API */
+enum {
+    MIS_OK = 0,
+    MIS_ERR_INVALID_ARG = 1,   /* null pointer, bad dtype, B < 0, V <= 0, row_stride < V */
+    MIS_ERR_WORKSPACE = 2,     /* workspace too small or misaligned */
+    MIS_ERR_HIP = 3,           /* a HIP launch failed; see mis_last_hip_error() */
+    MIS_ERR_UNSUPPORTED = 4    /* V or B beyond the supported range */
+};
+
+/* per-row status written to out_status */
+enum {
+    MIS_ROW_OK = 0,
+    MIS_ROW_BAD_PARAM = 1,     /* temperature < 0 or NaN, top_k < 0, top_p <= 0 or NaN,
+                                  uniform NaN (core/sequence.py:41-61 raises ValueError) */
+    MIS_ROW_INVALID = 2        /* NaN or +inf scaled logits, or nothing left to sample
+                                  (torch.multinomial raises RuntimeError, model/sampler.py:59) */
+};
+
+/*
+ * Per-row parameters, 16 bytes, device array [B].
+ *   temperature  f32(T); 0 selects greedy argmax (model/sampler.py:33-34).
+ *                Logits are scaled as dtype(f32(x) / temperature), sampler.py:37.
+ *   top_k        0 = off; otherwise k' = min(top_k, V) (sampler.py:40-43).
+ *   top_p        top-p filtering applies iff top_p < 1.0f (sampler.py:46-55);
+ *                the threshold is top_p rounded to the logits dtype.
+ *   uniform      u in [0, 1) for the inverse-CDF draw that replaces
+ *                torch.multinomial (sampler.py:59).
+ */
+typedef struct mis_row_params {
+    float temperature;
+    int32_t top_k;
+    float top_p;
+    float uniform;
+} mis_row_params;
+
+/* Bytes of device workspace mis_sample() needs for this shape. */
+size_t mis_workspace_bytes(int64_t B, int64_t V, int dtype);
+
+/*
+ * One decode-step sampling pass over `B` rows of `V` logits.
+ *   logits        device, B rows, row r starts at logits + r*row_stride elements
+ *   params        device [B] mis_row_params
+ *   out_ids       device [B] int64: sampled token id, -1 when status != OK
+ *   out_status    device [B] int32 (nullable)
+ *   out_probs     device [B, V] float32 post-filter probabilities, 0 for
+ *                 removed tokens, one-hot for greedy rows (nullable; debug)
+ *   out_keep      device [B, ceil(V/32)] uint32 keep bitmask, bit j%32 of word
+ *                 j/32 = token j survives every filter (nullable; debug)
+ *   workspace     device scratch of at least mis_workspace_bytes(B, V, dtype)
+ *                 bytes, 256-byte aligned; not shared by concurrent calls
+ *   stream        hipStream_t the kernels are launched on
+ * Returns MIS_OK or an error code; launches are asynchronous.
+ */
+int mis_sample(const void *logits, int dtype, int64_t B, int64_t V, int64_t row_stride,
+               const mis_row_params *params, int64_t *out_ids, int32_t *out_status,
+               float *out_probs, uint32_t *out_keep, void *workspace, size_t workspace_bytes,
+               void *stream);
+
+/* Human-readable text for an API return code. */
+const char *mis_strerror(int code);
+
+/* hipError_t of the last failed launch in this thread (0 if none). */
+int mis_last_hip_error(void);
+
+/* MIS_ABI_VERSION of the built library. */
+int mis_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MIS_SAMPLER_H */

@@ -1,0 +1,22 @@
+// Test-only shim: exposes the host/device helpers of mis_common.h to pytest
+// through a plain C ABI so the CPU suite checks the exact code the kernels run.
+#include "../../vllm_mps_amd/csrc/mis_common.h"
+
+extern "C" {
+float shim_chain_add_n(float F, float p, uint64_t n) { return mis::chain_add_n(F, p, n); }
+float shim_chain_E(float F, float p, int dt) { return mis::chain_E(F, p, dt); }
+float shim_rn_dtype(float f, int dt) { return mis::rn_dtype(f, dt); }
+uint32_t shim_row_key(float y, int dt) { return mis::row_key(y, dt); }
+float shim_value_of_row_key(uint32_t k, int dt) { return mis::value_of_row_key(k, dt); }
+uint32_t shim_argmax_key(float x) { return mis::argmax_key(x); }
+void shim_rn_dtype_array(const float *x, float *y, int64_t n, int dt)
+{
+    for (int64_t i = 0; i < n; ++i) y[i] = mis::rn_dtype(x[i], dt);
+}
+// naive reference for chain_add_n: one float addition per step
+float shim_chain_naive(float F, float p, uint64_t n)
+{
+    for (uint64_t i = 0; i < n; ++i) F = F + p;
+    return F;
+}
+}

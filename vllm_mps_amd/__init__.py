@@ -1,0 +1,11 @@
+"""MI355X-native decode-step token sampler (drop-in for vllm_mps's Sampler).
+
+``Sampler`` and ``SamplingParams`` keep the reference's call surface
+(``model/sampler.py``, ``core/sequence.py``); the arithmetic runs in
+hand-written HIP kernels for gfx950 behind the C ABI in
+``include/mis_sampler.h``.
+"""
+from .sampling_params import SamplingParams
+from .sampler import Sampler, pack_params
+
+__all__ = ["Sampler", "SamplingParams", "pack_params"]

@@ -1,0 +1,69 @@
+"""ctypes binding of the C ABI in ``include/mis_sampler.h``.
+
+The product path has no CPU or eager fallback: if ``libmis_sampler.so`` is
+missing or does not load, every entry point raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+from . import build as _build
+
+DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
+ROW_OK, ROW_BAD_PARAM, ROW_INVALID = 0, 1, 2
+ABI_VERSION = 1
+
+EXPORTED = ("mis_workspace_bytes", "mis_sample", "mis_strerror", "mis_last_hip_error", "mis_abi_version")
+
+_lib = None
+
+
+class MisError(RuntimeError):
+    pass
+
+
+def lib_path() -> str:
+    return os.environ.get("MIS_SAMPLER_LIB", _build.LIB)
+
+
+def load():
+    """Load (once) and return the native library; raises MisError when absent."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    path = lib_path()
+    if not os.path.exists(path):
+        raise MisError(f"MI355X sampler library not built: {path} is missing "
+                       "(run `python -m vllm_mps_amd.build`); there is no CPU fallback")
+    lib = ctypes.CDLL(path)
+    i64, vp = ctypes.c_int64, ctypes.c_void_p
+    lib.mis_workspace_bytes.argtypes = [i64, i64, ctypes.c_int]
+    lib.mis_workspace_bytes.restype = ctypes.c_size_t
+    lib.mis_sample.argtypes = [vp, ctypes.c_int, i64, i64, i64, vp, vp, vp, vp, vp, vp, ctypes.c_size_t, vp]
+    lib.mis_sample.restype = ctypes.c_int
+    lib.mis_strerror.argtypes = [ctypes.c_int]
+    lib.mis_strerror.restype = ctypes.c_char_p
+    lib.mis_last_hip_error.restype = ctypes.c_int
+    lib.mis_abi_version.restype = ctypes.c_int
+    if lib.mis_abi_version() != ABI_VERSION:
+        raise MisError(f"ABI mismatch: library {lib.mis_abi_version()} != {ABI_VERSION}")
+    _lib = lib
+    return lib
+
+
+def workspace_bytes(B: int, V: int, dtype: int) -> int:
+    return int(load().mis_workspace_bytes(B, V, dtype))
+
+
+def sample(logits_ptr: int, dtype: int, B: int, V: int, row_stride: int, params_ptr: int, ids_ptr: int,
+           status_ptr: int | None, probs_ptr: int | None, keep_ptr: int | None, ws_ptr: int, ws_bytes: int,
+           stream: int) -> None:
+    lib = load()
+    rc = lib.mis_sample(logits_ptr, dtype, B, V, row_stride, params_ptr, ids_ptr, status_ptr, probs_ptr,
+                        keep_ptr, ws_ptr, ws_bytes, stream)
+    if rc != 0:
+        msg = lib.mis_strerror(rc).decode()
+        if rc == 3:
+            msg += f" (hipError {lib.mis_last_hip_error()})"
+        raise MisError(f"mis_sample failed: {msg}")

@@ -1,0 +1,166 @@
+"""Drop-in ``Sampler`` for the decode step, backed by the MI355X HIP kernels.
+
+Mirrors the reference's ``Sampler`` (``model/sampler.py:11-79``):
+
+* ``Sampler()`` -- no-argument constructor, as the engine builds it
+  (``engine/llm_engine.py:108,180``).
+* ``sample(logits[V], params) -> int`` (``model/sampler.py:18``).
+* ``sample_batch(logits[B, V], params) -> list[int]`` (``model/sampler.py:62``).
+
+and adds the batched entry point the engine's per-row loop
+(``engine/llm_engine.py:339-345``) collapses into:
+
+* ``sample_rows(logits[B, V], params_per_row, uniforms=None) -> int64[B]`` on
+  the device, one launch sequence and no host synchronisation.
+
+Differences from the reference, all contract decisions:
+* the draw is an inverse CDF in vocabulary order from one uniform per row
+  instead of ``torch.multinomial``; uniforms come from ``torch.rand`` on the
+  device (``generator`` selects the stream) unless the caller passes them;
+* top-p ties at the cut keep the lowest indices first (stable order);
+* fp32 top-p masses are exact softmax masses, not torch's float softmax.
+
+There is no CPU path: logits must live on a ROCm device and the native
+library must be built, otherwise the calls raise.
+"""
+from __future__ import annotations
+
+from typing import Sequence
+
+import numpy as np
+import torch
+
+from . import _native
+from .sampling_params import SamplingParams
+
+_DTYPES = {torch.float32: _native.DTYPE_F32, torch.float16: _native.DTYPE_F16, torch.bfloat16: _native.DTYPE_BF16}
+_ONE_BELOW = float(np.nextafter(np.float32(1.0), np.float32(0.0)))
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    if dtype not in _DTYPES:
+        raise TypeError(f"logits dtype {dtype} not supported (float32, float16, bfloat16)")
+    return _DTYPES[dtype]
+
+
+def host_row_params(params: Sequence[SamplingParams], dtype: torch.dtype) -> np.ndarray:
+    """[B, 3] (temperature f32, top_k i32, top_p f32) packed as int32 words.
+
+    Python floats become the f32 values torch would use: the temperature is
+    divided as ``f32(x) / f32(T)`` and ``top_p`` is compared after a cast to
+    the logits dtype (probed on torch 2.10).  A top_p below 1.0 whose f32
+    rounding is 1.0 stays active for 16-bit logits (threshold RN16 = 1.0)
+    and is a no-op for fp32 logits (exact masses never reach 1.0 early).
+    """
+    B = len(params)
+    out = np.zeros((B, 3), dtype=np.int32)
+    f = out.view(np.float32)
+    for i, sp in enumerate(params):
+        t = float(sp.temperature)
+        t32 = np.float32(t)
+        if t > 0.0 and t32 == 0.0:
+            t32 = np.float32(np.nan)  # divides by f32(T) = 0 in torch: invalid distribution
+        f[i, 0] = t32
+        out[i, 1] = int(min(max(int(sp.top_k), 0), 2**31 - 1)) if sp.top_k >= 0 else int(sp.top_k)
+        p = float(sp.top_p)
+        p32 = np.float32(p)
+        if p < 1.0 and p32 == np.float32(1.0) and dtype != torch.float32:
+            p32 = np.float32(_ONE_BELOW)
+        f[i, 2] = p32
+    return out
+
+
+def pack_params(temperature: torch.Tensor, top_k: torch.Tensor, top_p: torch.Tensor, uniform: torch.Tensor) -> torch.Tensor:
+    """Device [B, 4] int32 buffer laid out as ``mis_row_params``."""
+    return torch.stack([temperature.to(torch.float32).view(torch.int32), top_k.to(torch.int32),
+                        top_p.to(torch.float32).view(torch.int32), uniform.to(torch.float32).view(torch.int32)],
+                       dim=1).contiguous()
+
+
+class Sampler:
+    """Samples the next token of every row on the GPU."""
+
+    def __init__(self, generator: torch.Generator | None = None) -> None:
+        self.generator = generator
+        self._workspace: dict[int, torch.Tensor] = {}
+
+    # -- workspace -------------------------------------------------------
+    def workspace(self, device: torch.device, B: int, V: int, code: int) -> torch.Tensor:
+        need = _native.workspace_bytes(B, V, code)
+        idx = device.index if device.index is not None else torch.cuda.current_device()
+        ws = self._workspace.get(idx)
+        if ws is None or ws.numel() < need:
+            ws = torch.empty(need, dtype=torch.uint8, device=device)
+            self._workspace[idx] = ws
+        return ws
+
+    # -- batched device entry point ---------------------------------------
+    def sample_packed(self, logits: torch.Tensor, packed: torch.Tensor, *, out: torch.Tensor | None = None,
+                      status_out: torch.Tensor | None = None, probs_out: torch.Tensor | None = None,
+                      keep_out: torch.Tensor | None = None) -> torch.Tensor:
+        """One launch sequence over ``logits[B, V]`` with a device ``packed``
+        [B, 4] int32 parameter buffer (see ``pack_params``)."""
+        if logits.dim() != 2:
+            raise ValueError("logits must be [B, V]")
+        if logits.device.type != "cuda":
+            raise _native.MisError("the MI355X sampler needs logits on a ROCm device; there is no CPU path")
+        code = dtype_code(logits.dtype)
+        if logits.stride(1) != 1:
+            logits = logits.contiguous()
+        B, V = logits.shape
+        dev = logits.device
+        if out is None:
+            out = torch.empty(B, dtype=torch.int64, device=dev)
+        for t, dt, shape in ((packed, torch.int32, (B, 4)), (out, torch.int64, (B,)),
+                             (status_out, torch.int32, (B,)), (probs_out, torch.float32, (B, V)),
+                             (keep_out, torch.int32, (B, (V + 31) // 32))):
+            if t is not None and (t.dtype != dt or tuple(t.shape) != shape or not t.is_contiguous() or t.device != dev):
+                raise ValueError(f"buffer must be a contiguous {dt} {shape} tensor on {dev}")
+        ws = self.workspace(dev, B, V, code)
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        ptr = lambda t: None if t is None else t.data_ptr()
+        _native.sample(logits.data_ptr(), code, B, V, logits.stride(0), packed.data_ptr(), out.data_ptr(),
+                       ptr(status_out), ptr(probs_out), ptr(keep_out), ws.data_ptr(), ws.numel(), stream)
+        return out
+
+    def sample_rows(self, logits: torch.Tensor, params: Sequence[SamplingParams],
+                    uniforms: torch.Tensor | None = None, **buffers) -> torch.Tensor:
+        """Per-row params, device int64[B] token ids (-1 where a row is invalid)."""
+        B = logits.shape[0]
+        if len(params) != B:
+            raise ValueError(f"{len(params)} SamplingParams for {B} rows")
+        dev = logits.device
+        if dev.type != "cuda":
+            raise _native.MisError("the MI355X sampler needs logits on a ROCm device; there is no CPU path")
+        host = torch.from_numpy(host_row_params(params, logits.dtype))
+        if uniforms is None:
+            uniforms = torch.rand(B, device=dev, dtype=torch.float32, generator=self.generator)
+        packed = torch.empty((B, 4), dtype=torch.int32, device=dev)
+        packed[:, :3].copy_(host, non_blocking=False)
+        packed[:, 3].copy_(uniforms.to(device=dev, dtype=torch.float32).view(torch.int32))
+        return self.sample_packed(logits, packed, **buffers)
+
+    # -- reference call surface -------------------------------------------
+    def _checked(self, ids: torch.Tensor, status: torch.Tensor) -> list[int]:
+        st = status.tolist()
+        for s in st:
+            if s == _native.ROW_BAD_PARAM:
+                raise ValueError("invalid sampling parameters")
+            if s == _native.ROW_INVALID:
+                raise RuntimeError("invalid probability distribution (NaN/inf logits or nothing left to sample)")
+        return ids.tolist()
+
+    def sample(self, logits: torch.Tensor, sampling_params: SamplingParams) -> int:
+        """Sample one token from ``logits[V]`` (model/sampler.py:18)."""
+        if logits.dim() != 1:
+            raise ValueError("logits must be [V]")
+        status = torch.empty(1, dtype=torch.int32, device=logits.device)
+        ids = self.sample_rows(logits.unsqueeze(0), [sampling_params], status_out=status)
+        return self._checked(ids, status)[0]
+
+    def sample_batch(self, logits_batch: torch.Tensor, sampling_params: SamplingParams) -> list[int]:
+        """One token per row with shared params (model/sampler.py:62)."""
+        B = logits_batch.shape[0]
+        status = torch.empty(B, dtype=torch.int32, device=logits_batch.device)
+        ids = self.sample_rows(logits_batch, [sampling_params] * B, status_out=status)
+        return self._checked(ids, status)
