@@ -940,8 +940,10 @@ __global__ __launch_bounds__(K2_THREADS) void k_final(const char *__restrict__ l
         if (ovf == 0) {
             const Cand *cand = reinterpret_cast<const Cand *>(ws + L.cand) + (size_t)row * L.G * CAND_CAP;
             // k'-th largest key among the candidates
+            // fewer than k' candidates means fewer than k' finite elements in
+            // the row: every finite element survives
             uint32_t thr = kneg + 1u;
-            if (ncand_tot > (uint32_t)pl.kk) {
+            if (ncand_tot >= (uint32_t)pl.kk) {
                 uint32_t prefix = 0u, rem = (uint32_t)pl.kk;
                 const int nlev = DT == F32 ? 4 : 2;
                 for (int lev = 0; lev < nlev; ++lev) {
@@ -964,9 +966,9 @@ __global__ __launch_bounds__(K2_THREADS) void k_final(const char *__restrict__ l
                     __syncthreads();
                     rem -= sh.bu[1];
                     prefix |= sh.bu[0] << shift;
-                    const uint32_t incnt = sh.bu[2];
                     __syncthreads();
-                    if (incnt == rem) break;
+                    // no early exit here: the threshold is applied to the whole
+                    // row, so it must be the exact k'-th key
                 }
                 thr = prefix;
             }
