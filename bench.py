@@ -1,0 +1,193 @@
+#!/usr/bin/env python3
+"""Decode-step sampler benchmark on one MI355X.
+
+Workload (default): config C3 -- fp32 logits [256, 128256], per-row
+temperature / top-k / top-p mix, one uniform per row (the headline
+configuration the metric is quoted on).  A "step" is one mis_sample() call
+over the whole batch: the chunk pass plus the per-row finalize; the sampled
+ids stay on the device.
+
+Inputs are resident in HBM before timing starts.  The batch (131 MB) fits
+the 256 MB Infinity Cache, so the timed loop rotates through >= 1 GiB of
+distinct copies of it.  Timing uses HIP events on the launch stream:
+* whole region: barrier + synchronize, start event, K steps, end event;
+* per kernel: mis_sample_profiled() records events around the chunk pass and
+  the finalize of every step, giving each kernel's mean duration for the
+  roofline entry.
+
+The CPU baseline is the literal reference algorithm re-stated with torch CPU
+ops (oracle/faithful.py: one call per row, unstable sort, torch.multinomial),
+timed on a bounded sample of the same rows, on this host's cores.
+
+Prints one JSON line.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "rows/sec + HBM GB/s (% of peak), B=256 V=128256 top-k/top-p; p50 µs/step"
+WORKLOAD_DESC = {
+    "C1": "C1 greedy fp32 [8, 32000]",
+    "C2": "C2 stochastic fp16 [8, 32000] T=0.8 k=50 p=0.9",
+    "C3": "C3 mixed fp32 [256, 128256] top-k {0,20,1000} / top-p {1,0.95,0.5}, T~U[0.5,1.5]",
+    "C4": "C4 single-stream bf16 [1, 152064] top-p 0.95",
+    "C5": "C5 edge-stress bf16 [1024, 128256]",
+}
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--config", default="C3", choices=sorted(WORKLOAD_DESC))
+    ap.add_argument("--rotate-gib", type=float, default=1.0, help="distinct input bytes cycled through")
+    ap.add_argument("--cpu-rows", type=int, default=32, help="rows in the CPU-baseline sample (0 = skip)")
+    ap.add_argument("--cpu-steps", type=int, default=5)
+    return ap.parse_args()
+
+
+def cpu_baseline(w, nrows: int, steps: int) -> dict:
+    """Literal reference sampler on the host cores, p50 over `steps` after 2 warmups."""
+    import numpy as np
+    import torch
+    from oracle import faithful
+
+    ncores = len(os.sched_getaffinity(0))
+    share = int(os.environ.get("OMP_NUM_THREADS", ncores) or ncores)
+    torch.set_num_threads(max(1, min(ncores, share)))
+    B = w.shape[0]
+    sel = np.linspace(0, B - 1, min(nrows, B)).round().astype(int)
+    sub = w.rows(sel)
+    x = sub.to_torch("cpu")
+    params = [(float(sub.temperature[i]), int(sub.top_k[i]), float(sub.top_p[i])) for i in range(len(sel))]
+    times = []
+    torch.manual_seed(0)
+    for it in range(2 + steps):
+        t0 = time.perf_counter()
+        faithful.sample_batch(x, params, literal=True)
+        dt = time.perf_counter() - t0
+        if it >= 2:
+            times.append(dt)
+    p50 = statistics.median(times)
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"value": round(len(sel) / p50, 2), "unit": "rows/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": (f"{len(sel)} of {B} {w.name} rows (evenly spaced), literal reference algorithm "
+                       f"(oracle/faithful.py) one call per row as engine/llm_engine.py:341-344, "
+                       f"p50 of {steps} steps after 2 warmups, torch CPU"),
+            "p50_ms_per_sample_step": round(p50 * 1e3, 3), "cpu_model": model}
+
+
+def main():
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE={world}); "
+              "rows are independent, so N GPUs would each run this single-GPU step on B/N rows.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from vllm_mps_amd import workloads as W
+    from vllm_mps_amd.sampler import Sampler, pack_params
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    w = W.make(args.config)
+    B, V = w.shape
+    esz = 4 if w.dtype == "f32" else 2
+    bytes_alg = W.algorithmic_bytes(B, V, w.dtype)
+    bytes_k1 = B * V * esz + 16 * B  # logits + params read by the chunk pass
+    nbuf = max(1, math.ceil(args.rotate_gib * (1 << 30) / (B * V * esz)))
+    base = w.to_torch(dev)
+    bufs = [base.clone() for _ in range(nbuf)]
+    del base
+    packed = pack_params(torch.from_numpy(w.temperature.copy()).to(dev), torch.from_numpy(w.top_k.copy()).to(dev),
+                         torch.from_numpy(w.top_p.copy()).to(dev), torch.from_numpy(w.uniform.copy()).to(dev))
+    out = torch.empty(B, dtype=torch.int64, device=dev)
+    s = Sampler()
+    for i in range(args.warmup):
+        s.sample_packed(bufs[i % nbuf], packed, out=out)
+    torch.cuda.synchronize()
+
+    K = args.steps
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(K)]
+    for trio in evs:
+        for e in trio:
+            e.record()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for i in range(K):
+        s.sample_packed(bufs[(args.warmup + i) % nbuf], packed, out=out, events=evs[i])
+    end.record()
+    torch.cuda.synchronize()
+    total_ms = start.elapsed_time(end)
+    step_us = [t[0].elapsed_time(t[2]) * 1e3 for t in evs]
+    k1_us = [t[0].elapsed_time(t[1]) * 1e3 for t in evs]
+    k2_us = [t[1].elapsed_time(t[2]) * 1e3 for t in evs]
+    ms_per_step = total_ms / K
+    rows_per_s = B * K / (total_ms / 1e3)
+    gbs_step = bytes_alg / (ms_per_step / 1e3) / 1e9
+    k1_mean, k2_mean = statistics.mean(k1_us), statistics.mean(k2_us)
+    q = statistics.quantiles(step_us, n=10)
+    if k1_mean >= k2_mean:
+        dom, dom_us, dom_bytes = "k_chunk", k1_mean, bytes_k1
+    else:
+        dom, dom_us, dom_bytes = "k_final", k2_mean, bytes_alg - bytes_k1
+    achieved = dom_bytes / (dom_us / 1e6) / 1e9
+    res = {
+        "metric": METRIC,
+        "value": round(rows_per_s, 1),
+        "unit": "rows/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": w.dtype,
+        "data": "synthetic",
+        "config": {"workload": WORKLOAD_DESC[args.config], "B": B, "V": V, "seed": W.SEEDS[args.config],
+                   "rotating_buffers": nbuf, "rotated_bytes": nbuf * B * V * esz},
+        "tokens_per_s": round(rows_per_s, 1),
+        "p50_us_per_step": round(statistics.median(step_us), 2),
+        "p90_us_per_step": round(q[8], 2),
+        "hbm_gbs_step": round(gbs_step, 1),
+        "hbm_frac_step": round(gbs_step / HBM_PEAK_GBS, 4),
+        "algorithmic_bytes_per_step": bytes_alg,
+        "kernels_us": {"k_chunk": round(k1_mean, 2), "k_final": round(k2_mean, 2)},
+        "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "algorithmic_bytes_per_launch": dom_bytes, "mean_launch_us": round(dom_us, 2)},
+    }
+    if args.cpu_rows > 0:
+        res["cpu_baseline"] = cpu_baseline(w, args.cpu_rows, args.cpu_steps)
+    else:
+        res["cpu_baseline"] = None
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -93,6 +93,18 @@ int mis_sample(const void *logits, int dtype, int64_t B, int64_t V, int64_t row_
                float *out_probs, uint32_t *out_keep, void *workspace, size_t workspace_bytes,
                void *stream);
 
+/*
+ * Instrumented mis_sample(): identical results, and additionally records the
+ * caller's hipEvent_t handles events[0] before the chunk pass, events[1]
+ * between the chunk pass and the finalize, events[2] after the finalize, all
+ * on `stream`.  No counterpart in the reference: it exists so benchmarks can
+ * time each kernel on the stream it runs on.
+ */
+int mis_sample_profiled(const void *logits, int dtype, int64_t B, int64_t V, int64_t row_stride,
+                        const mis_row_params *params, int64_t *out_ids, int32_t *out_status,
+                        float *out_probs, uint32_t *out_keep, void *workspace, size_t workspace_bytes,
+                        void *stream, void *const *events);
+
 /* Human-readable text for an API return code. */
 const char *mis_strerror(int code);
 

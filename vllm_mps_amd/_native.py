@@ -14,7 +14,8 @@ DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
 ROW_OK, ROW_BAD_PARAM, ROW_INVALID = 0, 1, 2
 ABI_VERSION = 1
 
-EXPORTED = ("mis_workspace_bytes", "mis_sample", "mis_strerror", "mis_last_hip_error", "mis_abi_version")
+EXPORTED = ("mis_workspace_bytes", "mis_sample", "mis_sample_profiled", "mis_strerror", "mis_last_hip_error",
+            "mis_abi_version")
 
 _lib = None
 
@@ -42,6 +43,9 @@ def load():
     lib.mis_workspace_bytes.restype = ctypes.c_size_t
     lib.mis_sample.argtypes = [vp, ctypes.c_int, i64, i64, i64, vp, vp, vp, vp, vp, vp, ctypes.c_size_t, vp]
     lib.mis_sample.restype = ctypes.c_int
+    lib.mis_sample_profiled.argtypes = [vp, ctypes.c_int, i64, i64, i64, vp, vp, vp, vp, vp, vp, ctypes.c_size_t, vp,
+                                        ctypes.POINTER(vp)]
+    lib.mis_sample_profiled.restype = ctypes.c_int
     lib.mis_strerror.argtypes = [ctypes.c_int]
     lib.mis_strerror.restype = ctypes.c_char_p
     lib.mis_last_hip_error.restype = ctypes.c_int
@@ -58,10 +62,15 @@ def workspace_bytes(B: int, V: int, dtype: int) -> int:
 
 def sample(logits_ptr: int, dtype: int, B: int, V: int, row_stride: int, params_ptr: int, ids_ptr: int,
            status_ptr: int | None, probs_ptr: int | None, keep_ptr: int | None, ws_ptr: int, ws_bytes: int,
-           stream: int) -> None:
+           stream: int, events: tuple[int, int, int] | None = None) -> None:
     lib = load()
-    rc = lib.mis_sample(logits_ptr, dtype, B, V, row_stride, params_ptr, ids_ptr, status_ptr, probs_ptr,
-                        keep_ptr, ws_ptr, ws_bytes, stream)
+    if events is None:
+        rc = lib.mis_sample(logits_ptr, dtype, B, V, row_stride, params_ptr, ids_ptr, status_ptr, probs_ptr,
+                            keep_ptr, ws_ptr, ws_bytes, stream)
+    else:
+        ev = (ctypes.c_void_p * 3)(*events)
+        rc = lib.mis_sample_profiled(logits_ptr, dtype, B, V, row_stride, params_ptr, ids_ptr, status_ptr,
+                                     probs_ptr, keep_ptr, ws_ptr, ws_bytes, stream, ev)
     if rc != 0:
         msg = lib.mis_strerror(rc).decode()
         if rc == 3:

@@ -1391,28 +1391,34 @@ static thread_local int g_last_hip = 0;
 template <int DT, int EPT>
 static hipError_t launch_main(const void *logits, int64_t B, int64_t V, int64_t stride_bytes, int vec_ok,
                               const mis_row_params *params, int64_t *ids, int32_t *status, const Layout &L,
-                              char *ws, hipStream_t st)
+                              char *ws, hipStream_t st, void *const *events)
 {
+    hipError_t e;
+    if (events && (e = hipEventRecord((hipEvent_t)events[0], st)) != hipSuccess) return e;
     hipLaunchKernelGGL((k_chunk<DT, EPT>), dim3(L.G, (unsigned)B), dim3(K1_THREADS), 0, st,
                        (const char *)logits, V, stride_bytes, vec_ok, params, L, ws);
-    hipError_t e = hipGetLastError();
+    e = hipGetLastError();
     if (e != hipSuccess) return e;
+    if (events && (e = hipEventRecord((hipEvent_t)events[1], st)) != hipSuccess) return e;
     hipLaunchKernelGGL((k_final<DT>), dim3((unsigned)B), dim3(K2_THREADS), 0, st,
                        (const char *)logits, V, stride_bytes, vec_ok, params, L, ws, ids, status);
-    return hipGetLastError();
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    if (events) e = hipEventRecord((hipEvent_t)events[2], st);
+    return e;
 }
 
 template <int DT>
 static hipError_t launch_dt(const void *logits, int64_t B, int64_t V, int64_t stride_bytes, int vec_ok,
                             const mis_row_params *params, int64_t *ids, int32_t *status, float *probs,
-                            uint32_t *keep, const Layout &L, char *ws, hipStream_t st)
+                            uint32_t *keep, const Layout &L, char *ws, hipStream_t st, void *const *ev)
 {
     hipError_t e;
     switch (L.ept) {
-    case 64: e = launch_main<DT, 64>(logits, B, V, stride_bytes, vec_ok, params, ids, status, L, ws, st); break;
-    case 32: e = launch_main<DT, 32>(logits, B, V, stride_bytes, vec_ok, params, ids, status, L, ws, st); break;
-    case 16: e = launch_main<DT, 16>(logits, B, V, stride_bytes, vec_ok, params, ids, status, L, ws, st); break;
-    default: e = launch_main<DT, 8>(logits, B, V, stride_bytes, vec_ok, params, ids, status, L, ws, st); break;
+    case 64: e = launch_main<DT, 64>(logits, B, V, stride_bytes, vec_ok, params, ids, status, L, ws, st, ev); break;
+    case 32: e = launch_main<DT, 32>(logits, B, V, stride_bytes, vec_ok, params, ids, status, L, ws, st, ev); break;
+    case 16: e = launch_main<DT, 16>(logits, B, V, stride_bytes, vec_ok, params, ids, status, L, ws, st, ev); break;
+    default: e = launch_main<DT, 8>(logits, B, V, stride_bytes, vec_ok, params, ids, status, L, ws, st, ev); break;
     }
     if (e != hipSuccess) return e;
     if (probs || keep) {
@@ -1435,9 +1441,10 @@ size_t mis_workspace_bytes(int64_t B, int64_t V, int dtype)
     return mis::make_layout(B, V).total;
 }
 
-int mis_sample(const void *logits, int dtype, int64_t B, int64_t V, int64_t row_stride,
-               const mis_row_params *params, int64_t *out_ids, int32_t *out_status, float *out_probs,
-               uint32_t *out_keep, void *workspace, size_t workspace_bytes, void *stream)
+static int sample_impl(const void *logits, int dtype, int64_t B, int64_t V, int64_t row_stride,
+                       const mis_row_params *params, int64_t *out_ids, int32_t *out_status, float *out_probs,
+                       uint32_t *out_keep, void *workspace, size_t workspace_bytes, void *stream,
+                       void *const *events)
 {
     using namespace mis;
     if (dtype < 0 || dtype > 2 || B < 0 || V <= 0 || row_stride < V) return MIS_ERR_INVALID_ARG;
@@ -1454,13 +1461,31 @@ int mis_sample(const void *logits, int dtype, int64_t B, int64_t V, int64_t row_
     char *ws = (char *)workspace;
     hipError_t e;
     if (dtype == MIS_DTYPE_F32)
-        e = launch_dt<F32>(logits, B, V, stride_bytes, vec_ok, params, out_ids, out_status, out_probs, out_keep, L, ws, st);
+        e = launch_dt<F32>(logits, B, V, stride_bytes, vec_ok, params, out_ids, out_status, out_probs, out_keep, L, ws, st, events);
     else if (dtype == MIS_DTYPE_F16)
-        e = launch_dt<F16>(logits, B, V, stride_bytes, vec_ok, params, out_ids, out_status, out_probs, out_keep, L, ws, st);
+        e = launch_dt<F16>(logits, B, V, stride_bytes, vec_ok, params, out_ids, out_status, out_probs, out_keep, L, ws, st, events);
     else
-        e = launch_dt<BF16>(logits, B, V, stride_bytes, vec_ok, params, out_ids, out_status, out_probs, out_keep, L, ws, st);
+        e = launch_dt<BF16>(logits, B, V, stride_bytes, vec_ok, params, out_ids, out_status, out_probs, out_keep, L, ws, st, events);
     if (e != hipSuccess) { g_last_hip = (int)e; return MIS_ERR_HIP; }
     return MIS_OK;
+}
+
+int mis_sample(const void *logits, int dtype, int64_t B, int64_t V, int64_t row_stride,
+               const mis_row_params *params, int64_t *out_ids, int32_t *out_status, float *out_probs,
+               uint32_t *out_keep, void *workspace, size_t workspace_bytes, void *stream)
+{
+    return sample_impl(logits, dtype, B, V, row_stride, params, out_ids, out_status, out_probs, out_keep,
+                       workspace, workspace_bytes, stream, nullptr);
+}
+
+int mis_sample_profiled(const void *logits, int dtype, int64_t B, int64_t V, int64_t row_stride,
+                        const mis_row_params *params, int64_t *out_ids, int32_t *out_status, float *out_probs,
+                        uint32_t *out_keep, void *workspace, size_t workspace_bytes, void *stream,
+                        void *const *events)
+{
+    if (!events || !events[0] || !events[1] || !events[2]) return MIS_ERR_INVALID_ARG;
+    return sample_impl(logits, dtype, B, V, row_stride, params, out_ids, out_status, out_probs, out_keep,
+                       workspace, workspace_bytes, stream, events);
 }
 
 const char *mis_strerror(int code)

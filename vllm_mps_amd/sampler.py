@@ -97,9 +97,11 @@ class Sampler:
     # -- batched device entry point ---------------------------------------
     def sample_packed(self, logits: torch.Tensor, packed: torch.Tensor, *, out: torch.Tensor | None = None,
                       status_out: torch.Tensor | None = None, probs_out: torch.Tensor | None = None,
-                      keep_out: torch.Tensor | None = None) -> torch.Tensor:
+                      keep_out: torch.Tensor | None = None, events=None) -> torch.Tensor:
         """One launch sequence over ``logits[B, V]`` with a device ``packed``
-        [B, 4] int32 parameter buffer (see ``pack_params``)."""
+        [B, 4] int32 parameter buffer (see ``pack_params``).  ``events``: three
+        recorded ``torch.cuda.Event`` objects to time the chunk pass and the
+        finalize (see ``mis_sample_profiled``)."""
         if logits.dim() != 2:
             raise ValueError("logits must be [B, V]")
         if logits.device.type != "cuda":
@@ -119,8 +121,9 @@ class Sampler:
         ws = self.workspace(dev, B, V, code)
         stream = torch.cuda.current_stream(dev).cuda_stream
         ptr = lambda t: None if t is None else t.data_ptr()
+        evs = None if events is None else tuple(int(e.cuda_event) for e in events)
         _native.sample(logits.data_ptr(), code, B, V, logits.stride(0), packed.data_ptr(), out.data_ptr(),
-                       ptr(status_out), ptr(probs_out), ptr(keep_out), ws.data_ptr(), ws.numel(), stream)
+                       ptr(status_out), ptr(probs_out), ptr(keep_out), ws.data_ptr(), ws.numel(), stream, evs)
         return out
 
     def sample_rows(self, logits: torch.Tensor, params: Sequence[SamplingParams],
