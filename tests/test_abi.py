@@ -1,0 +1,95 @@
+"""The C ABI library: builds, loads without a GPU, exports every declared symbol,
+and rejects bad arguments before touching the device."""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+import subprocess
+import sys
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "mis_sampler.h")
+
+
+def declared_functions() -> list[str]:
+    src = open(HEADER).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return re.findall(r"\b(mis_\w+)\s*\(", src)
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from vllm_mps_amd import _native
+    if not os.path.exists(_native.lib_path()):
+        pytest.fail("libmis_sampler.so not built (run __graft_entry__.build())")
+    return _native.load()
+
+
+def test_header_declares_expected_api():
+    names = declared_functions()
+    for n in ["mis_workspace_bytes", "mis_sample", "mis_sample_profiled", "mis_strerror", "mis_last_hip_error",
+              "mis_abi_version"]:
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol(lib):
+    from vllm_mps_amd import _native
+    out = subprocess.run(["nm", "-D", "--defined-only", _native.lib_path()], capture_output=True, text=True).stdout
+    exported = set(re.findall(r" T (mis_\w+)", out))
+    for n in declared_functions():
+        assert n in exported, n
+        assert hasattr(lib, n)
+    assert set(_native.EXPORTED) == set(declared_functions())
+
+
+def test_abi_version_and_strings(lib):
+    assert lib.mis_abi_version() == 1
+    assert lib.mis_strerror(0) == b"ok"
+    assert b"workspace" in lib.mis_strerror(2)
+    assert lib.mis_last_hip_error() == 0
+
+
+def test_workspace_bytes(lib):
+    for B, V in [(1, 1), (8, 32000), (256, 128256), (1024, 128256), (1, 152064)]:
+        n = lib.mis_workspace_bytes(B, V, 0)
+        assert n > 0 and n % 256 == 0
+    assert lib.mis_workspace_bytes(256, 128256, 0) < 256 << 20
+
+
+def test_argument_validation_without_gpu(lib):
+    vp = ctypes.c_void_p
+    fake = vp(0x1000)
+    call = lambda *a: lib.mis_sample(*a)
+    # bad dtype / shape / stride are rejected before any launch
+    assert call(fake, 7, 1, 10, 10, fake, fake, None, None, None, fake, 1 << 20, None) == 1
+    assert call(fake, 0, -1, 10, 10, fake, fake, None, None, None, fake, 1 << 20, None) == 1
+    assert call(fake, 0, 1, 0, 10, fake, fake, None, None, None, fake, 1 << 20, None) == 1
+    assert call(fake, 0, 1, 10, 9, fake, fake, None, None, None, fake, 1 << 20, None) == 1
+    assert call(None, 0, 1, 10, 10, fake, fake, None, None, None, fake, 1 << 20, None) == 1
+    assert call(fake, 0, 0, 10, 10, fake, fake, None, None, None, fake, 1 << 20, None) == 0  # empty batch
+    # workspace too small / misaligned
+    assert call(fake, 0, 4, 1000, 1000, fake, fake, None, None, None, fake, 16, None) == 2
+    assert call(fake, 0, 4, 1000, 1000, fake, fake, None, None, None, vp(0x1008), 1 << 30, None) == 2
+    # unsupported sizes
+    assert call(fake, 0, 70000, 10, 10, fake, fake, None, None, None, fake, 1 << 40, None) == 4
+    # profiled entry needs three events
+    ev = (vp * 3)(None, None, None)
+    assert lib.mis_sample_profiled(fake, 0, 1, 10, 10, fake, fake, None, None, None, fake, 1 << 20, None, ev) == 1
+
+
+def test_product_path_fails_loudly_without_library(tmp_path):
+    code = ("import os; os.environ['MIS_SAMPLER_LIB']='/nonexistent/lib.so';"
+            "from vllm_mps_amd import _native\n"
+            "try:\n    _native.load()\nexcept _native.MisError as e:\n    print('raised', e)\n")
+    out = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, cwd=ROOT)
+    assert "raised" in out.stdout and "no CPU fallback" in out.stdout
+
+
+def test_sampler_rejects_cpu_tensors():
+    import torch
+    from vllm_mps_amd import Sampler, SamplingParams, _native
+    with pytest.raises(_native.MisError):
+        Sampler().sample(torch.zeros(10), SamplingParams())

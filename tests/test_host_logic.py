@@ -1,0 +1,125 @@
+"""Host-compiled checks of the helpers the kernels share (vllm_mps_amd/csrc/mis_common.h).
+
+tests/csrc/host_shim.cpp exposes them through a C ABI; g++ builds it here so
+the CPU suite exercises the same source the gfx950 kernels compile.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+import pytest
+import torch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+F32, F16, BF16 = 0, 1, 2
+
+
+@pytest.fixture(scope="module")
+def shim(tmp_path_factory):
+    out = str(tmp_path_factory.mktemp("shim") / "host_shim.so")
+    subprocess.run(["g++", "-O2", "-fPIC", "-shared", "-ffp-contract=off", "-o", out,
+                    os.path.join(HERE, "csrc", "host_shim.cpp")], check=True)
+    L = ctypes.CDLL(out)
+    f, u64, i = ctypes.c_float, ctypes.c_uint64, ctypes.c_int
+    L.shim_chain_add_n.argtypes = [f, f, u64]; L.shim_chain_add_n.restype = f
+    L.shim_chain_naive.argtypes = [f, f, u64]; L.shim_chain_naive.restype = f
+    L.shim_chain_E.argtypes = [f, f, i]; L.shim_chain_E.restype = f
+    L.shim_rn_dtype.argtypes = [f, i]; L.shim_rn_dtype.restype = f
+    L.shim_row_key.argtypes = [f, i]; L.shim_row_key.restype = ctypes.c_uint32
+    L.shim_value_of_row_key.argtypes = [ctypes.c_uint32, i]; L.shim_value_of_row_key.restype = f
+    L.shim_argmax_key.argtypes = [f]; L.shim_argmax_key.restype = ctypes.c_uint32
+    L.shim_rn_dtype_array.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, i]
+    return L
+
+
+def bits(x) -> int:
+    return int(np.float32(x).view(np.uint32))
+
+
+def test_chain_add_n_matches_sequential_float(shim):
+    """Closed-form run addition == one IEEE float addition per element,
+    including ties to even and binade crossings."""
+    rng = np.random.default_rng(0)
+    for it in range(20000):
+        F = 0.0 if rng.random() < 0.1 else float(np.float32(2.0 ** rng.uniform(-30, 1)))
+        mode = it % 4
+        if mode == 0:
+            p = float(np.float32(2.0 ** rng.uniform(-40, 0)))
+        elif mode == 1:  # bf16-representable p
+            p = float(np.array([np.float32(2.0 ** rng.uniform(-30, -1)).view(np.uint32) & 0xFFFF0000],
+                               np.uint32).view(np.float32)[0])
+        elif mode == 2:  # exact half-ulp ties relative to F
+            if F == 0:
+                F = float(np.float32(2.0 ** rng.uniform(-10, 0)))
+            e = np.frexp(np.float32(F))[1] - 1
+            p = float(np.float32(2.0 ** (e - 23) * (rng.integers(0, 6) + 0.5)))
+        else:
+            p = float(np.float32(F * rng.uniform(0, 3))) if F > 0 else float(np.float32(2.0 ** rng.uniform(-20, 0)))
+        n = int(rng.integers(1, 2000))
+        a, b = shim.shim_chain_add_n(F, p, n), shim.shim_chain_naive(F, p, n)
+        assert bits(a) == bits(b), (F, p, n, a, b)
+
+
+def test_chain_add_n_subnormal_and_large_n(shim):
+    tiny = float(np.float32(1e-44))
+    assert bits(shim.shim_chain_add_n(0.0, tiny, 1000)) == bits(shim.shim_chain_naive(0.0, tiny, 1000))
+    for p in [1e-8, 3e-8, 6e-8, 1.2e-7]:
+        a = shim.shim_chain_add_n(0.5, p, 200000)
+        b = shim.shim_chain_naive(0.5, p, 200000)
+        assert bits(a) == bits(b), p
+
+
+@pytest.mark.parametrize("dt,name", [(F16, "f16"), (BF16, "bf16")])
+def test_rn_dtype_matches_reference_conversions(shim, dt, name):
+    rng = np.random.default_rng(1)
+    x = np.concatenate([rng.normal(0, 1, 50000), rng.normal(0, 1e-5, 20000), 2.0 ** rng.uniform(-40, 20, 20000),
+                        [0.0, -0.0, np.inf, -np.inf, 65504.0, 65520.0, 6e-8, 3e-8]]).astype(np.float32)
+    y = np.empty_like(x)
+    shim.shim_rn_dtype_array(x.ctypes.data, y.ctypes.data, x.size, dt)
+    ref = x.astype(np.float16).astype(np.float32) if name == "f16" else \
+        torch.from_numpy(x).to(torch.bfloat16).float().numpy()
+    with np.errstate(invalid="ignore"):
+        assert np.array_equal(y.view(np.uint32), ref.view(np.uint32))
+
+
+def test_chain_E_is_torch_subtraction(shim):
+    rng = np.random.default_rng(2)
+    for dt, tdt in [(F16, torch.float16), (BF16, torch.bfloat16)]:
+        C = torch.from_numpy(rng.uniform(0, 1, 5000).astype(np.float32)).to(tdt)
+        p = torch.from_numpy((rng.uniform(0, 1, 5000) ** 4).astype(np.float32)).to(tdt)
+        E = (C - p).float().numpy()
+        for i in range(0, 5000, 7):
+            # chain_E(F, p) rounds F to the dtype first; pass an F that already is C
+            got = shim.shim_chain_E(float(C[i].float()), float(p[i].float()), dt)
+            assert bits(got) == bits(E[i])
+
+
+@pytest.mark.parametrize("dt", [F32, F16, BF16])
+def test_row_key_orders_like_values(shim, dt):
+    rng = np.random.default_rng(3)
+    x = np.concatenate([rng.normal(0, 10, 3000), [0.0, -0.0, np.inf, -np.inf, 1e-30, -1e-30]]).astype(np.float32)
+    if dt != F32:
+        y = np.empty_like(x)
+        shim.shim_rn_dtype_array(x.ctypes.data, y.ctypes.data, x.size, dt)
+        x = y
+    keys = np.array([shim.shim_row_key(float(v), dt) for v in x], np.uint64)
+    order_k = np.argsort(keys, kind="stable")
+    assert np.all(np.diff(x[order_k]) >= 0)
+    # equal values <=> equal keys (+0 and -0 included)
+    eq_v = x[:, None] == x[None, :]
+    eq_k = keys[:, None] == keys[None, :]
+    sub = slice(0, 400)
+    assert np.array_equal(eq_v[sub, sub], eq_k[sub, sub])
+    back = np.array([shim.shim_value_of_row_key(int(k), dt) for k in keys], np.float32)
+    assert np.array_equal(back, x)  # -0.0 == 0.0 compares equal
+    if dt != F32:
+        assert np.all(keys & 0xFFFF == 0)
+
+
+def test_argmax_key_nan_first(shim):
+    assert shim.shim_argmax_key(float("nan")) == 0xFFFFFFFF
+    assert shim.shim_argmax_key(float("inf")) < 0xFFFFFFFF
+    assert shim.shim_argmax_key(1.0) > shim.shim_argmax_key(-1.0)

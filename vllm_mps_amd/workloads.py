@@ -212,6 +212,12 @@ def make_c5(rows: int | None = None) -> Workload:
     return w if rows is None else w.rows(slice(0, rows))
 
 
+def c5_row_classes() -> np.ndarray:
+    """Index into C5_CLASSES of every C5 row (same draws as make_c5)."""
+    rng = np.random.default_rng(SEEDS["C5"])
+    return rng.integers(0, len(C5_CLASSES), SHAPES["C5"][0])
+
+
 def c5_duplicate_rows() -> list[int]:
     """Rows of C5 holding an exact duplicate maximum (same draws as make_c5)."""
     B = SHAPES["C5"][0]
