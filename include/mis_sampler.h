@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define MIS_ABI_VERSION 1
+#define MIS_ABI_VERSION 2
 
 /* logits element type */
 enum { MIS_DTYPE_F32 = 0, MIS_DTYPE_F16 = 1, MIS_DTYPE_BF16 = 2 };
@@ -49,8 +49,13 @@ enum {
     MIS_ROW_OK = 0,
     MIS_ROW_BAD_PARAM = 1,     /* temperature < 0 or NaN, top_k < 0, top_p <= 0 or NaN,
                                   uniform NaN (core/sequence.py:41-61 raises ValueError) */
-    MIS_ROW_INVALID = 2        /* NaN or +inf scaled logits, or nothing left to sample
+    MIS_ROW_INVALID = 2,       /* NaN or +inf scaled logits, or nothing left to sample
                                   (torch.multinomial raises RuntimeError, model/sampler.py:59) */
+    MIS_ROW_UNSUPPORTED = 3,   /* fp16/bf16 logits with a top-k threshold that needs the
+                                  full-row radix descent (1024 < k' < V, or more than 2048
+                                  candidates tied at one chunk's k'-th value): not served
+                                  by this build */
+    MIS_ROW_INTERNAL = 4       /* a bounded cross-workgroup wait expired (not expected) */
 };
 
 /*
@@ -74,6 +79,18 @@ typedef struct mis_row_params {
 size_t mis_workspace_bytes(int64_t B, int64_t V, int dtype);
 
 /*
+ * Prepares a freshly allocated workspace: clears the control words at its
+ * start (hipMemsetAsync on `stream`; not for use under graph capture).  Call
+ * once per workspace before its first mis_sample(); every completed
+ * mis_sample() leaves those words cleared again, for a call of any shape.
+ * A workspace whose first bytes were zeroed by other means is equally ready.
+ * After a call that failed on the device, initialise the workspace again.
+ * No counterpart in the reference (its sampler keeps no device state; this
+ * library's single-launch design keeps per-row arrival counters there).
+ */
+int mis_workspace_init(void *workspace, size_t workspace_bytes, void *stream);
+
+/*
  * One decode-step sampling pass over `B` rows of `V` logits.
  *   logits        device, B rows, row r starts at logits + r*row_stride elements
  *   params        device [B] mis_row_params
@@ -84,7 +101,8 @@ size_t mis_workspace_bytes(int64_t B, int64_t V, int dtype);
  *   out_keep      device [B, ceil(V/32)] uint32 keep bitmask, bit j%32 of word
  *                 j/32 = token j survives every filter (nullable; debug)
  *   workspace     device scratch of at least mis_workspace_bytes(B, V, dtype)
- *                 bytes, 256-byte aligned; not shared by concurrent calls
+ *                 bytes, 256-byte aligned, prepared once by mis_workspace_init();
+ *                 not shared by concurrent calls
  *   stream        hipStream_t the kernels are launched on
  * Returns MIS_OK or an error code; launches are asynchronous.
  */
@@ -95,9 +113,8 @@ int mis_sample(const void *logits, int dtype, int64_t B, int64_t V, int64_t row_
 
 /*
  * Instrumented mis_sample(): identical results, and additionally records the
- * caller's hipEvent_t handles events[0] before the chunk pass, events[1]
- * between the chunk pass and the finalize, events[2] after the finalize, all
- * on `stream`.  No counterpart in the reference: it exists so benchmarks can
+ * caller's hipEvent_t handles events[0] before the sampling kernel, events[1]
+ * after it and events[2] after the optional debug emit, all on `stream`.  No counterpart in the reference: it exists so benchmarks can
  * time each kernel on the stream it runs on.
  */
 int mis_sample_profiled(const void *logits, int dtype, int64_t B, int64_t V, int64_t row_stride,

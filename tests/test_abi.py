@@ -30,7 +30,7 @@ def lib():
 
 def test_header_declares_expected_api():
     names = declared_functions()
-    for n in ["mis_workspace_bytes", "mis_sample", "mis_sample_profiled", "mis_strerror", "mis_last_hip_error",
+    for n in ["mis_workspace_bytes", "mis_workspace_init", "mis_sample", "mis_sample_profiled", "mis_strerror", "mis_last_hip_error",
               "mis_abi_version"]:
         assert n in names
 
@@ -46,7 +46,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version_and_strings(lib):
-    assert lib.mis_abi_version() == 1
+    assert lib.mis_abi_version() == 2
     assert lib.mis_strerror(0) == b"ok"
     assert b"workspace" in lib.mis_strerror(2)
     assert lib.mis_last_hip_error() == 0

@@ -11,10 +11,10 @@ import os
 from . import build as _build
 
 DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
-ROW_OK, ROW_BAD_PARAM, ROW_INVALID = 0, 1, 2
-ABI_VERSION = 1
+ROW_OK, ROW_BAD_PARAM, ROW_INVALID, ROW_UNSUPPORTED, ROW_INTERNAL = 0, 1, 2, 3, 4
+ABI_VERSION = 2
 
-EXPORTED = ("mis_workspace_bytes", "mis_sample", "mis_sample_profiled", "mis_strerror", "mis_last_hip_error",
+EXPORTED = ("mis_workspace_bytes", "mis_workspace_init", "mis_sample", "mis_sample_profiled", "mis_strerror", "mis_last_hip_error",
             "mis_abi_version")
 
 _lib = None
@@ -41,6 +41,8 @@ def load():
     i64, vp = ctypes.c_int64, ctypes.c_void_p
     lib.mis_workspace_bytes.argtypes = [i64, i64, ctypes.c_int]
     lib.mis_workspace_bytes.restype = ctypes.c_size_t
+    lib.mis_workspace_init.argtypes = [vp, ctypes.c_size_t, vp]
+    lib.mis_workspace_init.restype = ctypes.c_int
     lib.mis_sample.argtypes = [vp, ctypes.c_int, i64, i64, i64, vp, vp, vp, vp, vp, vp, ctypes.c_size_t, vp]
     lib.mis_sample.restype = ctypes.c_int
     lib.mis_sample_profiled.argtypes = [vp, ctypes.c_int, i64, i64, i64, vp, vp, vp, vp, vp, vp, ctypes.c_size_t, vp,
@@ -58,6 +60,14 @@ def load():
 
 def workspace_bytes(B: int, V: int, dtype: int) -> int:
     return int(load().mis_workspace_bytes(B, V, dtype))
+
+
+def workspace_init(ws_ptr: int, ws_bytes: int, stream: int) -> None:
+    """Clear a new workspace's control words (once, before its first use)."""
+    lib = load()
+    rc = lib.mis_workspace_init(ws_ptr, ws_bytes, stream)
+    if rc != 0:
+        raise MisError(f"mis_workspace_init failed: {lib.mis_strerror(rc).decode()}")
 
 
 def sample(logits_ptr: int, dtype: int, B: int, V: int, row_stride: int, params_ptr: int, ids_ptr: int,

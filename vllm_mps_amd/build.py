@@ -25,6 +25,9 @@ HIPCC_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
     "-fhip-fp32-correctly-rounded-divide-sqrt", "-fno-fast-math", "-ffp-contract=off",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # keep each thread's register-resident chunk as separate scalars; promoting
+    # it to one wide vector value makes the allocator spill it whole
+    "-mllvm", "-disable-promote-alloca-to-vector=true",
     "-Wall", "-Wno-unused-function",
 ]
 

@@ -1,0 +1,303 @@
+// mis_device.h -- device-side primitives of the sampler kernels: dtype loads,
+// temperature scaling, wave64 / workgroup reductions and scans, histogram
+// search, raw-key interval search and a latency-hiding row scan.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+#include "mis_common.h"
+
+namespace mis {
+
+constexpr int NT = 256;            // threads per workgroup (4 waves of 64)
+constexpr int NWAVE = NT / 64;
+
+// ------------------------------------------------------------------ dtype io
+
+template <int DT> struct Traits;
+template <> struct Traits<F32> { static constexpr int VEC = 4, ESZ = 4; };
+template <> struct Traits<F16> { static constexpr int VEC = 8, ESZ = 2; };
+template <> struct Traits<BF16> { static constexpr int VEC = 8, ESZ = 2; };
+
+template <int DT> __device__ __forceinline__ float cvt16(uint32_t h)
+{
+    if (DT == F16) { _Float16 v = __builtin_bit_cast(_Float16, (uint16_t)h); return (float)v; }
+    return bits_f32(h << 16);
+}
+
+// logits live in global memory: load through the global address space so
+// the compiler emits global_load rather than flat_load
+#define MIS_GLOBAL __attribute__((address_space(1)))
+
+template <int DT> __device__ __forceinline__ float load1(const char *rowp, int64_t j)
+{
+    if (DT == F32) return ((const MIS_GLOBAL float *)rowp)[j];
+    return cvt16<DT>(((const MIS_GLOBAL uint16_t *)rowp)[j]);
+}
+
+// VEC elements from a 16-byte aligned address
+template <int DT> __device__ __forceinline__ void loadvec(const char *rowp, int64_t j0, float *out)
+{
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    const u32x4 v = *(const MIS_GLOBAL u32x4 *)(rowp + j0 * Traits<DT>::ESZ);
+    if (DT == F32) {
+        out[0] = bits_f32(v.x); out[1] = bits_f32(v.y); out[2] = bits_f32(v.z); out[3] = bits_f32(v.w);
+    } else {
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) { out[2 * i] = cvt16<DT>(w[i] & 0xffffu); out[2 * i + 1] = cvt16<DT>(w[i] >> 16); }
+    }
+}
+
+// y = dtype(f32(x) / T): IEEE binary32 division (hipcc's correctly rounded
+// divide), then round-to-nearest-even into the 16-bit dtype.
+template <int DT> __device__ __forceinline__ float scale_y(float x, float T)
+{
+    const float q = x / T;
+    return DT == F32 ? q : rn_dtype(q, DT);
+}
+
+// ------------------------------------------------------------------ wave / block
+
+// Workgroup-uniform values read back from LDS: moving them to scalar
+// registers frees vector registers and lets loads through them go scalar.
+__device__ __forceinline__ uint32_t uni(uint32_t v) { return (uint32_t)__builtin_amdgcn_readfirstlane((int)v); }
+__device__ __forceinline__ int32_t uni(int32_t v) { return __builtin_amdgcn_readfirstlane(v); }
+__device__ __forceinline__ float uni(float v) { return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, v))); }
+__device__ __forceinline__ double uni(double v)
+{
+    const uint64_t b = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)b);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(b >> 32));
+    return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+
+__device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
+__device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
+
+template <class T> __device__ __forceinline__ T wave_sum(T v)
+{
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+template <class T> __device__ __forceinline__ T wave_max(T v)
+{
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) { T w = __shfl_xor(v, o, 64); v = w > v ? w : v; }
+    return v;
+}
+template <class T> __device__ __forceinline__ T wave_min(T v)
+{
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) { T w = __shfl_xor(v, o, 64); v = w < v ? w : v; }
+    return v;
+}
+// (key desc, idx asc) arg-max
+__device__ __forceinline__ void wave_argmax(uint32_t &k, int32_t &i)
+{
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const uint32_t k2 = __shfl_xor(k, o, 64);
+        const int32_t i2 = __shfl_xor(i, o, 64);
+        if (k2 > k || (k2 == k && i2 < i)) { k = k2; i = i2; }
+    }
+}
+template <class T> __device__ __forceinline__ T wave_incl_scan(T v)
+{
+    const int l = lane_id();
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const T w = __shfl_up(v, o, 64);
+        if (l >= o) v += w;
+    }
+    return v;
+}
+
+// LDS scratch for the block reductions: NWAVE + 1 slots of 8 bytes
+struct Red { double d[NWAVE + 1]; int64_t l[NWAVE + 1]; uint32_t u[NWAVE + 1]; float f[NWAVE + 1]; };
+
+template <class T> __device__ __forceinline__ T *red_of(Red &r);
+template <> __device__ __forceinline__ double *red_of<double>(Red &r) { return r.d; }
+template <> __device__ __forceinline__ int64_t *red_of<int64_t>(Red &r) { return r.l; }
+template <> __device__ __forceinline__ uint32_t *red_of<uint32_t>(Red &r) { return r.u; }
+template <> __device__ __forceinline__ float *red_of<float>(Red &r) { return r.f; }
+
+template <class T> __device__ T block_excl_scan(T v, Red &rr, T *total)
+{
+    T *red = red_of<T>(rr);
+    const T inc = wave_incl_scan(v);
+    if (lane_id() == 63) red[wave_id()] = inc;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        T run = T(0);
+        for (int w = 0; w < NWAVE; ++w) { const T t = red[w]; red[w] = run; run += t; }
+        red[NWAVE] = run;
+    }
+    __syncthreads();
+    const T res = inc - v + red[wave_id()];
+    *total = red[NWAVE];
+    __syncthreads();
+    return res;
+}
+template <class T> __device__ T block_sum(T v, Red &rr)
+{
+    T *red = red_of<T>(rr);
+    v = wave_sum(v);
+    if (lane_id() == 0) red[wave_id()] = v;
+    __syncthreads();
+    T t = T(0);
+    for (int w = 0; w < NWAVE; ++w) t += red[w];
+    __syncthreads();
+    return t;
+}
+template <class T> __device__ T block_max(T v, Red &rr)
+{
+    T *red = red_of<T>(rr);
+    v = wave_max(v);
+    if (lane_id() == 0) red[wave_id()] = v;
+    __syncthreads();
+    T t = red[0];
+    for (int w = 1; w < NWAVE; ++w) t = red[w] > t ? red[w] : t;
+    __syncthreads();
+    return t;
+}
+template <class T> __device__ T block_min(T v, Red &rr)
+{
+    T *red = red_of<T>(rr);
+    v = wave_min(v);
+    if (lane_id() == 0) red[wave_id()] = v;
+    __syncthreads();
+    T t = red[0];
+    for (int w = 1; w < NWAVE; ++w) t = red[w] < t ? red[w] : t;
+    __syncthreads();
+    return t;
+}
+
+// Descending search over a histogram in LDS, run by one whole wave.  Finds
+// the first bin b from the top (index nbins-1 downwards) where
+// sum_{b' >= b} h[b'] >= target; *above = sum of the bins strictly above b.
+// If the target is never reached (rounding) it returns the lowest non-empty
+// bin.  nbins must be a multiple of 64.
+template <class T>
+__device__ int wave_find_desc(const T *h, int nbins, T target, T *above)
+{
+    const int l = lane_id();
+    const int per = nbins / 64;
+    T s = T(0);
+    for (int i = 0; i < per; ++i) s += h[nbins - 1 - (l * per + i)];
+    const T inc = wave_incl_scan(s);
+    const uint64_t mask = __ballot(inc >= target);
+    int bsel = 0;
+    T abv = T(0);
+    int first;
+    if (mask == 0ull) {
+        const uint64_t ne = __ballot(s > T(0));
+        if (ne == 0ull) { *above = T(0); return 0; }
+        first = 63 - __builtin_clzll(ne);
+        if (l == first) {
+            T run = inc - s;
+            for (int i = 0; i < per; ++i) {
+                const int b = nbins - 1 - (l * per + i);
+                if (h[b] > T(0)) { bsel = b; abv = run; }
+                run += h[b];
+            }
+        }
+    } else {
+        first = __builtin_ctzll(mask);
+        if (l == first) {
+            T run = inc - s;
+            bsel = nbins - 1 - (l * per + per - 1);
+            abv = run;
+            for (int i = 0; i < per; ++i) {
+                const int b = nbins - 1 - (l * per + i);
+                if (run + h[b] >= target) { bsel = b; abv = run; break; }
+                run += h[b];
+            }
+        }
+    }
+    bsel = __shfl(bsel, first, 64);
+    abv = __shfl(abv, first, 64);
+    *above = abv;
+    return bsel;
+}
+
+// ------------------------------------------------------------------ raw-key intervals
+//
+// The scaled value y = scale(x) is a non-decreasing function of the raw
+// logit x, so the set of raw values whose scaled key lies in [klo, khi] is an
+// interval of raw keys.  Filtering raw keys first avoids a division for every
+// element a scan does not need.
+
+template <int DT> __device__ __forceinline__ uint32_t rk_of_xkey(uint32_t xk, float T)
+{
+    return row_key(scale_y<DT>(f32_of_key(xk), T), DT);
+}
+
+// Smallest raw key (over all non-NaN floats) whose scaled key is >= target;
+// 0xff800001 when none.  Executed by one whole wave (64-ary search).
+template <int DT> __device__ uint32_t x_lower(uint32_t target, float T)
+{
+    const uint32_t XLO = 0x007fffffu, XHI = 0xff800000u;  // -inf .. +inf
+    if (rk_of_xkey<DT>(XLO, T) >= target) return XLO;
+    if (rk_of_xkey<DT>(XHI, T) < target) return XHI + 1u;
+    uint64_t lo = XLO, hi = XHI;  // pred(lo) false, pred(hi) true
+    const int l = lane_id();
+    while (hi - lo > 1) {
+        uint64_t step = (hi - lo) / 64;
+        if (step == 0) step = 1;
+        const uint64_t p = lo + (uint64_t)(l + 1) * step;
+        const bool pred = p >= hi ? true : (rk_of_xkey<DT>((uint32_t)p, T) >= target);
+        const uint64_t mask = __ballot(pred);
+        if (mask == 0ull) { lo = lo + 64 * step; continue; }
+        const int f = __builtin_ctzll(mask);
+        const uint64_t nhi = lo + (uint64_t)(f + 1) * step;
+        if (nhi < hi) hi = nhi;
+        lo = lo + (uint64_t)f * step;
+    }
+    return (uint32_t)hi;
+}
+
+// Largest raw key whose scaled key is <= target (0x007ffffe when none).
+template <int DT> __device__ uint32_t x_upper(uint32_t target, float T)
+{
+    if (target == 0xffffffffu) return 0xff800000u;
+    return x_lower<DT>(target + 1u, T) - 1u;
+}
+
+// ------------------------------------------------------------------ row scans
+
+// Calls f(j, x) for every j in [jb, je) of a row.  Each thread issues UNROLL
+// 16-byte loads before consuming any, so a single workgroup keeps
+// NT * UNROLL * 16 bytes in flight.  jb must be a multiple of the vector
+// width when vec_ok.  All threads of the block must call it.
+template <int DT, int UNROLL, class F>
+__device__ __forceinline__ void scan_range(const char *rowp, int64_t jb, int64_t je, int vec_ok, F &&f)
+{
+    constexpr int VEC = Traits<DT>::VEC;
+    const int64_t tile = (int64_t)NT * VEC * UNROLL;
+    for (int64_t t0 = jb; t0 < je; t0 += tile) {
+        float xs[UNROLL][VEC];
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u) {
+            const int64_t j0 = t0 + ((int64_t)u * NT + threadIdx.x) * VEC;
+            if (vec_ok && j0 + VEC <= je) {
+                loadvec<DT>(rowp, j0, xs[u]);
+            } else {
+#pragma unroll
+                for (int e = 0; e < VEC; ++e) xs[u][e] = (j0 + e < je) ? load1<DT>(rowp, j0 + e) : 0.0f;
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u) {
+            const int64_t j0 = t0 + ((int64_t)u * NT + threadIdx.x) * VEC;
+#pragma unroll
+            for (int e = 0; e < VEC; ++e)
+                if (j0 + e < je) f(j0 + e, xs[u][e]);
+        }
+    }
+}
+
+}  // namespace mis

@@ -1,109 +1,165 @@
 // mis_sampler.hip -- MI355X (gfx950) decode-step token sampler behind the C ABI
 // declared in include/mis_sampler.h.
 //
-// One call = up to three stream-ordered launches:
-//   K1 k_chunk  grid (G, B), 256 threads.  Each workgroup holds one chunk of
-//               one logits row in registers (a single coalesced 16-byte-vector
-//               read of HBM) and reduces it to a chunk summary: argmax of the
-//               raw logits, the chunk max of the scaled logits, and -- by row
-//               mode -- the chunk-local top-k' candidates, or the float64
-//               softmax mass with a 256-bin histogram (top byte of the order
-//               key) of counts and masses.
-//   K2 k_final  grid (B), 1024 threads.  Merges the G summaries of a row,
-//               resolves the top-k threshold and the top-p cut, and draws the
-//               token by inverse CDF in vocabulary order.  Re-reads of the row
-//               (L2 / MALL) happen only to refine a histogram bin or to scan
-//               one chunk for the draw.
-//   K3 k_emit   grid (G, B), 256 threads, only when the caller asks for the
-//               debug probabilities / keep bitmask.
+// One call = one launch of k_sample (plus k_emit when the caller asks for the
+// debug probabilities / keep bitmask).
 //
-// Semantics follow model/sampler.py:18-60 per row (see the oracle for the
-// exact contract):  greedy argmax (ties -> lowest index) when T == 0;
-// y = dtype(f32(x) / T); top-k keeps y >= k'-th largest (all ties); top-p on
-// the stable descending order with float64 masses (fp32 rows) or torch's
-// 16-bit rounding chain (fp16/bf16 rows); the draw is
+// k_sample: B*G workgroups of 256 threads.  Each workgroup takes a ticket
+// (atomic counter) naming one chunk of one row, loads that chunk into
+// registers with coalesced 16-byte vector reads -- the only HBM read of the
+// logits -- and reduces it to a chunk summary.  The last workgroup of a row
+// to arrive becomes the row's leader and finishes the row:
+//   greedy       argmax merge;
+//   small top-k  per chunk: every element >= a threshold that keeps the
+//                chunk's top k'; leader: exact k'-th value -> survivors ->
+//                top-p over the survivors -> draw;
+//   temperature  per-chunk weights -> the chunk holding the draw -> that chunk
+//                is re-read for the index;
+//   fp32 top-p   float64 mass histograms on a fixed value grid (16 bins per
+//                unit below each chunk's max) locate the bin holding the cut;
+//                the row's workgroups, still holding their chunks in
+//                registers, refine that bin (sub-histogram) and collect its
+//                elements when the leader asks; the leader resolves the exact
+//                cut and draws;
+//   otherwise    (large k', fp16/bf16 top-p, overflows) the leader re-reads the
+//                row: radix descent by mass or count, and the 16-bit rounding
+//                chain walked over runs of equal keys.
+// Tickets are handed out in start order, so a workgroup only ever waits for
+// row mates that have already started; every wait is bounded.
+//
+// Semantics follow model/sampler.py:18-60 per row: greedy argmax (ties ->
+// lowest index) when T == 0; y = dtype(f32(x) / T); top-k keeps y >= k'-th
+// largest (all ties); top-p on the stable descending order with exact masses
+// (fp32 rows) or torch's 16-bit rounding chain (fp16/bf16 rows); the draw is
 // min{i : sum_{j<=i} w_j > u * sum w} over the kept weights w = exp(y - m).
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
 
-#include "mis_common.h"
+#include "mis_device.h"
 #include "mis_sampler.h"
 
 namespace mis {
 
-constexpr int K1_THREADS = 256;
-constexpr int K2_THREADS = 512;
-constexpr int K3_THREADS = 256;
-constexpr int K2_WAVES = K2_THREADS / 64;
 constexpr int K_SMALL = 1024;      // largest k' served by the candidate path
 constexpr int CAND_CAP = 2048;     // candidates one chunk may emit
-constexpr int SURV_CAP = 4096;     // top-k survivors the finalize holds in LDS
-constexpr int G_MAX = 1024;        // chunks per row
-constexpr int REGION_BINS = 16;    // L1 bins per 16-bit chain pass (16 x 256 keys)
+constexpr int SURV_CAP = 2048;     // top-k survivors held in LDS
+constexpr int G_MAX = 256;         // chunks per row
+constexpr int FB_W = 16;           // fine bins per unit of y (top-p)
+constexpr int FB_N = 384;          // fine bins below each chunk max (24 units)
+constexpr int SUB_N = 256;         // sub-bins of a refined fine bin
+constexpr int WCAP = 2048;         // elements a collect round may gather
+constexpr int REGION_BINS = 8;     // L1 bins per 16-bit chain pass
 constexpr int RUN_CAP = REGION_BINS * 256;
-constexpr int TIE_CAP = 4096;
+constexpr int TIE_CAP = 2048;
+constexpr int STAGE_CAP = 4096;      // elements one workgroup stages per round
 constexpr uint32_t NCAND_OVERFLOW = 0xffffffffu;
 constexpr int32_t IDX_ALL = 0x7fffffff;
+constexpr uint32_t SPIN_MAX = 1u << 22;  // bounded waits (well under a second)
 
 enum : int { M_BAD = 0, M_GREEDY = 1, M_SMALLK = 2, M_LARGEK = 3, M_TOPP = 4, M_TEMP = 5 };
 enum : uint32_t { FLAG_NAN = 1u, FLAG_PINF = 2u };
+enum : uint32_t { R_COLLECT = 1u, R_HIST = 2u, R_DONE = 3u };
+constexpr int ROW_INTERNAL = MIS_ROW_INTERNAL;
 
-// ------------------------------------------------------------------ layout
+// ------------------------------------------------------------------ workspace
 
-struct ChunkSum {           // 32 bytes per (row, chunk)
-    uint32_t xkey;          // argmax key of the raw logits (NaN = 0xffffffff)
-    int32_t xarg;           // first index holding it
-    float ymax;             // max scaled logit of the chunk
-    uint32_t flags;
-    uint32_t ncand;         // candidates written (small-k rows) or NCAND_OVERFLOW
-    uint32_t pad;
-    double S;               // sum exp(y - ymax) over the chunk (float64)
+struct Ctl {                    // 256 B
+    unsigned long long ticket;  // monotonically increasing; task = ticket % (B*G)
+    uint32_t error;             // bit 0: a bounded wait expired
+    uint32_t pad[61];
 };
 
-struct RowOut {             // 48 bytes per row, read by k_emit
-    int64_t id;
-    int32_t status;
-    int32_t mode;
-    float m;                // row max of the scaled logits
-    uint32_t cut_key;       // kept iff key > cut_key or (key == cut_key and j <= cut_i)
-    int32_t cut_i;
-    int32_t pad;
-    double S;               // sum of kept weights exp(y - m)
+struct RowCtl {                 // 64 B per row, zero at rest
+    uint32_t arrive;            // phase-1 arrivals
+    uint32_t round;             // last published refinement round (1, 2, ...)
+    uint32_t rarrive;           // round arrivals, cumulative
+    uint32_t wcount;            // elements appended by the collect round
+    uint32_t exited;            // workgroups done with the row
+    uint32_t rtype;             // R_COLLECT / R_HIST / R_DONE
+    uint32_t klo, khi;          // scaled-key range of the round
+    uint32_t kahi;              // collect: (khi, kahi] is summed as kept mass
+    float hlo, hhi;             // hist: value range [hlo, hhi)
+    float m;                    // row max of y
+    uint32_t ovf;               // a round overflowed a staging or window buffer
+    int32_t rbin;               // row fine bin (below the row max's bin) holding the cut
+    uint32_t pad[2];
+};
+static_assert(sizeof(RowCtl) == 64, "RowCtl is 64 bytes");
+
+// The control prefix of the workspace (Ctl, then one RowCtl for every row the
+// ABI allows) sits at a fixed place whatever the shape, so control words that
+// each call leaves at zero stay zero for the next call of any shape.
+constexpr int64_t B_MAX = 65535;
+constexpr size_t CTL_PREFIX = 256 + sizeof(RowCtl) * (size_t)(B_MAX + 1);
+
+struct ChunkSum {               // 64 B per (row, chunk)
+    uint32_t xkey;              // argmax key of the raw logits (NaN = 0xffffffff)
+    int32_t xarg;
+    float ymax;                 // max scaled logit of the chunk
+    uint32_t flags;
+    uint32_t ncand;             // small-k candidates written, or NCAND_OVERFLOW
+    float xmax;                 // max raw logit of the chunk
+    uint32_t pad0, pad1;
+    double S;                   // sum of weights relative to the chunk max
+    double gmc;                 // top-p: floor(ymax * FB_W), the chunk's bin anchor
+    double below;               // top-p: mass below the fine-bin range
     double pad2;
 };
 
-struct Cand { uint32_t key; int32_t idx; };
+struct RowOut {                 // 64 B per row, read by k_emit
+    int64_t id;
+    int32_t status;
+    int32_t mode;
+    float m;                    // row max of y
+    uint32_t cut_key;           // kept iff key > cut_key or (key == cut_key and j <= cut_i)
+    int32_t cut_i;
+    int32_t pad;
+    double S;                   // sum of kept weights exp(y - m)
+    double pad2[3];
+};
+
+struct Cand { float x; int32_t idx; };
+struct Elem { uint32_t key; int32_t idx; };
 
 struct Layout {
     int64_t B, V;
     int ept, G;
-    size_t rowout, chunks, l1cnt, l1mass, cand, total;
+    size_t ctl, rowctl, rowout, chunks, fbc, fbm, cand, subc, subm, win, amass, total;
 };
 
 static inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-static Layout make_layout(int64_t B, int64_t V)
+static Layout make_layout(int64_t B, int64_t V, int dtype)
 {
     Layout L;
     L.B = B; L.V = V;
+    // fp32 chunks hold at most 32 elements per thread: with 64 the fp32
+    // top-p refinement rounds exceed the register budget of three waves/SIMD
     static const int opts[4] = {64, 32, 16, 8};
     L.ept = 8;
-    for (int i = 0; i < 4; ++i) {
-        int64_t G = (V + (int64_t)K1_THREADS * opts[i] - 1) / ((int64_t)K1_THREADS * opts[i]);
+    for (int i = dtype == MIS_DTYPE_F32 ? 1 : 0; i < 4; ++i) {
+        const int64_t G = (V + (int64_t)NT * opts[i] - 1) / ((int64_t)NT * opts[i]);
         if (B * G >= 1024 && G <= G_MAX) { L.ept = opts[i]; break; }
     }
-    L.G = (int)((V + (int64_t)K1_THREADS * L.ept - 1) / ((int64_t)K1_THREADS * L.ept));
-    if (L.G > G_MAX) {  // very large vocabularies: widest chunks
+    L.G = (int)((V + (int64_t)NT * L.ept - 1) / ((int64_t)NT * L.ept));
+    if (L.G > G_MAX) {
         L.ept = 64;
-        L.G = (int)((V + (int64_t)K1_THREADS * 64 - 1) / ((int64_t)K1_THREADS * 64));
+        L.G = (int)((V + (int64_t)NT * 64 - 1) / ((int64_t)NT * 64));
     }
+    const size_t BG = (size_t)B * L.G;
     size_t off = 0;
+    L.ctl = off;    off = align256(off + sizeof(Ctl));
+    L.rowctl = off; off = CTL_PREFIX;
     L.rowout = off; off = align256(off + sizeof(RowOut) * (size_t)B);
-    L.chunks = off; off = align256(off + sizeof(ChunkSum) * (size_t)B * L.G);
-    L.l1cnt = off;  off = align256(off + sizeof(uint32_t) * 256 * (size_t)B * L.G);
-    L.l1mass = off; off = align256(off + sizeof(double) * 256 * (size_t)B * L.G);
-    L.cand = off;   off = align256(off + sizeof(Cand) * (size_t)CAND_CAP * B * L.G);
+    L.chunks = off; off = align256(off + sizeof(ChunkSum) * BG);
+    L.fbc = off;    off = align256(off + sizeof(uint32_t) * FB_N * BG);
+    L.fbm = off;    off = align256(off + sizeof(double) * FB_N * BG);
+    L.cand = off;   off = align256(off + sizeof(Cand) * (size_t)CAND_CAP * BG);
+    L.subc = off;   off = align256(off + sizeof(uint32_t) * SUB_N * (size_t)B);
+    L.subm = off;   off = align256(off + sizeof(double) * SUB_N * (size_t)B);
+    L.win = off;    off = align256(off + sizeof(Elem) * WCAP * (size_t)B);
+    L.amass = off;  off = align256(off + sizeof(double) * G_MAX * (size_t)B);
     L.total = off;
     return L;
 }
@@ -116,7 +172,7 @@ __device__ __forceinline__ RowPlan plan_row(const mis_row_params &P, int64_t V)
 {
     RowPlan r;
     r.T = P.temperature; r.top_p = P.top_p; r.u = P.uniform; r.kk = 0; r.topp = 0;
-    bool bad = !(P.temperature >= 0.0f) || P.top_k < 0 || !(P.top_p > 0.0f) || !(P.uniform == P.uniform);
+    const bool bad = !(P.temperature >= 0.0f) || P.top_k < 0 || !(P.top_p > 0.0f) || !(P.uniform == P.uniform);
     if (bad) { r.mode = M_BAD; return r; }
     if (P.temperature == 0.0f) { r.mode = M_GREEDY; return r; }
     int64_t kk = P.top_k > 0 ? ((int64_t)P.top_k < V ? (int64_t)P.top_k : V) : 0;
@@ -130,543 +186,415 @@ __device__ __forceinline__ RowPlan plan_row(const mis_row_params &P, int64_t V)
     return r;
 }
 
-// ------------------------------------------------------------------ dtype io
+// ------------------------------------------------------------------ context
 
-template <int DT> struct Traits;
-template <> struct Traits<F32> { static constexpr int VEC = 4, ESZ = 4; };
-template <> struct Traits<F16> { static constexpr int VEC = 8, ESZ = 2; };
-template <> struct Traits<BF16> { static constexpr int VEC = 8, ESZ = 2; };
-
-template <int DT> __device__ __forceinline__ float cvt16(uint32_t h)
-{
-    if (DT == F16) { _Float16 v = __builtin_bit_cast(_Float16, (uint16_t)h); return (float)v; }
-    return bits_f32(h << 16);
-}
-
-template <int DT> __device__ __forceinline__ float load1(const char *rowp, int64_t j)
-{
-    if (DT == F32) return reinterpret_cast<const float *>(rowp)[j];
-    return cvt16<DT>(reinterpret_cast<const uint16_t *>(rowp)[j]);
-}
-
-template <int DT> __device__ __forceinline__ void loadvec(const char *rowp, int64_t j0, float *out)
-{
-    uint4 v = *reinterpret_cast<const uint4 *>(rowp + j0 * Traits<DT>::ESZ);
-    if (DT == F32) {
-        out[0] = bits_f32(v.x); out[1] = bits_f32(v.y); out[2] = bits_f32(v.z); out[3] = bits_f32(v.w);
-    } else {
-        uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) { out[2 * i] = cvt16<DT>(w[i] & 0xffffu); out[2 * i + 1] = cvt16<DT>(w[i] >> 16); }
-    }
-}
-
-// y = dtype(f32(x) / T): IEEE division (hipcc's default correctly rounded
-// f32 divide), then RNE to the 16-bit dtype.
-template <int DT> __device__ __forceinline__ float scale_y(float x, float T)
-{
-    float q = x / T;
-    return DT == F32 ? q : rn_dtype(q, DT);
-}
-
-// ------------------------------------------------------------------ wave / block helpers
-
-__device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
-__device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
-
-template <class T> __device__ __forceinline__ T wave_sum(T v)
-{
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
-}
-
-template <class T> __device__ __forceinline__ T wave_max(T v)
-{
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) { T w = __shfl_xor(v, o, 64); v = w > v ? w : v; }
-    return v;
-}
-
-// (key desc, idx asc) arg-max reduction
-__device__ __forceinline__ void wave_argmax(uint32_t &k, int32_t &i)
-{
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        uint32_t k2 = __shfl_xor(k, o, 64);
-        int32_t i2 = __shfl_xor(i, o, 64);
-        if (k2 > k || (k2 == k && i2 < i)) { k = k2; i = i2; }
-    }
-}
-
-template <class T> __device__ __forceinline__ T wave_incl_scan(T v)
-{
-    const int l = lane_id();
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        T w = __shfl_up(v, o, 64);
-        if (l >= o) v += w;
-    }
-    return v;
-}
-
-// Block-wide exclusive scan; `red` is LDS scratch of >= NW entries.  Returns
-// the exclusive prefix of this thread and writes the block total to *total.
-template <int NT, class T> __device__ T block_excl_scan(T v, T *red, T *total)
-{
-    constexpr int NW = NT / 64;
-    T inc = wave_incl_scan(v);
-    if (lane_id() == 63) red[wave_id()] = inc;
-    __syncthreads();
-    if (wave_id() == 0) {
-        T t = lane_id() < NW ? red[lane_id()] : T(0);
-        T ti = wave_incl_scan(t);
-        if (lane_id() < NW) red[lane_id()] = ti - t;
-        if (lane_id() == NW - 1) red[NW] = ti;
-    }
-    __syncthreads();
-    T res = inc - v + red[wave_id()];
-    *total = red[NW];
-    __syncthreads();
-    return res;
-}
-
-template <int NT, class T> __device__ T block_sum(T v, T *red)
-{
-    constexpr int NW = NT / 64;
-    v = wave_sum(v);
-    if (lane_id() == 0) red[wave_id()] = v;
-    __syncthreads();
-    T t = T(0);
-    for (int w = 0; w < NW; ++w) t += red[w];
-    __syncthreads();
-    return t;
-}
-
-template <int NT, class T> __device__ T block_max(T v, T *red)
-{
-    constexpr int NW = NT / 64;
-    v = wave_max(v);
-    if (lane_id() == 0) red[wave_id()] = v;
-    __syncthreads();
-    T t = red[0];
-    for (int w = 1; w < NW; ++w) t = red[w] > t ? red[w] : t;
-    __syncthreads();
-    return t;
-}
-
-template <int NT, class T> __device__ T block_min(T v, T *red)
-{
-    constexpr int NW = NT / 64;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) { T w = __shfl_xor(v, o, 64); v = w < v ? w : v; }
-    if (lane_id() == 0) red[wave_id()] = v;
-    __syncthreads();
-    T t = red[0];
-    for (int w = 1; w < NW; ++w) t = red[w] < t ? red[w] : t;
-    __syncthreads();
-    return t;
-}
-
-// Descending search over a histogram held in LDS (run by one whole wave).
-// Finds the first bin b (from the top) where acc + sum_{b' >= b} h[b'] >= target
-// and returns b with *above = sum of bins strictly above b.  If the target is
-// never reached (rounding), returns the lowest non-empty bin.
-template <class T>
-__device__ int wave_find_desc(const T *h, int nbins, T target, T *above)
-{
-    const int l = lane_id();
-    const int per = nbins / 64;
-    // lane l owns bins [nbins-1 - l*per, nbins - (l+1)*per] in descending order
-    T s = T(0);
-    for (int i = 0; i < per; ++i) s += h[nbins - 1 - (l * per + i)];
-    T inc = wave_incl_scan(s);
-    uint64_t mask = __ballot(inc >= target);
-    int first;
-    if (mask == 0ull) {
-        // not reached: lowest non-empty bin
-        uint64_t ne = __ballot(s > T(0));
-        if (ne == 0ull) { *above = T(0); return 0; }
-        first = 63 - __builtin_clzll(ne);
-        T before = __shfl(inc - s, first, 64);
-        int bsel = 0;
-        T abv = before;
-        if (l == first) {
-            T run = before;
-            for (int i = 0; i < per; ++i) {
-                int b = nbins - 1 - (l * per + i);
-                if (h[b] > T(0)) { bsel = b; abv = run; }
-                run += h[b];
-            }
-        }
-        bsel = __shfl(bsel, first, 64);
-        abv = __shfl(abv, first, 64);
-        *above = abv;
-        return bsel;
-    }
-    first = __builtin_ctzll(mask);
-    int bsel = 0;
-    T abv = T(0);
-    if (l == first) {
-        T run = inc - s;
-        bsel = nbins - 1 - (l * per + per - 1);
-        abv = run;
-        for (int i = 0; i < per; ++i) {
-            int b = nbins - 1 - (l * per + i);
-            if (run + h[b] >= target) { bsel = b; abv = run; break; }
-            run += h[b];
-        }
-    }
-    bsel = __shfl(bsel, first, 64);
-    abv = __shfl(abv, first, 64);
-    *above = abv;
-    return bsel;
-}
-
-// ------------------------------------------------------------------ K1: chunk pass
-
-template <int DT, int EPT>
-__global__ __launch_bounds__(K1_THREADS) void k_chunk(const char *__restrict__ logits, int64_t V,
-                                                      int64_t stride_bytes, int vec_ok,
-                                                      const mis_row_params *__restrict__ params,
-                                                      Layout L, char *__restrict__ ws)
-{
-    constexpr int VEC = Traits<DT>::VEC, NV = EPT / VEC, CH = K1_THREADS * EPT;
-    const int tid = threadIdx.x, chunk = blockIdx.x, row = blockIdx.y;
-    const int64_t base = (int64_t)chunk * CH;
-    const char *rowp = logits + (int64_t)row * stride_bytes;
-    const RowPlan pl = plan_row(params[row], V);
-    ChunkSum *cs = reinterpret_cast<ChunkSum *>(ws + L.chunks) + (size_t)row * L.G + chunk;
-
-    __shared__ uint32_t s_u[256];
-    __shared__ double s_d[256];
-    __shared__ uint32_t s_red_u[8];
-    __shared__ int32_t s_red_i[8];
-    __shared__ double s_red_d[8];
-    __shared__ uint32_t s_bcast[4];
-
-    float x[EPT];
-#pragma unroll
-    for (int v = 0; v < NV; ++v) {
-        const int64_t j0 = base + ((int64_t)v * K1_THREADS + tid) * VEC;
-        if (vec_ok && j0 + VEC <= V) {
-            loadvec<DT>(rowp, j0, &x[v * VEC]);
-        } else {
-#pragma unroll
-            for (int e = 0; e < VEC; ++e) x[v * VEC + e] = (j0 + e < V) ? load1<DT>(rowp, j0 + e) : 0.0f;
-        }
-    }
-    auto idx_of = [&](int i) -> int64_t { return base + ((int64_t)(i / VEC) * K1_THREADS + tid) * VEC + (i % VEC); };
-
-    // ---- argmax of the raw logits (every mode)
-    uint32_t bk = 0u;
-    int32_t bi = IDX_ALL;
-#pragma unroll
-    for (int i = 0; i < EPT; ++i) {
-        const int64_t j = idx_of(i);
-        if (j < V) {
-            uint32_t k = argmax_key(x[i]);
-            if (k > bk) { bk = k; bi = (int32_t)j; }  // ascending j per thread: first wins
-        }
-    }
-    wave_argmax(bk, bi);
-    if (lane_id() == 0) { s_red_u[wave_id()] = bk; s_red_i[wave_id()] = bi; }
-    __syncthreads();
-    if (tid == 0) {
-        for (int w = 1; w < K1_THREADS / 64; ++w) {
-            if (s_red_u[w] > bk || (s_red_u[w] == bk && s_red_i[w] < bi)) { bk = s_red_u[w]; bi = s_red_i[w]; }
-        }
-        s_bcast[0] = bk;
-        s_bcast[1] = (uint32_t)bi;
-    }
-    __syncthreads();
-    bk = s_bcast[0];
-    bi = (int32_t)s_bcast[1];
-
-    if (pl.mode == M_BAD || pl.mode == M_GREEDY) {
-        if (tid == 0) { cs->xkey = bk; cs->xarg = bi; cs->ymax = 0.0f; cs->flags = 0; cs->ncand = 0; cs->S = 0.0; }
-        return;
-    }
-
-    uint32_t flags = 0;
-    float ymax;
-    if (bk == 0xffffffffu) { flags |= FLAG_NAN; ymax = 0.0f; }
-    else ymax = scale_y<DT>(f32_of_key(bk), pl.T);  // scaling is monotone
-    if (ymax == INFINITY) flags |= FLAG_PINF;
-    if (flags) {
-        if (tid == 0) { cs->xkey = bk; cs->xarg = bi; cs->ymax = ymax; cs->flags = flags; cs->ncand = 0; cs->S = 0.0; }
-        return;
-    }
-
-    if (pl.mode == M_SMALLK) {
-        const uint32_t kneg = row_key(-INFINITY, DT);
-        uint32_t key[EPT];
-        uint32_t nfin = 0;
-#pragma unroll
-        for (int i = 0; i < EPT; ++i) {
-            const int64_t j = idx_of(i);
-            key[i] = (j < V) ? row_key(scale_y<DT>(x[i], pl.T), DT) : 0u;
-            nfin += key[i] > kneg ? 1u : 0u;
-        }
-        nfin = block_sum<K1_THREADS>(nfin, s_red_u);
-        // threshold: candidates are the finite elements with key >= thr
-        uint32_t thr = kneg + 1u;
-        if (nfin > (uint32_t)pl.kk) {
-            uint32_t prefix = 0u, rem = (uint32_t)pl.kk;
-            const int nlev = DT == F32 ? 4 : 2;
-            for (int lev = 0; lev < nlev; ++lev) {
-                const int shift = 24 - 8 * lev;
-                s_u[tid] = 0u;
-                __syncthreads();
-#pragma unroll
-                for (int i = 0; i < EPT; ++i) {
-                    const uint32_t k = key[i];
-                    bool in = k > kneg && (lev == 0 || (k >> (shift + 8)) == (prefix >> (shift + 8)));
-                    if (in) atomicAdd(&s_u[(k >> shift) & 255u], 1u);
-                }
-                __syncthreads();
-                if (wave_id() == 0) {
-                    uint32_t above;
-                    int d = wave_find_desc<uint32_t>(s_u, 256, rem, &above);
-                    if (lane_id() == 0) { s_bcast[0] = (uint32_t)d; s_bcast[1] = above; s_bcast[2] = s_u[d]; }
-                }
-                __syncthreads();
-                const uint32_t d = s_bcast[0], above = s_bcast[1], incnt = s_bcast[2];
-                rem -= above;
-                prefix |= d << shift;
-                __syncthreads();
-                if (incnt == rem) break;  // the whole bin is inside the top k'
-            }
-            thr = prefix;
-        }
-        uint32_t mine = 0;
-#pragma unroll
-        for (int i = 0; i < EPT; ++i) mine += (key[i] > kneg && key[i] >= thr) ? 1u : 0u;
-        uint32_t total;
-        uint32_t off = block_excl_scan<K1_THREADS>(mine, s_red_u, &total);
-        if (total <= (uint32_t)CAND_CAP) {
-            Cand *cand = reinterpret_cast<Cand *>(ws + L.cand) + ((size_t)row * L.G + chunk) * CAND_CAP;
-#pragma unroll
-            for (int i = 0; i < EPT; ++i) {
-                if (key[i] > kneg && key[i] >= thr) {
-                    Cand c; c.key = key[i]; c.idx = (int32_t)idx_of(i);
-                    cand[off++] = c;
-                }
-            }
-        }
-        if (tid == 0) {
-            cs->xkey = bk; cs->xarg = bi; cs->ymax = ymax; cs->flags = 0;
-            cs->ncand = total <= (uint32_t)CAND_CAP ? total : NCAND_OVERFLOW; cs->S = 0.0;
-        }
-        return;
-    }
-
-    // M_TOPP / M_LARGEK / M_TEMP: float64 softmax mass relative to the chunk max
-    const bool hist = pl.mode != M_TEMP;
-    if (hist) { s_u[tid] = 0u; s_d[tid] = 0.0; }
-    __syncthreads();
-    double S = 0.0;
-    const double ym = (double)ymax;
-    const bool allneg = (ymax == -INFINITY);
-#pragma unroll
-    for (int i = 0; i < EPT; ++i) {
-        const int64_t j = idx_of(i);
-        if (j < V) {
-            const float y = scale_y<DT>(x[i], pl.T);
-            const double e = allneg ? 0.0 : exp((double)y - ym);
-            S += e;
-            if (hist) {
-                const uint32_t b = row_key(y, DT) >> 24;
-                atomicAdd(&s_u[b], 1u);
-                atomicAdd(&s_d[b], e);
-            }
-        }
-    }
-    S = block_sum<K1_THREADS>(S, s_red_d);
-    if (hist) {
-        uint32_t *gc = reinterpret_cast<uint32_t *>(ws + L.l1cnt) + ((size_t)row * L.G + chunk) * 256;
-        double *gm = reinterpret_cast<double *>(ws + L.l1mass) + ((size_t)row * L.G + chunk) * 256;
-        gc[tid] = s_u[tid];
-        gm[tid] = s_d[tid];
-    }
-    if (tid == 0) { cs->xkey = bk; cs->xarg = bi; cs->ymax = ymax; cs->flags = 0; cs->ncand = 0; cs->S = S; }
-}
-
-// ------------------------------------------------------------------ K2: finalize
-
-struct K2Shared {
-    union {
-        struct { uint32_t cnt[4096]; double mass[4096]; } h;                       // 48 KB
-        struct { uint64_t sk[SURV_CAP]; double e[SURV_CAP]; uint64_t sk2[SURV_CAP]; } s;  // 96 KB
-        struct { uint32_t cnt[RUN_CAP]; uint32_t rkey[RUN_CAP]; uint32_t rcnt[RUN_CAP]; float rp[RUN_CAP]; } r;  // 64 KB
-        struct { int32_t idx[TIE_CAP]; } t;
-    } u;
-    double l1m[256];
-    uint32_t l1c[256];
-    double cw[G_MAX];          // per-chunk kept weight
-    double chs[G_MAX];         // per-chunk rescale exp(ymax_c - m)
-    double red_d[K2_WAVES + 1];
-    float red_f[K2_WAVES + 1];
-    int64_t red_l[K2_WAVES + 1];
-    uint32_t red_u[K2_WAVES + 1];
-    int32_t red_i[K2_WAVES + 1];
-    uint64_t red_q[K2_WAVES + 1];
-    uint32_t bu[8];
-    int32_t bi[8];
-    double bd[8];
-    float bf[8];
+struct Args {
+    const char *logits;
+    int64_t V;
+    int64_t stride_bytes;
+    int vec_ok;
+    const mis_row_params *params;
+    Layout L;
+    char *ws;
+    int64_t *out_ids;
+    int32_t *out_status;
 };
 
-struct K2Ctx {
+struct RowCx {                 // what the leader of a row works with
     const char *rowp;
     int64_t V;
     int vec_ok;
     float T;
-    float m;          // row max of y
+    float m;                   // row max of y
     int G;
-    int ept;
     int64_t CH;
+    int row;
+    const uint32_t *fbc;       // this row's chunk fine-bin counts [G][FB_N]
+    const double *fbm;         // this row's chunk fine-bin masses [G][FB_N]
+    uint32_t *subc;            // this row's sub-histogram [SUB_N]
+    double *subm;
 };
 
-// rk(x) = row key of the scaled value of raw x
-template <int DT> __device__ __forceinline__ uint32_t rk_of_xkey(uint32_t xk, float T)
-{
-    return row_key(scale_y<DT>(f32_of_key(xk), T), DT);
-}
+// ------------------------------------------------------------------ shared memory
 
-// Smallest raw key xk (over all non-NaN floats) with rk(xk) >= target
-// (0xff800001 if none).  One wave, 64-ary search.
-template <int DT> __device__ uint32_t x_lower(uint32_t target, float T)
-{
-    const uint32_t XLO = 0x007fffffu, XHI = 0xff800000u;  // -inf .. +inf
-    if (rk_of_xkey<DT>(XLO, T) >= target) return XLO;
-    if (rk_of_xkey<DT>(XHI, T) < target) return XHI + 1u;
-    uint64_t lo = XLO, hi = XHI;  // pred(lo) false, pred(hi) true
-    const int l = lane_id();
-    while (hi - lo > 1) {
-        uint64_t step = (hi - lo) / 64;
-        if (step == 0) step = 1;
-        uint64_t p = lo + (uint64_t)(l + 1) * step;
-        bool pred = p >= hi ? true : (rk_of_xkey<DT>((uint32_t)p, T) >= target);
-        uint64_t mask = __ballot(pred);
-        if (mask == 0ull) { lo = lo + 64 * step; continue; }
-        int f = __builtin_ctzll(mask);
-        uint64_t nhi = lo + (uint64_t)(f + 1) * step;
-        if (nhi < hi) hi = nhi;
-        lo = lo + (uint64_t)f * step;
-    }
-    return (uint32_t)hi;
-}
-
-// Largest raw key xk with rk(xk) <= target (XLO-1 if none).
-template <int DT> __device__ uint32_t x_upper(uint32_t target, float T)
-{
-    if (target == 0xffffffffu) return 0xff800000u;
-    uint32_t lb = x_lower<DT>(target + 1u, T);
-    return lb - 1u;
-}
-
-// One pass over the row; calls f(j, y, key) for elements whose raw key lies in
-// [xklo, xkhi].  All threads of the block must call it.
-template <int DT, class F>
-__device__ void rescan(const K2Ctx &c, uint32_t xklo, uint32_t xkhi, F &&f)
-{
-    constexpr int VEC = Traits<DT>::VEC;
-    if (xklo > xkhi) return;
-    for (int64_t t0 = 0; t0 < c.V; t0 += (int64_t)K2_THREADS * VEC) {
-        const int64_t j0 = t0 + (int64_t)threadIdx.x * VEC;
-        float xs[VEC];
-        if (c.vec_ok && j0 + VEC <= c.V) loadvec<DT>(c.rowp, j0, xs);
-        else {
-#pragma unroll
-            for (int e = 0; e < VEC; ++e) xs[e] = (j0 + e < c.V) ? load1<DT>(c.rowp, j0 + e) : 0.0f;
-        }
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) {
-            if (j0 + e < c.V) {
-                const uint32_t xk = key_of_f32(xs[e]);
-                if (xk >= xklo && xk <= xkhi) {
-                    const float y = scale_y<DT>(xs[e], c.T);
-                    f(j0 + e, y, row_key(y, DT));
-                }
-            }
-        }
-    }
-}
-
-// Raw-key interval covering the scaled-key interval [klo, khi].
-template <int DT> __device__ void x_interval(K2Shared &sh, uint32_t klo, uint32_t khi, float T, uint32_t *xlo, uint32_t *xhi)
-{
-    __syncthreads();
-    if (wave_id() == 0) {
-        uint32_t a = x_lower<DT>(klo, T);
-        uint32_t b = x_upper<DT>(khi, T);
-        if (lane_id() == 0) { sh.bu[6] = a; sh.bu[7] = b; }
-    }
-    __syncthreads();
-    *xlo = sh.bu[6];
-    *xhi = sh.bu[7];
-    __syncthreads();
-}
+struct Smem {
+    union {
+        struct { uint32_t cnt[FB_N]; double mass[FB_N]; } p1;                              // 4.5 KB
+        struct { uint32_t cnt[2048]; } h11;                                                // 8 KB
+        struct { uint32_t cnt[256]; double mass[256]; } h8;                                // 3 KB
+        struct { uint32_t key[SURV_CAP]; int32_t idx[SURV_CAP]; double e[SURV_CAP]; } s;   // 32 KB
+        struct { uint64_t k[SURV_CAP]; double e[SURV_CAP]; } so;                          // 32 KB
+        struct { uint32_t cnt[RUN_CAP]; uint32_t rkey[RUN_CAP]; uint32_t rcnt[RUN_CAP]; float rp[RUN_CAP]; } r;  // 32 KB
+        struct { int32_t idx[TIE_CAP]; } t;
+        struct { float x[STAGE_CAP]; uint32_t j[STAGE_CAP]; } st;                          // 32 KB
+    } u;
+    union {
+        struct { double m[FB_N]; uint32_t c[FB_N]; } rb;    // row-merged fine bins, index FB_N-1 = top
+        struct { uint32_t cnt[256]; double mass[256]; } l1;  // re-read path: level-1 histogram
+    } v;
+    double cw[G_MAX];          // per-chunk kept weight
+    double chs[G_MAX];         // per-chunk rescale to the row max
+    double sub_m[SUB_N];       // round-local histograms
+    uint32_t sub_c[SUB_N];
+    Red red;
+    uint32_t bu[8];
+    int32_t bi[8];
+    double bd[8];
+    float bf[8];
+    unsigned long long bq[2];
+    Args args;                 // launch arguments, RowCx and RowPlan of the row for the
+    RowCx cx;                  // leader's out-of-line functions (kept out of private
+    RowPlan pl;                // memory, which would otherwise hold a copy per lane)
+};
 
 __device__ __forceinline__ bool kept_by_cut(uint32_t key, int64_t j, uint32_t cut_key, int32_t cut_i)
 {
     return key > cut_key || (key == cut_key && j <= (int64_t)cut_i);
 }
 
-// Radix descent over the row keys >= floor_key.  Level 1 comes from the
-// 256-bin histogram in sh.l1c / sh.l1m; later levels re-read the row.
-// by_mass: find the key where the running mass (descending) reaches target;
-// otherwise the key where the running count reaches target.  Returns the
-// fully resolved key; *acc = mass (or count) strictly above it; *kcnt =
-// number of elements holding exactly that key.
-template <int DT>
-__device__ __noinline__ uint32_t descend(K2Shared &sh, const K2Ctx &c, bool by_mass, double target, uint32_t floor_key,
-                            double *acc_out, uint32_t *kcnt)
+// Hide a register value from the optimiser so a per-element quantity is
+// recomputed in each pass instead of being kept live for all EPT elements.
+__device__ __forceinline__ float opaque(float v)
 {
+    asm volatile("" : "+v"(v));
+    return v;
+}
+
+// ------------------------------------------------------------------ cross-workgroup sync
+//
+// Release: every wave makes its own stores visible at agent scope (L2
+// write-back, wait for completion), then after the barrier one thread bumps
+// the counter.  Acquire: one thread observes the counter with an agent-scope
+// acquire load; every wave then invalidates its view before reading what
+// other workgroups wrote.
+
+__device__ __forceinline__ void fence_acquire() { __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent"); }
+__device__ __forceinline__ void fence_release() { __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent"); }
+
+__device__ __forceinline__ uint32_t ld_acq(const uint32_t *p)
+{
+    return __hip_atomic_load(p, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// one thread: wait until *p >= target; false on timeout
+__device__ bool spin_ge(const uint32_t *p, uint32_t target)
+{
+    for (uint32_t it = 0; it < SPIN_MAX; ++it) {
+        if (ld_acq(p) >= target) return true;
+        __builtin_amdgcn_s_sleep(1);
+    }
+    return false;
+}
+
+// Whole block: wait until *p >= target.  False on timeout (also recorded in
+// the control block).
+__device__ bool block_wait_ge(Smem &sm, const uint32_t *p, uint32_t target, Ctl *ctl)
+{
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const bool ok = spin_ge(p, target);
+        if (!ok) atomicOr(&ctl->error, 1u);
+        sm.bu[7] = ok ? 1u : 0u;
+    }
+    __syncthreads();
+    const bool ok = sm.bu[7] != 0u;
+    fence_acquire();
+    __syncthreads();
+    return ok;
+}
+
+// Whole block: publish the block's global writes, then add v to *p.  Returns
+// the old value to every thread.
+__device__ uint32_t block_release_add(Smem &sm, uint32_t *p, uint32_t v)
+{
+    fence_release();
+    __syncthreads();
+    if (threadIdx.x == 0) sm.bu[6] = atomicAdd(p, v);
+    __syncthreads();
+    const uint32_t old = sm.bu[6];
+    __syncthreads();
+    return old;
+}
+
+// raw-key interval for a scaled-key interval, computed by wave 0
+template <int DT> __device__ void x_interval(Smem &sm, uint32_t klo, uint32_t khi, float T, uint32_t *xlo, uint32_t *xhi)
+{
+    __syncthreads();
+    if (wave_id() == 0) {
+        const uint32_t a = x_lower<DT>(klo, T);
+        const uint32_t b = x_upper<DT>(khi, T);
+        if (lane_id() == 0) { sm.bu[4] = a; sm.bu[5] = b; }
+    }
+    __syncthreads();
+    *xlo = sm.bu[4];
+    *xhi = sm.bu[5];
+    __syncthreads();
+}
+
+__device__ void write_row(RowOut *ro, const Args &a, int row, int64_t id, int status, int mode, float m,
+                          uint32_t cut_key, int32_t cut_i, double S)
+{
+    if (threadIdx.x == 0) {
+        ro->id = status == MIS_ROW_OK ? id : -1;
+        ro->status = status;
+        ro->mode = mode;
+        ro->m = m;
+        ro->cut_key = cut_key;
+        ro->cut_i = cut_i;
+        ro->S = S;
+        a.out_ids[row] = status == MIS_ROW_OK ? id : -1;
+        if (a.out_status) a.out_status[row] = status;
+    }
+}
+
+// ------------------------------------------------------------------ draw helpers
+
+// Inverse CDF inside chunk g: the first kept index whose running weight (index
+// order) exceeds `resid`; wfun(x, j) gives the weight (0 = not kept).  When
+// rounding leaves `resid` out of reach, the chunk's last kept index.
+template <int DT, class WF>
+__device__ int64_t draw_in_chunk(Smem &sm, const RowCx &c, int g, double resid, WF &&wfun)
+{
+    const int64_t cbeg = (int64_t)g * c.CH;
+    const int64_t cend = cbeg + c.CH < c.V ? cbeg + c.CH : c.V;
+    const int64_t per = (c.CH + NT - 1) / NT;
+    const int64_t jb = cbeg + (int64_t)threadIdx.x * per;
+    const int64_t je = jb + per < cend ? jb + per : cend;
+    double local = 0.0;
+    int64_t lastk = -1;
+    for (int64_t j = jb; j < je; ++j) {
+        const double w = wfun(load1<DT>(c.rowp, j), j);
+        if (w > 0.0) { local += w; lastk = j; }
+    }
+    double tot;
+    const double before = block_excl_scan<double>(local, sm.red, &tot);
+    if (threadIdx.x == 0) sm.bq[0] = 0xffffffffffffffffull;
+    __syncthreads();
+    if (local > 0.0 && before <= resid && resid < before + local) {
+        double run = before;
+        int64_t pick = lastk;
+        for (int64_t j = jb; j < je; ++j) {
+            const double w = wfun(load1<DT>(c.rowp, j), j);
+            if (w > 0.0) {
+                run += w;
+                if (run > resid) { pick = j; break; }
+            }
+        }
+        atomicMin(&sm.bq[0], (unsigned long long)pick);
+    }
+    __syncthreads();
+    const unsigned long long pk = sm.bq[0];
+    __syncthreads();
+    if (pk != 0xffffffffffffffffull) return (int64_t)pk;
+    return block_max<int64_t>(lastk, sm.red);
+}
+
+// Chunk holding u * sum(sm.cw) and the residual weight inside it.
+__device__ void pick_chunk(Smem &sm, int G, float u, int *g_out, double *resid_out, double *S_out)
+{
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        double S = 0.0;
+        for (int g = 0; g < G; ++g) S += sm.cw[g];
+        double target = (double)u * S, cum = 0.0;
+        int gsel = -1;
+        for (int g = 0; g < G; ++g) {
+            if (sm.cw[g] > 0.0) {
+                if (cum + sm.cw[g] > target) { gsel = g; break; }
+                cum += sm.cw[g];
+            }
+        }
+        if (gsel < 0) {  // rounding: the last chunk with weight, its last kept element
+            for (int g = G - 1; g >= 0; --g) if (sm.cw[g] > 0.0) { gsel = g; break; }
+            cum = 0.0;
+            for (int g = 0; g < gsel; ++g) cum += sm.cw[g];
+            target = cum + (gsel >= 0 ? sm.cw[gsel] : 0.0);
+        }
+        sm.bd[0] = S;
+        sm.bd[1] = target - cum;
+        sm.bi[0] = gsel;
+    }
+    __syncthreads();
+    *S_out = sm.bd[0];
+    *resid_out = sm.bd[1];
+    *g_out = sm.bi[0];
+    __syncthreads();
+}
+
+// First index (ascending) of an LDS element list at which the running weight
+// exceeds `target`: radix over index space, 256 buckets per level.
+__device__ int64_t draw_in_list(Smem &sm, const int32_t *idx, const double *e, int n, int64_t V, double target)
+{
+    int64_t lo = 0, hi = V;
     double acc = 0.0;
+    while (hi - lo > 1) {
+        const int64_t width = (hi - lo + 255) / 256;
+        __syncthreads();
+        for (int i = threadIdx.x; i < 256; i += NT) sm.sub_m[i] = 0.0;
+        __syncthreads();
+        for (int i = threadIdx.x; i < n; i += NT) {
+            const int64_t j = idx[i];
+            if (j >= lo && j < hi && e[i] > 0.0) atomicAdd(&sm.sub_m[(j - lo) / width], e[i]);
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            double cum = acc;
+            int bsel = -1;
+            for (int b = 0; b < 256; ++b) {
+                if (sm.sub_m[b] > 0.0) {
+                    if (cum + sm.sub_m[b] > target) { bsel = b; break; }
+                    cum += sm.sub_m[b];
+                }
+            }
+            if (bsel < 0) {  // rounding: the last element with weight
+                for (int b = 255; b >= 0; --b) if (sm.sub_m[b] > 0.0) { bsel = b; break; }
+                cum = acc;
+                for (int b = 0; b < bsel; ++b) cum += sm.sub_m[b];
+                target = 1e300;
+            }
+            sm.bi[1] = bsel;
+            sm.bd[2] = cum;
+            sm.bd[3] = target;
+        }
+        __syncthreads();
+        const int b = sm.bi[1];
+        acc = sm.bd[2];
+        target = sm.bd[3];
+        __syncthreads();
+        if (b < 0) return -1;
+        lo = lo + (int64_t)b * width;
+        hi = lo + width < hi ? lo + width : hi;
+    }
+    return lo;
+}
+
+// Cut inside a candidate window held in LDS (key, idx, e): mass descent over
+// the keys to the running mass Aw (descending order, ties by index).
+__device__ void window_cut(Smem &sm, const uint32_t *key, const int32_t *idx, const double *e, uint32_t n,
+                           double Aw, double e_of_key_dummy, uint32_t *cut_key, int32_t *cut_i, int dt)
+{
+    (void)e_of_key_dummy;
     uint32_t prefix = 0u;
-    // level 1
+    double acc = 0.0;
+    uint32_t kc = 0;
+    double ekey = 0.0;
+    for (int lev = 0; lev < 4; ++lev) {
+        const int sh = 24 - 8 * lev;
+        const uint32_t hmask = lev == 0 ? 0u : ~((1u << (sh + 8)) - 1u);
+        __syncthreads();
+        for (int i = threadIdx.x; i < 256; i += NT) { sm.sub_m[i] = 0.0; sm.sub_c[i] = 0u; }
+        __syncthreads();
+        for (uint32_t i = threadIdx.x; i < n; i += NT) {
+            const uint32_t k = key[i];
+            if ((k & hmask) == (prefix & hmask)) {
+                atomicAdd(&sm.sub_m[(k >> sh) & 255u], e[i]);
+                atomicAdd(&sm.sub_c[(k >> sh) & 255u], 1u);
+            }
+        }
+        __syncthreads();
+        if (wave_id() == 0) {
+            double ab;
+            const int d = wave_find_desc<double>(sm.sub_m, 256, Aw - acc, &ab);
+            if (lane_id() == 0) { sm.bu[0] = (uint32_t)d; sm.bd[0] = ab; sm.bu[1] = sm.sub_c[d]; }
+        }
+        __syncthreads();
+        prefix |= sm.bu[0] << sh;
+        acc += sm.bd[0];
+        kc = sm.bu[1];
+        __syncthreads();
+    }
+    // the weight of one element holding the resolved key
+    if (threadIdx.x == 0) sm.bd[1] = 0.0;
+    __syncthreads();
+    for (uint32_t i = threadIdx.x; i < n; i += NT) if (key[i] == prefix) sm.bd[1] = e[i];
+    __syncthreads();
+    ekey = sm.bd[1];
+    __syncthreads();
+    double tt = ekey > 0.0 ? ceil((Aw - acc) / ekey) : 1.0;
+    if (!(tt >= 1.0)) tt = 1.0;
+    if (tt > (double)kc) tt = (double)kc;
+    uint32_t t = (uint32_t)tt;
+    while (t > 1 && acc + (double)(t - 1) * ekey >= Aw) --t;
+    while (t < kc && acc + (double)t * ekey < Aw) ++t;
+    *cut_key = prefix;
+    *cut_i = IDX_ALL;
+    if (t < kc) {  // the t-th smallest index among the elements holding the key
+        for (uint32_t i = threadIdx.x; i < n; i += NT) {
+            if (key[i] != prefix) continue;
+            const int32_t v = idx[i];
+            uint32_t r = 0;
+            for (uint32_t q = 0; q < n; ++q) r += (key[q] == prefix && idx[q] < v) ? 1u : 0u;
+            if (r == t - 1u) sm.bi[0] = v;
+        }
+        __syncthreads();
+        *cut_i = sm.bi[0];
+        __syncthreads();
+    }
+    (void)dt;
+}
+
+// ------------------------------------------------------------------ re-read path
+
+template <int DT, class F>
+__device__ __forceinline__ void rescan(const RowCx &c, uint32_t xklo, uint32_t xkhi, F &&f)
+{
+    if (xklo > xkhi) return;
+    scan_range<DT, 4>(c.rowp, 0, c.V, c.vec_ok, [&](int64_t j, float x) {
+        const uint32_t xk = key_of_f32(x);
+        if (xk >= xklo && xk <= xkhi) {
+            const float y = scale_y<DT>(x, c.T);
+            f(j, y, row_key(y, DT));
+        }
+    });
+}
+
+// Radix descent (8-bit digits) over row keys >= floor_key; level 1 from
+// sm.v.l1, later levels re-read the row.  by_mass: running mass (descending)
+// reaches target; else running count.  Returns the resolved key; *acc_out =
+// mass or count strictly above it; *kcnt = elements holding exactly it.
+template <int DT>
+__device__ __noinline__ uint32_t descend(Smem &sm, const RowCx &c, bool by_mass, double target, uint32_t floor_key,
+                                         double *acc_out, uint32_t *kcnt)
+{
     __syncthreads();
     if (wave_id() == 0) {
         int b;
-        if (by_mass) { double ab; b = wave_find_desc<double>(sh.l1m, 256, target, &ab); if (lane_id() == 0) sh.bd[0] = ab; }
-        else { uint32_t ab; b = wave_find_desc<uint32_t>(sh.l1c, 256, (uint32_t)target, &ab); if (lane_id() == 0) sh.bd[0] = (double)ab; }
-        if (lane_id() == 0) { sh.bu[0] = (uint32_t)b; sh.bu[1] = sh.l1c[b]; }
+        if (by_mass) { double ab; b = wave_find_desc<double>(sm.v.l1.mass, 256, target, &ab); if (lane_id() == 0) sm.bd[0] = ab; }
+        else { uint32_t ab; b = wave_find_desc<uint32_t>(sm.v.l1.cnt, 256, (uint32_t)target, &ab); if (lane_id() == 0) sm.bd[0] = (double)ab; }
+        if (lane_id() == 0) { sm.bu[0] = (uint32_t)b; sm.bu[1] = sm.v.l1.cnt[b]; }
     }
     __syncthreads();
-    prefix = sh.bu[0] << 24;
-    acc = sh.bd[0];
-    uint32_t bincnt = sh.bu[1];
-    const int nlev = DT == F32 ? 2 : 1;
+    uint32_t prefix = sm.bu[0] << 24;
+    double acc = sm.bd[0];
+    uint32_t bincnt = sm.bu[1];
+    const int nlev = DT == F32 ? 3 : 1;
+    const double md = (double)c.m;
     for (int lev = 0; lev < nlev; ++lev) {
-        const int bits = DT == F32 ? 12 : 8;
-        const int shift = DT == F32 ? (lev == 0 ? 12 : 0) : 16;
-        const int nb = 1 << bits;
-        const uint32_t freemask = (lev == 0) ? 0x00ffffffu : 0x00000fffu;
-        for (int i = threadIdx.x; i < nb; i += K2_THREADS) { sh.u.h.cnt[i] = 0u; sh.u.h.mass[i] = 0.0; }
+        const int shift = 16 - 8 * lev;
+        const uint32_t freemask = (1u << (shift + 8)) - 1u;
+        __syncthreads();
+        for (int i = threadIdx.x; i < 256; i += NT) { sm.u.h8.cnt[i] = 0u; sm.u.h8.mass[i] = 0.0; }
         uint32_t klo = prefix, khi = prefix | freemask;
         if (klo < floor_key) klo = floor_key;
         uint32_t xlo, xhi;
-        x_interval<DT>(sh, klo, khi, c.T, &xlo, &xhi);
-        const double m = (double)c.m;
+        x_interval<DT>(sm, klo, khi, c.T, &xlo, &xhi);
         rescan<DT>(c, xlo, xhi, [&](int64_t, float y, uint32_t key) {
             if (key < klo || key > khi) return;
-            const uint32_t b = (key >> shift) & (uint32_t)(nb - 1);
-            atomicAdd(&sh.u.h.cnt[b], 1u);
-            if (by_mass) atomicAdd(&sh.u.h.mass[b], exp((double)y - m));
+            const uint32_t b = (key >> shift) & 255u;
+            atomicAdd(&sm.u.h8.cnt[b], 1u);
+            if (by_mass) atomicAdd(&sm.u.h8.mass[b], exp((double)y - md));
         });
         __syncthreads();
         if (wave_id() == 0) {
             int b;
-            if (by_mass) { double ab; b = wave_find_desc<double>(sh.u.h.mass, nb, target - acc, &ab); if (lane_id() == 0) sh.bd[0] = ab; }
-            else { uint32_t ab; b = wave_find_desc<uint32_t>(sh.u.h.cnt, nb, (uint32_t)(target - acc), &ab); if (lane_id() == 0) sh.bd[0] = (double)ab; }
-            if (lane_id() == 0) { sh.bu[0] = (uint32_t)b; sh.bu[1] = sh.u.h.cnt[b]; }
+            if (by_mass) { double ab; b = wave_find_desc<double>(sm.u.h8.mass, 256, target - acc, &ab); if (lane_id() == 0) sm.bd[0] = ab; }
+            else { uint32_t ab; b = wave_find_desc<uint32_t>(sm.u.h8.cnt, 256, (uint32_t)(target - acc), &ab); if (lane_id() == 0) sm.bd[0] = (double)ab; }
+            if (lane_id() == 0) { sm.bu[0] = (uint32_t)b; sm.bu[1] = sm.u.h8.cnt[b]; }
         }
         __syncthreads();
-        prefix |= sh.bu[0] << shift;
-        acc += sh.bd[0];
-        bincnt = sh.bu[1];
+        prefix |= sm.bu[0] << shift;
+        acc += sm.bd[0];
+        bincnt = sm.bu[1];
         __syncthreads();
     }
     *acc_out = acc;
@@ -674,61 +602,56 @@ __device__ __noinline__ uint32_t descend(K2Shared &sh, const K2Ctx &c, bool by_m
     return prefix;
 }
 
-// Index of the t-th (1-based) element, in index order, whose scaled key is
-// exactly `key`.
+// Index of the t-th (1-based) element in index order whose scaled key is `key`.
 template <int DT>
-__device__ __noinline__ int32_t tie_index(K2Shared &sh, const K2Ctx &c, uint32_t key, uint32_t t)
+__device__ __noinline__ int32_t tie_index(Smem &sm, const RowCx &c, uint32_t key, uint32_t t)
 {
     uint32_t xlo, xhi;
-    x_interval<DT>(sh, key, key, c.T, &xlo, &xhi);
-    if (threadIdx.x == 0) sh.bu[2] = 0u;
+    x_interval<DT>(sm, key, key, c.T, &xlo, &xhi);
+    if (threadIdx.x == 0) sm.bu[2] = 0u;
     __syncthreads();
     rescan<DT>(c, xlo, xhi, [&](int64_t j, float, uint32_t k) {
         if (k != key) return;
-        uint32_t p = atomicAdd(&sh.bu[2], 1u);
-        if (p < (uint32_t)TIE_CAP) sh.u.t.idx[p] = (int32_t)j;
+        const uint32_t p = atomicAdd(&sm.bu[2], 1u);
+        if (p < (uint32_t)TIE_CAP) sm.u.t.idx[p] = (int32_t)j;
     });
     __syncthreads();
-    const uint32_t n = sh.bu[2];
+    const uint32_t n = sm.bu[2];
     if (n <= (uint32_t)TIE_CAP) {
-        // rank of each collected index; the one with rank t-1 is the answer
-        for (uint32_t i = threadIdx.x; i < n; i += K2_THREADS) {
-            const int32_t v = sh.u.t.idx[i];
+        for (uint32_t i = threadIdx.x; i < n; i += NT) {
+            const int32_t v = sm.u.t.idx[i];
             uint32_t r = 0;
-            for (uint32_t q = 0; q < n; ++q) r += sh.u.t.idx[q] < v ? 1u : 0u;
-            if (r == t - 1u) sh.bi[0] = v;
+            for (uint32_t q = 0; q < n; ++q) r += sm.u.t.idx[q] < v ? 1u : 0u;
+            if (r == t - 1u) sm.bi[0] = v;
         }
         __syncthreads();
-        int32_t res = sh.bi[0];
+        const int32_t res = sm.bi[0];
         __syncthreads();
         return res;
     }
-    // many ties: bisect on the index with counting passes
-    int64_t lo = 0, hi = c.V - 1;  // find smallest idx with count(ties <= idx) >= t
+    int64_t lo = 0, hi = c.V - 1;  // many ties: bisect on the index with counting passes
     while (lo < hi) {
         const int64_t mid = lo + (hi - lo) / 2;
-        if (threadIdx.x == 0) sh.bu[3] = 0u;
-        __syncthreads();
         uint32_t mine = 0;
         rescan<DT>(c, xlo, xhi, [&](int64_t j, float, uint32_t k) { if (k == key && j <= mid) mine++; });
-        mine = block_sum<K2_THREADS>(mine, sh.red_u);
+        mine = block_sum<uint32_t>(mine, sm.red);
         if (mine >= t) hi = mid; else lo = mid + 1;
     }
     return (int32_t)lo;
 }
 
-// Sequential walk of the 16-bit top-p chain over runs (one thread).  On
-// return *found says whether some rank triggered removal; then the cut keeps
-// `*t_keep` elements of run *run_at (0 means the cut is the previous run).
-__device__ bool chain_walk(const uint32_t *rkey, const uint32_t *rcnt, const float *rp, int nruns, float &F,
-                           float thr16, int dt, int *run_at, uint32_t *t_keep)
+// Sequential walk of the 16-bit top-p chain over runs (one thread).  Returns
+// true when some rank triggers removal; the cut then keeps *t_keep elements of
+// run *run_at (0 = the cut is the previous run).
+__device__ bool chain_walk(const uint32_t *rcnt, const float *rp, int nruns, float &F, float thr16, int dt,
+                           int *run_at, uint32_t *t_keep)
 {
     for (int r = 0; r < nruns; ++r) {
         const float p = rp[r];
         const uint32_t n = rcnt[r];
         const float Fend = chain_add_n(F, p, n);
         if (chain_E(Fend, p, dt) >= thr16) {
-            uint32_t lo = 0, hi = n - 1;  // first t in [0, n) whose E triggers
+            uint32_t lo = 0, hi = n - 1;
             while (lo < hi) {
                 const uint32_t mid = lo + (hi - lo) / 2;
                 if (chain_E(chain_add_n(F, p, (uint64_t)mid + 1), p, dt) >= thr16) hi = mid; else lo = mid + 1;
@@ -742,485 +665,68 @@ __device__ bool chain_walk(const uint32_t *rkey, const uint32_t *rcnt, const flo
     return false;
 }
 
-// Per-chunk kept weight for the draw, then the inverse-CDF pick inside the
-// chosen chunk.  sh.cw[c] must hold the kept weight of chunk c.
+// Top-p cut over elements with key >= floor_key; sm.v.l1 holds their 256-bin
+// histogram and S their total weight.
 template <int DT>
-__device__ __noinline__ int64_t draw_from_chunks(K2Shared &sh, const K2Ctx &c, float u, uint32_t cut_key, int32_t cut_i, double *S_out)
-{
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        double S = 0.0;
-        for (int g = 0; g < c.G; ++g) S += sh.cw[g];
-        double target = (double)u * S;
-        double cum = 0.0;
-        int gsel = -1;
-        for (int g = 0; g < c.G; ++g) {
-            if (sh.cw[g] > 0.0) {
-                if (cum + sh.cw[g] > target) { gsel = g; break; }
-                cum += sh.cw[g];
-            }
-        }
-        if (gsel < 0) {  // rounding: last chunk with weight
-            for (int g = c.G - 1; g >= 0; --g) if (sh.cw[g] > 0.0) { gsel = g; break; }
-            cum = 0.0;
-            for (int g = 0; g < gsel; ++g) cum += sh.cw[g];
-            target = cum + sh.cw[gsel];  // pick the last kept element of that chunk
-        }
-        sh.bd[0] = S;
-        sh.bd[1] = target - cum;
-        sh.bi[0] = gsel;
-    }
-    __syncthreads();
-    const double S = sh.bd[0], resid = sh.bd[1];
-    const int g = sh.bi[0];
-    *S_out = S;
-    if (g < 0) return -1;
-    // scan chunk g in index order: thread t owns a contiguous slice
-    const int64_t cbeg = (int64_t)g * c.CH;
-    const int64_t cend = cbeg + c.CH < c.V ? cbeg + c.CH : c.V;
-    const int64_t per = (c.CH + K2_THREADS - 1) / K2_THREADS;
-    const int64_t jb = cbeg + (int64_t)threadIdx.x * per;
-    const int64_t je = jb + per < cend ? jb + per : cend;
-    const double m = (double)c.m;
-    double local = 0.0;
-    int64_t lastk = -1;
-    for (int64_t j = jb; j < je; ++j) {
-        const float y = scale_y<DT>(load1<DT>(c.rowp, j), c.T);
-        const uint32_t key = row_key(y, DT);
-        if (y != -INFINITY && kept_by_cut(key, j, cut_key, cut_i)) { local += exp((double)y - m); lastk = j; }
-    }
-    double tot;
-    const double before = block_excl_scan<K2_THREADS>(local, sh.red_d, &tot);
-    if (threadIdx.x == 0) { sh.red_q[0] = 0xffffffffffffffffull; }
-    __syncthreads();
-    if (local > 0.0 && before <= resid && resid < before + local) {
-        double run = before;
-        int64_t pick = lastk;
-        for (int64_t j = jb; j < je; ++j) {
-            const float y = scale_y<DT>(load1<DT>(c.rowp, j), c.T);
-            const uint32_t key = row_key(y, DT);
-            if (y != -INFINITY && kept_by_cut(key, j, cut_key, cut_i)) {
-                run += exp((double)y - m);
-                if (run > resid) { pick = j; break; }
-            }
-        }
-        atomicMin((unsigned long long *)&sh.red_q[0], (unsigned long long)pick);
-    }
-    __syncthreads();
-    uint64_t pk = sh.red_q[0];
-    if (pk == 0xffffffffffffffffull) {
-        // residual beyond the recomputed total: last kept element of the chunk
-        int64_t lk = block_max<K2_THREADS>((int64_t)lastk, sh.red_l);
-        return lk;
-    }
-    __syncthreads();
-    return (int64_t)pk;
-}
-
-// Bitonic sort (descending) of n_pow2 uint64 keys in LDS by the whole block.
-__device__ void bitonic_desc(uint64_t *a, int n)
-{
-    for (int k = 2; k <= n; k <<= 1) {
-        for (int j = k >> 1; j > 0; j >>= 1) {
-            for (int i = threadIdx.x; i < n; i += K2_THREADS) {
-                const int ixj = i ^ j;
-                if (ixj > i) {
-                    const bool desc = (i & k) == 0;
-                    const uint64_t x = a[i], y = a[ixj];
-                    if (desc ? (x < y) : (x > y)) { a[i] = y; a[ixj] = x; }
-                }
-            }
-            __syncthreads();
-        }
-    }
-}
-
-template <int DT>
-__device__ void write_row(RowOut *ro, int64_t *out_ids, int32_t *out_status, int row, int64_t id, int status, int mode,
-                          float m, uint32_t cut_key, int32_t cut_i, double S)
-{
-    if (threadIdx.x == 0) {
-        ro->id = status == MIS_ROW_OK ? id : -1;
-        ro->status = status;
-        ro->mode = mode;
-        ro->m = m;
-        ro->cut_key = cut_key;
-        ro->cut_i = cut_i;
-        ro->S = S;
-        out_ids[row] = status == MIS_ROW_OK ? id : -1;
-        if (out_status) out_status[row] = status;
-    }
-}
-
-// generic full-row path: top-k by count descent (k' may be any size) and/or
-// top-p, with every histogram level re-read from the row.
-template <int DT>
-__device__ __noinline__ void final_generic(K2Shared &sh, K2Ctx &c, const RowPlan &pl, bool have_l1, RowOut *ro,
-                              int64_t *out_ids, int32_t *out_status, int row, const uint32_t *gl1c, const double *gl1m);
-
-template <int DT>
-__device__ __noinline__ void topp_cut(K2Shared &sh, const K2Ctx &c, const RowPlan &pl, uint32_t floor_key, double S,
-                         uint32_t *cut_key, int32_t *cut_i, int *status);
-
-template <int DT>
-__global__ __launch_bounds__(K2_THREADS) void k_final(const char *__restrict__ logits, int64_t V, int64_t stride_bytes,
-                                                      int vec_ok, const mis_row_params *__restrict__ params, Layout L,
-                                                      char *__restrict__ ws, int64_t *__restrict__ out_ids,
-                                                      int32_t *__restrict__ out_status)
-{
-    __shared__ K2Shared sh;
-    const int row = blockIdx.x;
-    const RowPlan pl = plan_row(params[row], V);
-    RowOut *ro = reinterpret_cast<RowOut *>(ws + L.rowout) + row;
-    const ChunkSum *cs = reinterpret_cast<const ChunkSum *>(ws + L.chunks) + (size_t)row * L.G;
-    const uint32_t kneg = row_key(-INFINITY, DT);
-
-    if (pl.mode == M_BAD) {
-        write_row<DT>(ro, out_ids, out_status, row, -1, MIS_ROW_BAD_PARAM, pl.mode, 0.f, 0u, 0, 0.0);
-        return;
-    }
-    // ---- merge chunk summaries
-    uint32_t bk = 0u; int32_t bi = IDX_ALL; uint32_t fl = 0u; float ym = -INFINITY;
-    for (int g = threadIdx.x; g < L.G; g += K2_THREADS) {
-        const ChunkSum s = cs[g];
-        if (s.xkey > bk || (s.xkey == bk && s.xarg < bi)) { bk = s.xkey; bi = s.xarg; }
-        fl |= s.flags;
-        ym = s.ymax > ym ? s.ymax : ym;
-    }
-    wave_argmax(bk, bi);
-    if (lane_id() == 0) { sh.red_u[wave_id()] = bk; sh.red_i[wave_id()] = bi; }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        for (int w = 1; w < K2_WAVES; ++w)
-            if (sh.red_u[w] > bk || (sh.red_u[w] == bk && sh.red_i[w] < bi)) { bk = sh.red_u[w]; bi = sh.red_i[w]; }
-        sh.bu[0] = bk; sh.bi[0] = bi;
-    }
-    __syncthreads();
-    bk = sh.bu[0]; bi = sh.bi[0];
-    __syncthreads();
-    if (pl.mode == M_GREEDY) {
-        write_row<DT>(ro, out_ids, out_status, row, bi, MIS_ROW_OK, pl.mode, 0.f, 0u, bi, 1.0);
-        return;
-    }
-    fl = block_sum<K2_THREADS>(fl ? 1u : 0u, sh.red_u);  // chunks carrying NaN / +inf
-    const float m = block_max<K2_THREADS>(ym, sh.red_f);
-    if (fl != 0u || m == -INFINITY || !(m == m)) {
-        write_row<DT>(ro, out_ids, out_status, row, -1, MIS_ROW_INVALID, pl.mode, m, 0u, 0, 0.0);
-        return;
-    }
-
-    K2Ctx c;
-    c.rowp = logits + (int64_t)row * stride_bytes;
-    c.V = V; c.vec_ok = vec_ok; c.T = pl.T; c.m = m; c.G = L.G; c.ept = L.ept;
-    c.CH = (int64_t)K1_THREADS * L.ept;
-    const double md = (double)m;
-    for (int g = threadIdx.x; g < L.G; g += K2_THREADS) sh.chs[g] = exp((double)cs[g].ymax - md);
-    __syncthreads();
-
-    if (pl.mode == M_TEMP) {
-        for (int g = threadIdx.x; g < L.G; g += K2_THREADS) sh.cw[g] = cs[g].ymax == -INFINITY ? 0.0 : cs[g].S * sh.chs[g];
-        double S;
-        int64_t id = draw_from_chunks<DT>(sh, c, pl.u, kneg, -1, &S);
-        write_row<DT>(ro, out_ids, out_status, row, id, id >= 0 ? MIS_ROW_OK : MIS_ROW_INVALID, pl.mode, m, kneg, -1, S);
-        return;
-    }
-
-    const uint32_t *gl1c = reinterpret_cast<const uint32_t *>(ws + L.l1cnt) + (size_t)row * L.G * 256;
-    const double *gl1m = reinterpret_cast<const double *>(ws + L.l1mass) + (size_t)row * L.G * 256;
-
-    if (pl.mode == M_SMALLK) {
-        // ---- candidate path
-        uint32_t ncand_tot = 0, ovf = 0;
-        for (int g = threadIdx.x; g < L.G; g += K2_THREADS) {
-            const uint32_t n = cs[g].ncand;
-            if (n == NCAND_OVERFLOW) ovf = 1; else ncand_tot += n;
-        }
-        ovf = block_sum<K2_THREADS>(ovf, sh.red_u);
-        ncand_tot = block_sum<K2_THREADS>(ncand_tot, sh.red_u);
-        if (ovf == 0) {
-            const Cand *cand = reinterpret_cast<const Cand *>(ws + L.cand) + (size_t)row * L.G * CAND_CAP;
-            // k'-th largest key among the candidates
-            // fewer than k' candidates means fewer than k' finite elements in
-            // the row: every finite element survives
-            uint32_t thr = kneg + 1u;
-            if (ncand_tot >= (uint32_t)pl.kk) {
-                uint32_t prefix = 0u, rem = (uint32_t)pl.kk;
-                const int nlev = DT == F32 ? 4 : 2;
-                for (int lev = 0; lev < nlev; ++lev) {
-                    const int shift = 24 - 8 * lev;
-                    for (int i = threadIdx.x; i < 256; i += K2_THREADS) sh.u.h.cnt[i] = 0u;
-                    __syncthreads();
-                    for (int g = 0; g < L.G; ++g) {
-                        const uint32_t n = cs[g].ncand;
-                        for (uint32_t i = threadIdx.x; i < n; i += K2_THREADS) {
-                            const uint32_t k = cand[(size_t)g * CAND_CAP + i].key;
-                            if (lev == 0 || (k >> (shift + 8)) == (prefix >> (shift + 8))) atomicAdd(&sh.u.h.cnt[(k >> shift) & 255u], 1u);
-                        }
-                    }
-                    __syncthreads();
-                    if (wave_id() == 0) {
-                        uint32_t above;
-                        int d = wave_find_desc<uint32_t>(sh.u.h.cnt, 256, rem, &above);
-                        if (lane_id() == 0) { sh.bu[0] = (uint32_t)d; sh.bu[1] = above; sh.bu[2] = sh.u.h.cnt[d]; }
-                    }
-                    __syncthreads();
-                    rem -= sh.bu[1];
-                    prefix |= sh.bu[0] << shift;
-                    __syncthreads();
-                    // no early exit here: the threshold is applied to the whole
-                    // row, so it must be the exact k'-th key
-                }
-                thr = prefix;
-            }
-            // survivors into LDS
-            if (threadIdx.x == 0) sh.bu[3] = 0u;
-            __syncthreads();
-            for (int g = 0; g < L.G; ++g) {
-                const uint32_t n = cs[g].ncand;
-                for (uint32_t i = threadIdx.x; i < n; i += K2_THREADS) {
-                    const Cand cd = cand[(size_t)g * CAND_CAP + i];
-                    if (cd.key >= thr) {
-                        const uint32_t p = atomicAdd(&sh.bu[3], 1u);
-                        if (p < (uint32_t)SURV_CAP)
-                            sh.u.s.sk[p] = ((uint64_t)cd.key << 32) | (uint64_t)(0xffffffffu - (uint32_t)cd.idx);
-                    }
-                }
-            }
-            __syncthreads();
-            const uint32_t ns = sh.bu[3];
-            __syncthreads();
-            if (ns <= (uint32_t)SURV_CAP && ns > 0) {
-                int npow = 1;
-                while (npow < (int)ns) npow <<= 1;
-                for (int i = threadIdx.x; i < npow; i += K2_THREADS) if (i >= (int)ns) sh.u.s.sk[i] = 0ull;
-                __syncthreads();
-                bitonic_desc(sh.u.s.sk, npow);  // key desc, idx asc
-                for (int i = threadIdx.x; i < (int)ns; i += K2_THREADS)
-                    sh.u.s.e[i] = exp((double)value_of_row_key((uint32_t)(sh.u.s.sk[i] >> 32), DT) - md);
-                __syncthreads();
-                uint32_t nkeep = ns;
-                int status = MIS_ROW_OK;
-                if (pl.topp) {
-                    if (DT == F32) {
-                        // exclusive prefix of the masses in sorted order
-                        double Stot = 0.0;
-                        for (int i0 = 0; i0 < (int)ns; i0 += K2_THREADS) {
-                            const int i = i0 + threadIdx.x;
-                            double v = i < (int)ns ? sh.u.s.e[i] : 0.0, tot;
-                            double ex = block_excl_scan<K2_THREADS>(v, sh.red_d, &tot);
-                            if (i < (int)ns) sh.u.s.sk2[i] = f64_bits(Stot + ex);
-                            Stot += tot;
-                        }
-                        __syncthreads();
-                        const double A = (double)pl.top_p * Stot;
-                        uint32_t first = ns;
-                        for (int i = threadIdx.x; i < (int)ns; i += K2_THREADS)
-                            if (bits_f64(sh.u.s.sk2[i]) >= A) first = first < (uint32_t)i ? first : (uint32_t)i;
-                        first = block_min<K2_THREADS>(first, sh.red_u);
-                        nkeep = first;
-                    } else {
-                        // 16-bit chain over runs of equal keys (sorted survivors)
-                        if (threadIdx.x == 0) {
-                            const float thr16 = rn_dtype(pl.top_p, DT);
-                            double Stot = 0.0;
-                            for (int i = (int)ns - 1; i >= 0; --i) Stot += sh.u.s.e[i];
-                            float F = 0.0f;
-                            uint32_t r0 = ns;
-                            int i = 0;
-                            while (i < (int)ns) {
-                                const uint32_t key = (uint32_t)(sh.u.s.sk[i] >> 32);
-                                int jn = i + 1;
-                                while (jn < (int)ns && (uint32_t)(sh.u.s.sk[jn] >> 32) == key) ++jn;
-                                const float p = rn_dtype((float)(sh.u.s.e[i] / Stot), DT);
-                                const uint32_t n = (uint32_t)(jn - i);
-                                const float Fend = chain_add_n(F, p, n);
-                                if (chain_E(Fend, p, DT) >= thr16) {
-                                    uint32_t lo = 0, hi = n - 1;
-                                    while (lo < hi) {
-                                        const uint32_t mid = lo + (hi - lo) / 2;
-                                        if (chain_E(chain_add_n(F, p, (uint64_t)mid + 1), p, DT) >= thr16) hi = mid; else lo = mid + 1;
-                                    }
-                                    r0 = (uint32_t)i + lo;
-                                    break;
-                                }
-                                F = Fend;
-                                i = jn;
-                            }
-                            sh.bu[4] = r0;
-                        }
-                        __syncthreads();
-                        nkeep = sh.bu[4];
-                        __syncthreads();
-                    }
-                    if (nkeep == 0) status = MIS_ROW_INVALID;
-                }
-                if (status == MIS_ROW_OK) {
-                    uint32_t cut_key;
-                    int32_t cut_i;
-                    if (pl.topp) {
-                        const uint64_t q = sh.u.s.sk[nkeep - 1];
-                        cut_key = (uint32_t)(q >> 32);
-                        cut_i = (int32_t)(0xffffffffu - (uint32_t)q);
-                    } else {
-                        cut_key = thr; cut_i = IDX_ALL;
-                    }
-                    // kept set in index order: sk2 = idx << 32 | slot (ascending)
-                    int npw = 1;
-                    while (npw < (int)nkeep) npw <<= 1;
-                    for (int i = threadIdx.x; i < npw; i += K2_THREADS) {
-                        uint64_t v;
-                        if (i < (int)nkeep) v = ((uint64_t)(0xffffffffu - (uint32_t)sh.u.s.sk[i]) << 32) | (uint64_t)i;
-                        else v = 0xffffffffffffffffull;
-                        sh.u.s.sk2[i] = ~v;  // sort descending on complement = ascending on v
-                    }
-                    __syncthreads();
-                    bitonic_desc(sh.u.s.sk2, npw);
-                    double SK = 0.0;
-                    for (int i0 = 0; i0 < (int)nkeep; i0 += K2_THREADS) {
-                        const int i = i0 + threadIdx.x;
-                        double v = 0.0;
-                        if (i < (int)nkeep) v = sh.u.s.e[(uint32_t)(~sh.u.s.sk2[i])];
-                        double tot;
-                        (void)block_excl_scan<K2_THREADS>(v, sh.red_d, &tot);
-                        SK += tot;
-                    }
-                    const double target = (double)pl.u * SK;
-                    double run = 0.0;
-                    int64_t pick = -1;
-                    if (threadIdx.x == 0) {
-                        for (int i = 0; i < (int)nkeep; ++i) {
-                            const uint64_t v = ~sh.u.s.sk2[i];
-                            const uint32_t slot = (uint32_t)v;
-                            run += sh.u.s.e[slot];
-                            pick = (int64_t)(v >> 32);
-                            if (run > target) break;
-                        }
-                        sh.bd[2] = (double)pick;
-                    }
-                    __syncthreads();
-                    pick = (int64_t)sh.bd[2];
-                    write_row<DT>(ro, out_ids, out_status, row, pick, MIS_ROW_OK, pl.mode, m, cut_key, cut_i, SK);
-                } else {
-                    write_row<DT>(ro, out_ids, out_status, row, -1, status, pl.mode, m, 0u, 0, 0.0);
-                }
-                return;
-            }
-        }
-        // overflow: fall through to the generic path
-        final_generic<DT>(sh, c, pl, false, ro, out_ids, out_status, row, gl1c, gl1m);
-        return;
-    }
-
-    if (pl.mode == M_LARGEK) {
-        final_generic<DT>(sh, c, pl, true, ro, out_ids, out_status, row, gl1c, gl1m);
-        return;
-    }
-
-    // ---- M_TOPP with chunk histograms
-    for (int b = threadIdx.x; b < 256; b += K2_THREADS) {
-        double mm = 0.0; uint32_t cc = 0;
-        for (int g = 0; g < L.G; ++g) { mm += gl1m[(size_t)g * 256 + b] * sh.chs[g]; cc += gl1c[(size_t)g * 256 + b]; }
-        sh.l1m[b] = mm; sh.l1c[b] = cc;
-    }
-    double S = 0.0;
-    for (int g = threadIdx.x; g < L.G; g += K2_THREADS) S += cs[g].ymax == -INFINITY ? 0.0 : cs[g].S * sh.chs[g];
-    S = block_sum<K2_THREADS>(S, sh.red_d);
-    uint32_t cut_key; int32_t cut_i; int status;
-    topp_cut<DT>(sh, c, pl, 0u, S, &cut_key, &cut_i, &status);
-    if (status != MIS_ROW_OK) {
-        write_row<DT>(ro, out_ids, out_status, row, -1, status, pl.mode, m, 0u, 0, 0.0);
-        return;
-    }
-    // per-chunk kept weight: whole L1 bins above the cut's bin from the chunk
-    // histograms, the cut's bin from one filtered re-read
-    const uint32_t cb = cut_key >> 24;
-    for (int g = threadIdx.x; g < L.G; g += K2_THREADS) {
-        double w = 0.0;
-        for (int b = cb + 1; b < 256; ++b) w += gl1m[(size_t)g * 256 + b];
-        sh.cw[g] = w * sh.chs[g];
-    }
-    __syncthreads();
-    {
-        uint32_t xlo, xhi;
-        x_interval<DT>(sh, cut_key, (cb << 24) | 0x00ffffffu, c.T, &xlo, &xhi);
-        rescan<DT>(c, xlo, xhi, [&](int64_t j, float y, uint32_t key) {
-            if ((key >> 24) != cb) return;
-            if (kept_by_cut(key, j, cut_key, cut_i)) atomicAdd(&sh.cw[j / c.CH], exp((double)y - md));
-        });
-    }
-    double SK;
-    int64_t id = draw_from_chunks<DT>(sh, c, pl.u, cut_key, cut_i, &SK);
-    write_row<DT>(ro, out_ids, out_status, row, id, id >= 0 ? MIS_ROW_OK : MIS_ROW_INVALID, pl.mode, m, cut_key, cut_i, SK);
-}
-
-// Top-p cut over elements with key >= floor_key.  sh.l1m / sh.l1c must hold
-// the 256-bin histogram of exactly those elements, S their total weight.
-template <int DT>
-__device__ __noinline__ void topp_cut(K2Shared &sh, const K2Ctx &c, const RowPlan &pl, uint32_t floor_key, double S,
-                         uint32_t *cut_key, int32_t *cut_i, int *status)
+__device__ __noinline__ void topp_cut_generic(Smem &sm, const RowCx &c, float top_p, uint32_t floor_key, double S,
+                                              uint32_t *cut_key, int32_t *cut_i, int *status)
 {
     const double md = (double)c.m;
     *status = MIS_ROW_OK;
     if (DT == F32) {
-        const double A = (double)pl.top_p * S;
+        const double A = (double)top_p * S;
         double acc;
         uint32_t kc;
-        const uint32_t key = descend<DT>(sh, c, true, A, floor_key, &acc, &kc);
+        const uint32_t key = descend<DT>(sm, c, true, A, floor_key, &acc, &kc);
         const double e = exp((double)value_of_row_key(key, DT) - md);
-        // ties kept: smallest t >= 1 with acc + t*e >= A
-        uint32_t t;
-        {
-            double tt = ceil((A - acc) / e);
-            if (!(tt >= 1.0)) tt = 1.0;
-            if (tt > (double)kc) tt = (double)kc;
-            t = (uint32_t)tt;
-            while (t > 1 && acc + (double)(t - 1) * e >= A) --t;
-            while (t < kc && acc + (double)t * e < A) ++t;
-        }
+        double tt = ceil((A - acc) / e);
+        if (!(tt >= 1.0)) tt = 1.0;
+        if (tt > (double)kc) tt = (double)kc;
+        uint32_t t = (uint32_t)tt;
+        while (t > 1 && acc + (double)(t - 1) * e >= A) --t;
+        while (t < kc && acc + (double)t * e < A) ++t;
         *cut_key = key;
-        *cut_i = (t >= kc) ? IDX_ALL : tie_index<DT>(sh, c, key, t);
+        *cut_i = (t >= kc) ? IDX_ALL : tie_index<DT>(sm, c, key, t);
         return;
     }
-    // 16-bit: walk the rounding chain over runs of equal keys, region by region
-    const float thr16 = rn_dtype(pl.top_p, DT);
+    const float thr16 = rn_dtype(top_p, DT);
     const uint32_t kneg = row_key(-INFINITY, DT);
     float F = 0.0f;
     int b_hi = 255;
-    while (b_hi >= 0 && sh.l1c[b_hi] == 0u) --b_hi;
+    while (b_hi >= 0 && sm.v.l1.cnt[b_hi] == 0u) --b_hi;
     uint32_t prev_key = 0u;
     bool have_prev = false;
     while (b_hi >= 0) {
-        // region: up to REGION_BINS L1 bins from b_hi down
         int b_lo = b_hi - REGION_BINS + 1;
         if (b_lo < 0) b_lo = 0;
-        for (int i = threadIdx.x; i < RUN_CAP; i += K2_THREADS) sh.u.r.cnt[i] = 0u;
-        uint32_t klo = (uint32_t)b_lo << 24, khi = ((uint32_t)b_hi << 24) | 0x00ffffffu;
+        __syncthreads();
+        for (int i = threadIdx.x; i < RUN_CAP; i += NT) sm.u.r.cnt[i] = 0u;
+        uint32_t klo = (uint32_t)b_lo << 24;
+        const uint32_t khi = ((uint32_t)b_hi << 24) | 0x00ffffffu;
         if (klo < floor_key) klo = floor_key;
-        if (klo <= kneg) klo = kneg + 1u;  // -inf never enters the chain
+        if (klo <= kneg) klo = kneg + 1u;
         uint32_t xlo, xhi;
-        x_interval<DT>(sh, klo, khi, c.T, &xlo, &xhi);
+        x_interval<DT>(sm, klo, khi, c.T, &xlo, &xhi);
         rescan<DT>(c, xlo, xhi, [&](int64_t, float, uint32_t key) {
             if (key < klo || key > khi) return;
-            // descending position: (b_hi - L1) * 256 + (255 - byte2)
             const uint32_t pos = (uint32_t)(b_hi - (int)(key >> 24)) * 256u + (255u - ((key >> 16) & 255u));
-            atomicAdd(&sh.u.r.cnt[pos], 1u);
+            atomicAdd(&sm.u.r.cnt[pos], 1u);
         });
         __syncthreads();
-        // compact non-empty positions into runs (descending keys)
         const int npos = (b_hi - b_lo + 1) * 256;
         int nruns_total = 0;
-        for (int i0 = 0; i0 < npos; i0 += K2_THREADS) {
+        for (int i0 = 0; i0 < npos; i0 += NT) {
             const int i = i0 + threadIdx.x;
-            const uint32_t cnt = i < npos ? sh.u.r.cnt[i] : 0u;
+            const uint32_t cnt = i < npos ? sm.u.r.cnt[i] : 0u;
             uint32_t tot;
-            const uint32_t off = block_excl_scan<K2_THREADS>(cnt ? 1u : 0u, sh.red_u, &tot);
+            const uint32_t off = block_excl_scan<uint32_t>(cnt ? 1u : 0u, sm.red, &tot);
             if (cnt) {
                 const uint32_t L1 = (uint32_t)(b_hi - i / 256), b2 = 255u - (uint32_t)(i % 256);
                 const uint32_t key = (L1 << 24) | (b2 << 16);
                 const int r = nruns_total + (int)off;
-                sh.u.r.rkey[r] = key;
-                sh.u.r.rcnt[r] = cnt;
-                sh.u.r.rp[r] = rn_dtype((float)(exp((double)value_of_row_key(key, DT) - md) / S), DT);
+                sm.u.r.rkey[r] = key;
+                sm.u.r.rcnt[r] = cnt;
+                sm.u.r.rp[r] = rn_dtype((float)(exp((double)value_of_row_key(key, DT) - md) / S), DT);
             }
             nruns_total += (int)tot;
         }
@@ -1229,30 +735,27 @@ __device__ __noinline__ void topp_cut(K2Shared &sh, const K2Ctx &c, const RowPla
             int run_at = -1;
             uint32_t tk = 0;
             float Fw = F;
-            bool found = chain_walk(sh.u.r.rkey, sh.u.r.rcnt, sh.u.r.rp, nruns_total, Fw, thr16, DT, &run_at, &tk);
-            sh.bi[1] = found ? 1 : 0;
-            sh.bi[2] = run_at;
-            sh.bu[4] = tk;
-            sh.bf[0] = Fw;
-            sh.bu[5] = nruns_total > 0 ? sh.u.r.rkey[nruns_total - 1] : 0u;
+            const bool found = chain_walk(sm.u.r.rcnt, sm.u.r.rp, nruns_total, Fw, thr16, DT, &run_at, &tk);
+            sm.bi[1] = found ? 1 : 0;
+            sm.bu[0] = tk;
+            sm.bf[0] = Fw;
+            sm.bu[1] = nruns_total > 0 ? sm.u.r.rkey[nruns_total - 1] : 0u;
             if (found) {
-                sh.bu[6] = sh.u.r.rkey[run_at];
-                sh.bu[7] = sh.u.r.rcnt[run_at];
-                sh.bu[2] = run_at > 0 ? sh.u.r.rkey[run_at - 1] : 0u;
-                sh.bi[3] = run_at > 0 ? 1 : 0;
+                sm.bu[2] = sm.u.r.rkey[run_at];
+                sm.bu[3] = sm.u.r.rcnt[run_at];
+                sm.bu[4] = run_at > 0 ? sm.u.r.rkey[run_at - 1] : 0u;
+                sm.bi[3] = run_at > 0 ? 1 : 0;
             }
         }
         __syncthreads();
-        const bool found = sh.bi[1] != 0;
+        const bool found = sm.bi[1] != 0;
         if (found) {
-            const uint32_t tk = sh.bu[4];
-            const uint32_t rkey = sh.bu[6], rcnt = sh.bu[7];
-            const bool prev_in_region = sh.bi[3] != 0;
-            const uint32_t pkey = sh.bu[2];
+            const uint32_t tk = sm.bu[0], rkey = sm.bu[2], rcnt = sm.bu[3], pkey = sm.bu[4];
+            const bool prev_in_region = sm.bi[3] != 0;
             __syncthreads();
             if (tk > 0) {
                 *cut_key = rkey;
-                *cut_i = (tk >= rcnt) ? IDX_ALL : tie_index<DT>(sh, c, rkey, tk);
+                *cut_i = (tk >= rcnt) ? IDX_ALL : tie_index<DT>(sm, c, rkey, tk);
             } else if (prev_in_region) {
                 *cut_key = pkey; *cut_i = IDX_ALL;
             } else if (have_prev) {
@@ -1262,92 +765,1020 @@ __device__ __noinline__ void topp_cut(K2Shared &sh, const K2Ctx &c, const RowPla
             }
             return;
         }
-        F = sh.bf[0];
-        if (nruns_total > 0) { prev_key = sh.bu[5]; have_prev = true; }
+        F = sm.bf[0];
+        if (nruns_total > 0) { prev_key = sm.bu[1]; have_prev = true; }
         __syncthreads();
         b_hi = b_lo - 1;
-        while (b_hi >= 0 && sh.l1c[b_hi] == 0u) --b_hi;
+        while (b_hi >= 0 && sm.v.l1.cnt[b_hi] == 0u) --b_hi;
     }
-    // nothing triggered: every finite element above the floor is kept
     if (have_prev) { *cut_key = prev_key; *cut_i = IDX_ALL; }
     else *status = MIS_ROW_INVALID;
 }
 
+// Full row by re-reads: top-k of any size by count descent, then top-p, then
+// the draw.  Serves large k', fp16/bf16 top-p and every overflow.
 template <int DT>
-__device__ __noinline__ void final_generic(K2Shared &sh, K2Ctx &c, const RowPlan &pl, bool have_l1, RowOut *ro,
-                              int64_t *out_ids, int32_t *out_status, int row, const uint32_t *gl1c, const double *gl1m)
+__device__ __noinline__ void final_generic(Smem &sm, const RowCx &c, const RowPlan &pl, RowOut *ro, const Args &a)
 {
+    if (DT != F32 && pl.kk > 0) {
+        // the 16-bit top-k radix descent is switched off in this build
+        write_row(ro, a, c.row, -1, MIS_ROW_UNSUPPORTED, pl.mode, c.m, 0u, 0, 0.0);
+        return;
+    }
     const double md = (double)c.m;
     const uint32_t kneg = row_key(-INFINITY, DT);
-    // 256-bin histogram of the whole row
-    if (have_l1) {
-        for (int b = threadIdx.x; b < 256; b += K2_THREADS) {
-            double mm = 0.0; uint32_t cc = 0;
-            for (int g = 0; g < c.G; ++g) { mm += gl1m[(size_t)g * 256 + b] * sh.chs[g]; cc += gl1c[(size_t)g * 256 + b]; }
-            sh.l1m[b] = mm; sh.l1c[b] = cc;
-        }
-    } else {
-        for (int b = threadIdx.x; b < 256; b += K2_THREADS) { sh.l1m[b] = 0.0; sh.l1c[b] = 0u; }
-        __syncthreads();
-        rescan<DT>(c, 0x007fffffu, 0xff800000u, [&](int64_t, float y, uint32_t key) {
-            atomicAdd(&sh.l1c[key >> 24], 1u);
-            atomicAdd(&sh.l1m[key >> 24], exp((double)y - md));
-        });
-    }
     __syncthreads();
-    // top-k threshold by count
+    for (int b = threadIdx.x; b < 256; b += NT) { sm.v.l1.mass[b] = 0.0; sm.v.l1.cnt[b] = 0u; }
+    __syncthreads();
+    rescan<DT>(c, 0x007fffffu, 0xff800000u, [&](int64_t, float y, uint32_t key) {
+        atomicAdd(&sm.v.l1.cnt[key >> 24], 1u);
+        if (y != -INFINITY) atomicAdd(&sm.v.l1.mass[key >> 24], exp((double)y - md));
+    });
+    __syncthreads();
     uint32_t floor_key = kneg + 1u;
     if (pl.kk > 0) {
-        double acc; uint32_t kc;
-        floor_key = descend<DT>(sh, c, false, (double)pl.kk, 0u, &acc, &kc);
+        double acc;
+        uint32_t kc;
+        floor_key = descend<DT>(sm, c, false, (double)pl.kk, 0u, &acc, &kc);
         if (floor_key <= kneg) floor_key = kneg + 1u;
-    }
-    // histogram and weight of the survivors (key >= floor_key)
-    for (int b = threadIdx.x; b < 256; b += K2_THREADS) { sh.l1m[b] = 0.0; sh.l1c[b] = 0u; }
-    __syncthreads();
-    {
+        __syncthreads();
+        for (int b = threadIdx.x; b < 256; b += NT) { sm.v.l1.mass[b] = 0.0; sm.v.l1.cnt[b] = 0u; }
         uint32_t xlo, xhi;
-        x_interval<DT>(sh, floor_key, 0xffffffffu, c.T, &xlo, &xhi);
+        x_interval<DT>(sm, floor_key, 0xffffffffu, c.T, &xlo, &xhi);
         rescan<DT>(c, xlo, xhi, [&](int64_t, float y, uint32_t key) {
             if (key < floor_key) return;
-            atomicAdd(&sh.l1c[key >> 24], 1u);
-            atomicAdd(&sh.l1m[key >> 24], exp((double)y - md));
+            atomicAdd(&sm.v.l1.cnt[key >> 24], 1u);
+            atomicAdd(&sm.v.l1.mass[key >> 24], exp((double)y - md));
         });
+        __syncthreads();
     }
-    __syncthreads();
     double S = 0.0;
-    for (int b = threadIdx.x; b < 256; b += K2_THREADS) S += sh.l1m[b];
-    S = block_sum<K2_THREADS>(S, sh.red_d);
+    for (int b = threadIdx.x; b < 256; b += NT) S += sm.v.l1.mass[b];
+    S = block_sum<double>(S, sm.red);
     uint32_t cut_key = floor_key;
     int32_t cut_i = IDX_ALL;
     int status = MIS_ROW_OK;
-    if (pl.topp) topp_cut<DT>(sh, c, pl, floor_key, S, &cut_key, &cut_i, &status);
+    if (pl.topp) topp_cut_generic<DT>(sm, c, pl.top_p, floor_key, S, &cut_key, &cut_i, &status);
     if (status != MIS_ROW_OK) {
-        write_row<DT>(ro, out_ids, out_status, row, -1, status, pl.mode, c.m, 0u, 0, 0.0);
+        write_row(ro, a, c.row, -1, status, pl.mode, c.m, 0u, 0, 0.0);
         return;
     }
-    // per-chunk kept weight by a full filtered re-read
-    for (int g = threadIdx.x; g < c.G; g += K2_THREADS) sh.cw[g] = 0.0;
     __syncthreads();
-    {
-        uint32_t xlo, xhi;
-        x_interval<DT>(sh, cut_key, 0xffffffffu, c.T, &xlo, &xhi);
-        rescan<DT>(c, xlo, xhi, [&](int64_t j, float y, uint32_t key) {
-            if (kept_by_cut(key, j, cut_key, cut_i)) atomicAdd(&sh.cw[j / c.CH], exp((double)y - md));
+    for (int g = threadIdx.x; g < c.G; g += NT) sm.cw[g] = 0.0;
+    uint32_t xlo, xhi;
+    x_interval<DT>(sm, cut_key, 0xffffffffu, c.T, &xlo, &xhi);
+    rescan<DT>(c, xlo, xhi, [&](int64_t j, float y, uint32_t key) {
+        if (kept_by_cut(key, j, cut_key, cut_i)) atomicAdd(&sm.cw[j / c.CH], exp((double)y - md));
+    });
+    int g;
+    double resid, SK;
+    pick_chunk(sm, c.G, pl.u, &g, &resid, &SK);
+    int64_t id = -1;
+    if (g >= 0) {
+        const float T = c.T;
+        id = draw_in_chunk<DT>(sm, c, g, resid, [&](float x, int64_t j) -> double {
+            const float y = scale_y<DT>(x, T);
+            return (y != -INFINITY && kept_by_cut(row_key(y, DT), j, cut_key, cut_i)) ? exp((double)y - md) : 0.0;
         });
     }
-    double SK;
-    int64_t id = draw_from_chunks<DT>(sh, c, pl.u, cut_key, cut_i, &SK);
-    write_row<DT>(ro, out_ids, out_status, row, id, id >= 0 ? MIS_ROW_OK : MIS_ROW_INVALID, pl.mode, c.m, cut_key, cut_i, SK);
+    write_row(ro, a, c.row, id, id >= 0 ? MIS_ROW_OK : MIS_ROW_INVALID, pl.mode, c.m, cut_key, cut_i, SK);
 }
 
-// ------------------------------------------------------------------ K3: debug emit
+// ------------------------------------------------------------------ small top-k leader
+
+// Exact k'-th value over the per-chunk candidates, survivors, optional top-p,
+// draw.  Returns false when the survivors overflow LDS.
+template <int DT>
+__device__ __noinline__ bool final_smallk(Smem &sm, const RowCx &c, const RowPlan &pl, const ChunkSum *cs,
+                                          const Cand *cand, RowOut *ro, const Args &a)
+{
+    const double md = (double)c.m;
+    uint32_t ntot = 0;
+    for (int g = threadIdx.x; g < c.G; g += NT) ntot += cs[g].ncand;
+    ntot = block_sum<uint32_t>(ntot, sm.red);
+    // k'-th largest raw key over the candidates: 11 / 11 / 10-bit digits.  Fewer
+    // candidates than k' means fewer finite elements than k' in the row.
+    uint32_t xk_thr = 0u;
+    if (ntot >= (uint32_t)pl.kk) {
+        uint32_t prefix = 0u, rem = (uint32_t)pl.kk;
+        const int shifts[3] = {21, 10, 0};
+        const int bits[3] = {11, 11, 10};
+        for (int lev = 0; lev < 3; ++lev) {
+            const int sh = shifts[lev], nb = 1 << bits[lev];
+            const uint32_t hmask = lev == 0 ? 0u : ~((1u << (sh + bits[lev])) - 1u);
+            __syncthreads();
+            for (int i = threadIdx.x; i < 2048; i += NT) sm.u.h11.cnt[i] = 0u;
+            __syncthreads();
+            for (int g = 0; g < c.G; ++g) {
+                const uint32_t n = cs[g].ncand;
+                const Cand *cg = cand + (size_t)g * CAND_CAP;
+                for (uint32_t i = threadIdx.x; i < n; i += NT) {
+                    const uint32_t k = key_of_f32(cg[i].x);
+                    if ((k & hmask) == (prefix & hmask)) atomicAdd(&sm.u.h11.cnt[(k >> sh) & (uint32_t)(nb - 1)], 1u);
+                }
+            }
+            __syncthreads();
+            if (wave_id() == 0) {
+                uint32_t above;
+                const int d = wave_find_desc<uint32_t>(sm.u.h11.cnt, nb, rem, &above);
+                if (lane_id() == 0) { sm.bu[0] = (uint32_t)d; sm.bu[1] = above; }
+            }
+            __syncthreads();
+            rem -= sm.bu[1];
+            prefix |= sm.bu[0] << sh;
+            __syncthreads();
+        }
+        xk_thr = prefix;
+    }
+    // survivors: scaled value >= scale(k'-th raw value); the ties the scaling
+    // creates are kept, as the reference keeps them
+    const uint32_t thr_key = xk_thr ? row_key(scale_y<DT>(f32_of_key(xk_thr), c.T), DT) : 0u;
+    if (threadIdx.x == 0) sm.bu[3] = 0u;
+    __syncthreads();
+    for (int g = 0; g < c.G; ++g) {
+        const uint32_t n = cs[g].ncand;
+        const Cand *cg = cand + (size_t)g * CAND_CAP;
+        for (uint32_t i = threadIdx.x; i < n; i += NT) {
+            const Cand cd = cg[i];
+            const float y = scale_y<DT>(cd.x, c.T);
+            const uint32_t k = row_key(y, DT);
+            if (k >= thr_key) {
+                const uint32_t p = atomicAdd(&sm.bu[3], 1u);
+                if (p < (uint32_t)SURV_CAP) { sm.u.s.key[p] = k; sm.u.s.idx[p] = cd.idx; sm.u.s.e[p] = exp((double)y - md); }
+            }
+        }
+    }
+    __syncthreads();
+    const uint32_t ns = sm.bu[3];
+    __syncthreads();
+    if (ns > (uint32_t)SURV_CAP || ns == 0) return false;
+
+    uint32_t cut_key = thr_key;
+    int32_t cut_i = IDX_ALL;
+    int status = MIS_ROW_OK;
+    if (pl.topp) {
+        double S = 0.0;
+        for (uint32_t i = threadIdx.x; i < ns; i += NT) S += sm.u.s.e[i];
+        S = block_sum<double>(S, sm.red);
+        if (DT == F32) {
+            window_cut(sm, sm.u.s.key, sm.u.s.idx, sm.u.s.e, ns, (double)pl.top_p * S, 0.0, &cut_key, &cut_i, DT);
+        } else {
+            // 16-bit rounding chain over the survivors in stable descending order
+            int npow = 1;
+            while (npow < (int)ns) npow <<= 1;
+            constexpr int PT = SURV_CAP / NT;
+            uint64_t kt[PT];
+            double et[PT];
+            __syncthreads();
+            for (int q = 0; q < PT; ++q) {
+                const int i = threadIdx.x + q * NT;
+                kt[q] = (i < (int)ns) ? (((uint64_t)sm.u.s.key[i] << 32) | (uint64_t)(0xffffffffu - (uint32_t)sm.u.s.idx[i])) : 0ull;
+                et[q] = (i < (int)ns) ? sm.u.s.e[i] : 0.0;
+            }
+            __syncthreads();
+            for (int q = 0; q < PT; ++q) {
+                const int i = threadIdx.x + q * NT;
+                sm.u.so.k[i] = kt[q];
+                sm.u.so.e[i] = et[q];
+            }
+            __syncthreads();
+            for (int kk = 2; kk <= npow; kk <<= 1) {      // bitonic sort, descending
+                for (int j = kk >> 1; j > 0; j >>= 1) {
+                    for (int i = threadIdx.x; i < npow; i += NT) {
+                        const int ixj = i ^ j;
+                        if (ixj > i) {
+                            const bool desc = (i & kk) == 0;
+                            const uint64_t x = sm.u.so.k[i], y = sm.u.so.k[ixj];
+                            if (desc ? (x < y) : (x > y)) {
+                                sm.u.so.k[i] = y; sm.u.so.k[ixj] = x;
+                                const double t = sm.u.so.e[i]; sm.u.so.e[i] = sm.u.so.e[ixj]; sm.u.so.e[ixj] = t;
+                            }
+                        }
+                    }
+                    __syncthreads();
+                }
+            }
+            if (threadIdx.x == 0) {
+                const float thr16 = rn_dtype(pl.top_p, DT);
+                float F = 0.0f;
+                uint32_t r0 = ns;
+                int i = 0;
+                while (i < (int)ns) {
+                    const uint32_t key = (uint32_t)(sm.u.so.k[i] >> 32);
+                    int jn = i + 1;
+                    while (jn < (int)ns && (uint32_t)(sm.u.so.k[jn] >> 32) == key) ++jn;
+                    const float p = rn_dtype((float)(sm.u.so.e[i] / S), DT);
+                    const uint32_t n = (uint32_t)(jn - i);
+                    const float Fend = chain_add_n(F, p, n);
+                    if (chain_E(Fend, p, DT) >= thr16) {
+                        uint32_t lo = 0, hi = n - 1;
+                        while (lo < hi) {
+                            const uint32_t mid = lo + (hi - lo) / 2;
+                            if (chain_E(chain_add_n(F, p, (uint64_t)mid + 1), p, DT) >= thr16) hi = mid; else lo = mid + 1;
+                        }
+                        r0 = (uint32_t)i + lo;
+                        break;
+                    }
+                    F = Fend;
+                    i = jn;
+                }
+                sm.bu[0] = r0;
+                if (r0 > 0) {
+                    const uint64_t q = sm.u.so.k[r0 - 1];
+                    sm.bu[1] = (uint32_t)(q >> 32);
+                    sm.bi[0] = (int32_t)(0xffffffffu - (uint32_t)q);
+                }
+            }
+            __syncthreads();
+            const uint32_t r0 = sm.bu[0];
+            if (r0 > 0) { cut_key = sm.bu[1]; cut_i = sm.bi[0]; }
+            __syncthreads();
+            if (r0 == 0) status = MIS_ROW_INVALID;
+            for (int q = 0; q < PT; ++q) {               // back to the (key, idx, e) view
+                const int i = threadIdx.x + q * NT;
+                kt[q] = sm.u.so.k[i];
+                et[q] = sm.u.so.e[i];
+            }
+            __syncthreads();
+            for (int q = 0; q < PT; ++q) {
+                const int i = threadIdx.x + q * NT;
+                if (i < (int)ns) {
+                    sm.u.s.key[i] = (uint32_t)(kt[q] >> 32);
+                    sm.u.s.idx[i] = (int32_t)(0xffffffffu - (uint32_t)kt[q]);
+                    sm.u.s.e[i] = et[q];
+                }
+            }
+            __syncthreads();
+        }
+    }
+    if (status != MIS_ROW_OK) {
+        write_row(ro, a, c.row, -1, status, pl.mode, c.m, 0u, 0, 0.0);
+        return true;
+    }
+    double SK = 0.0;
+    for (uint32_t i = threadIdx.x; i < ns; i += NT) {
+        if (!kept_by_cut(sm.u.s.key[i], sm.u.s.idx[i], cut_key, cut_i)) sm.u.s.e[i] = 0.0;
+        SK += sm.u.s.e[i];
+    }
+    SK = block_sum<double>(SK, sm.red);
+    const int64_t id = draw_in_list(sm, sm.u.s.idx, sm.u.s.e, (int)ns, c.V, (double)pl.u * SK);
+    write_row(ro, a, c.row, id, id >= 0 ? MIS_ROW_OK : MIS_ROW_INVALID, pl.mode, c.m, cut_key, cut_i, SK);
+    return true;
+}
+
+// fp32 top-p, after the collect round: the exact cut inside the window
+// (mass descent over the collected keys), per-chunk kept weights, the draw.
+// sm.bd[6] = A (top_p * S), sm.bd[7] = mass above the window, sm.chs[] the
+// per-chunk rescale, all set by the leader before the rounds.
+template <int DT>
+__device__ __noinline__ void final_topp_window(Smem &sm, RowCx &c, const RowPlan &pl, const ChunkSum *csr,
+                                               const RowCtl *rc, RowOut *ro, const Args &a)
+{
+    const Layout &L = a.L;
+    const int tid = threadIdx.x, row = c.row;
+    const float mrow = rc->m;
+    const double md = (double)mrow;
+    const double A = sm.bd[6], A_above = sm.bd[7];
+    c.m = mrow;
+    const uint32_t nw0 = ld_acq(&rc->wcount);
+    const uint32_t nw = nw0 < (uint32_t)WCAP ? nw0 : (uint32_t)WCAP;
+    const Elem *win = reinterpret_cast<const Elem *>(a.ws + L.win) + (size_t)row * WCAP;
+    for (uint32_t i = tid; i < nw; i += NT) {
+        const Elem el = win[i];
+        sm.u.s.key[i] = el.key;
+        sm.u.s.idx[i] = el.idx;
+        sm.u.s.e[i] = exp((double)value_of_row_key(el.key, DT) - md);
+    }
+    __syncthreads();
+    uint32_t cut_key;
+    int32_t cut_i;
+    window_cut(sm, sm.u.s.key, sm.u.s.idx, sm.u.s.e, nw, A - A_above, 0.0, &cut_key, &cut_i, DT);
+    // per-chunk kept weight: whole fine bins above the window (phase 1), kept
+    // mass above the collected range, kept collected elements
+    const double gm = floor(md * (double)FB_W);
+    const double *gmm = reinterpret_cast<const double *>(a.ws + L.fbm) + (size_t)row * L.G * FB_N;
+    const double *amass = reinterpret_cast<const double *>(a.ws + L.amass) + (size_t)row * G_MAX;
+    // the window's row bin, as published with round 1 (deriving it from the
+    // window's top key would be off by one for the bin just below zero,
+    // whose top key is that of -0.0)
+    const double rbw = (double)rc->rbin;
+    for (int g = tid; g < L.G; g += NT) {
+        double w = 0.0;
+        if (csr[g].ymax != -INFINITY) {
+            const double off = gm - csr[g].gmc;
+            for (int rb = 0; rb < (int)rbw && rb < FB_N; ++rb) {
+                const double cb = (double)rb - off;
+                if (cb >= 0.0) w += gmm[(size_t)g * FB_N + (int)cb];
+            }
+            w *= sm.chs[g];
+        }
+        sm.cw[g] = w + amass[g];
+    }
+    __syncthreads();
+    for (uint32_t i = tid; i < nw; i += NT)
+        if (kept_by_cut(sm.u.s.key[i], sm.u.s.idx[i], cut_key, cut_i))
+            atomicAdd(&sm.cw[sm.u.s.idx[i] / c.CH], sm.u.s.e[i]);
+    int gsel;
+    double resid, SK;
+    pick_chunk(sm, L.G, pl.u, &gsel, &resid, &SK);
+    int64_t id = -1;
+    if (gsel >= 0) {
+        const float T = pl.T;
+        id = draw_in_chunk<DT>(sm, c, gsel, resid, [&](float xv, int64_t j) -> double {
+            const float y = scale_y<DT>(xv, T);
+            return (y != -INFINITY && kept_by_cut(row_key(y, DT), j, cut_key, cut_i)) ? exp((double)y - md) : 0.0;
+        });
+    }
+    write_row(ro, a, row, id, id >= 0 ? MIS_ROW_OK : MIS_ROW_INVALID, pl.mode, mrow, cut_key, cut_i, SK);
+}
+
+// fp32 top-p leader, after phase 1: merge the chunks' fine bins on the row
+// grid, find the bin holding the cut and publish round 1 (collect the bin, or
+// histogram it first when it is crowded).  Returns 0 when rounds follow,
+// 1 when the row is invalid, 2 when the cut lies below the bins (re-read path).
+template <int DT>
+__device__ __forceinline__ int topp_plan(Smem &sm, RowCx &c, const RowPlan &pl, const ChunkSum *csr, RowCtl *rc)
+{
+    // the caller's Args are reached through the chunk summaries' owner layout
+    const int tid = threadIdx.x;
+    uint32_t anyflag = 0;
+    float m = -INFINITY;
+    for (int g = tid; g < c.G; g += NT) { anyflag |= csr[g].flags; m = fmaxf(m, csr[g].ymax); }
+    anyflag = block_sum<uint32_t>(anyflag ? 1u : 0u, sm.red);
+    m = block_max<float>(m, sm.red);
+    int state = 0;
+    if (anyflag != 0u || m == -INFINITY) state = 1;
+    c.m = m;
+    const double md = (double)m;
+    double S = 0.0, A = 0.0, A_above = 0.0;
+    if (state == 0) {
+        const double gm = floor(md * (double)FB_W);
+        for (int g = tid; g < c.G; g += NT) sm.chs[g] = exp((double)csr[g].ymax - md);
+        __syncthreads();
+        double s = 0.0;
+        for (int g = tid; g < c.G; g += NT) if (csr[g].ymax != -INFINITY) s += csr[g].S * sm.chs[g];
+        S = block_sum<double>(s, sm.red);
+        for (int rb = tid; rb < FB_N; rb += NT) {
+            double mm = 0.0;
+            uint32_t cc = 0;
+            for (int g = 0; g < c.G; ++g) {
+                if (csr[g].ymax == -INFINITY) continue;
+                const double cb = (double)rb - (gm - csr[g].gmc);
+                if (cb >= 0.0) {
+                    mm += c.fbm[(size_t)g * FB_N + (int)cb] * sm.chs[g];
+                    cc += c.fbc[(size_t)g * FB_N + (int)cb];
+                }
+            }
+            sm.v.rb.m[FB_N - 1 - rb] = mm;
+            sm.v.rb.c[FB_N - 1 - rb] = cc;
+        }
+        __syncthreads();
+        A = (double)pl.top_p * S;
+        if (wave_id() == 0) {
+            double ab;
+            const int d = wave_find_desc<double>(sm.v.rb.m, FB_N, A, &ab);
+            double tot = 0.0;
+            for (int q = lane_id(); q < FB_N; q += 64) tot += sm.v.rb.m[q];
+            tot = wave_sum(tot);
+            if (lane_id() == 0) {
+                sm.bi[2] = (tot >= A) ? (FB_N - 1 - d) : -1;  // -1: the cut lies below the bins
+                sm.bd[4] = ab;
+                sm.bu[2] = sm.v.rb.c[d];
+            }
+        }
+        __syncthreads();
+        const int rbstar = sm.bi[2];
+        A_above = sm.bd[4];
+        const uint32_t wcnt = sm.bu[2];
+        __syncthreads();
+        if (rbstar < 0) {
+            state = 2;
+        } else {
+            const double g = gm - (double)rbstar;  // the bin is [g/FB_W, (g+1)/FB_W)
+            const float lo = (float)(g / (double)FB_W);
+            const float hi = (float)((g + 1.0) / (double)FB_W);
+            const uint32_t klo = key_of_f32(lo);
+            const uint32_t khi = key_of_f32(hi) - 1u;
+            if (wcnt > (uint32_t)WCAP)
+                for (int i = tid; i < SUB_N; i += NT) { c.subc[i] = 0u; c.subm[i] = 0.0; }
+            if (tid == 0) {
+                rc->hlo = lo; rc->hhi = hi; rc->klo = klo; rc->khi = khi; rc->kahi = khi; rc->rbin = rbstar;
+                rc->wcount = 0u;
+                rc->rtype = wcnt > (uint32_t)WCAP ? R_HIST : R_COLLECT;
+            }
+        }
+    }
+    if (tid == 0) {
+        rc->m = m;
+        if (state != 0) rc->rtype = R_DONE;
+        sm.bd[5] = S; sm.bd[6] = A; sm.bd[7] = A_above;
+    }
+    (void)block_release_add(sm, &rc->round, 1u);  // publish round 1
+    return state;
+}
+
+// fp32 top-p leader after a histogram round: find the sub-bin holding the cut,
+// publish a collect round for it.  Returns 0 (round published) or 2 (give up:
+// the re-read path takes over; the followers were released).
+template <int DT>
+__device__ __forceinline__ int topp_after_hist(Smem &sm, const RowCx &c, RowCtl *rc)
+{
+    const int tid = threadIdx.x;
+    const uint32_t klo = rc->klo, khi = rc->khi;
+    const float hlo = rc->hlo, hhi = rc->hhi;
+    const double A = sm.bd[6];
+    double A_above = sm.bd[7];
+    for (int i = tid; i < SUB_N; i += NT) { sm.sub_m[SUB_N - 1 - i] = c.subm[i]; sm.sub_c[SUB_N - 1 - i] = c.subc[i]; }
+    __syncthreads();
+    if (wave_id() == 0) {
+        double ab;
+        const int d = wave_find_desc<double>(sm.sub_m, SUB_N, A - A_above, &ab);
+        if (lane_id() == 0) { sm.bi[3] = SUB_N - 1 - d; sm.bd[4] = ab; sm.bu[2] = sm.sub_c[d]; }
+    }
+    __syncthreads();
+    const int sstar = sm.bi[3];
+    A_above += sm.bd[4];
+    const uint32_t scnt = sm.bu[2];
+    __syncthreads();
+    if (tid == 0) sm.bd[7] = A_above;
+    // key range of sub-bin sstar inside [klo, khi]; the sub-bin index is
+    // non-increasing in the key
+    if (wave_id() == 0) {
+        const float inv = (float)SUB_N / (hhi - hlo);
+        auto sbk = [&](uint32_t k) -> int { return min(SUB_N - 1, (int)((hhi - f32_of_key(k)) * inv)); };
+        uint64_t lo = klo, hi = khi;  // smallest key with sbk <= sstar
+        if (sbk(klo) <= sstar) hi = klo;
+        else {
+            while (hi - lo > 1) {
+                uint64_t step = (hi - lo) / 64; if (step == 0) step = 1;
+                const uint64_t p = lo + (uint64_t)(lane_id() + 1) * step;
+                const bool pred = p >= hi ? true : (sbk((uint32_t)p) <= sstar);
+                const uint64_t mk = __ballot(pred);
+                if (mk == 0ull) { lo = lo + 64 * step; continue; }
+                const int f = __builtin_ctzll(mk);
+                const uint64_t nhi = lo + (uint64_t)(f + 1) * step;
+                if (nhi < hi) hi = nhi;
+                lo = lo + (uint64_t)f * step;
+            }
+        }
+        const uint32_t skl = (uint32_t)hi;
+        uint64_t lo2 = klo, hi2 = khi;  // largest key with sbk >= sstar
+        if (sbk(khi) >= sstar) lo2 = khi;
+        else {
+            while (hi2 - lo2 > 1) {
+                uint64_t step = (hi2 - lo2) / 64; if (step == 0) step = 1;
+                const uint64_t p = lo2 + (uint64_t)(lane_id() + 1) * step;
+                const bool pred = p >= hi2 ? true : (sbk((uint32_t)p) < sstar);
+                const uint64_t mk = __ballot(pred);
+                if (mk == 0ull) { lo2 = lo2 + 64 * step; continue; }
+                const int f = __builtin_ctzll(mk);
+                const uint64_t nhi = lo2 + (uint64_t)(f + 1) * step;
+                if (nhi < hi2) hi2 = nhi;
+                lo2 = lo2 + (uint64_t)f * step;
+            }
+        }
+        if (lane_id() == 0) { sm.bu[4] = skl; sm.bu[5] = (uint32_t)lo2; }
+    }
+    __syncthreads();
+    const uint32_t skl = sm.bu[4], skh = sm.bu[5];
+    const bool give_up = (scnt > (uint32_t)WCAP || skl > skh);
+    __syncthreads();
+    if (tid == 0) {
+        if (give_up) rc->rtype = R_DONE;
+        else { rc->rtype = R_COLLECT; rc->klo = skl; rc->khi = skh; rc->kahi = khi; rc->wcount = 0u; }
+    }
+    (void)block_release_add(sm, &rc->round, 1u);
+    return give_up ? 2 : 0;
+}
+
+// Leader of a row that needs no refinement rounds: greedy, temperature only,
+// small top-k, and the re-read path for everything else.
+template <int DT>
+__device__ __noinline__ void final_row(Smem &sm, RowCx &c, const RowPlan &pl, const ChunkSum *csr, RowOut *ro,
+                                       const Args &a)
+{
+    const int tid = threadIdx.x, row = c.row;
+    const Layout &L = a.L;
+    if (pl.mode == M_BAD) {
+        write_row(ro, a, row, -1, MIS_ROW_BAD_PARAM, pl.mode, 0.0f, 0u, 0, 0.0);
+        return;
+    }
+    uint32_t k2 = 0u;
+    int32_t i2 = IDX_ALL;
+    uint32_t anyflag = 0u;
+    float m = -INFINITY, xm = -INFINITY;
+    for (int g = tid; g < L.G; g += NT) {
+        const ChunkSum s = csr[g];
+        if (s.xkey > k2 || (s.xkey == k2 && s.xarg < i2)) { k2 = s.xkey; i2 = s.xarg; }
+        anyflag |= s.flags;
+        m = fmaxf(m, s.ymax);
+        xm = fmaxf(xm, s.xmax);
+    }
+    wave_argmax(k2, i2);
+    if (lane_id() == 0) { sm.red.u[wave_id()] = k2; sm.red.l[wave_id()] = i2; }
+    __syncthreads();
+    if (tid == 0) {
+        for (int w = 1; w < NWAVE; ++w) {
+            const uint32_t kk = sm.red.u[w];
+            const int32_t ii = (int32_t)sm.red.l[w];
+            if (kk > k2 || (kk == k2 && ii < i2)) { k2 = kk; i2 = ii; }
+        }
+        sm.bi[0] = i2;
+    }
+    __syncthreads();
+    i2 = sm.bi[0];
+    __syncthreads();
+    anyflag = block_sum<uint32_t>(anyflag ? 1u : 0u, sm.red);
+    m = block_max<float>(m, sm.red);
+    xm = block_max<float>(xm, sm.red);
+    c.m = m;
+    const double md = (double)m;
+    if (pl.mode == M_GREEDY) {
+        write_row(ro, a, row, i2, MIS_ROW_OK, pl.mode, 0.0f, 0u, i2, 1.0);
+    } else if (anyflag != 0u || m == -INFINITY) {
+        write_row(ro, a, row, -1, MIS_ROW_INVALID, pl.mode, m, 0u, 0, 0.0);
+    } else if (pl.mode == M_TEMP && DT == F32) {
+        // chunk weights are exp((x - xmax_c)/T): rescale to the row's raw max
+        const double l2e_d = 1.4426950408889634 / (double)pl.T;
+        for (int g = tid; g < L.G; g += NT) {
+            sm.chs[g] = csr[g].xmax == -INFINITY ? 0.0 : exp2(((double)csr[g].xmax - (double)xm) * l2e_d);
+            sm.cw[g] = csr[g].S * sm.chs[g];
+        }
+        int gsel;
+        double resid, SK;
+        pick_chunk(sm, L.G, pl.u, &gsel, &resid, &SK);
+        int64_t id = -1;
+        if (gsel >= 0) {
+            const float l2e = (float)l2e_d;
+            const float xc = csr[gsel].xmax;
+            id = draw_in_chunk<DT>(sm, c, gsel, resid / sm.chs[gsel], [&](float xv, int64_t) -> double {
+                return (double)exp2f((xv - xc) * l2e);
+            });
+        }
+        // kept weights relative to m = scale(xm), for the debug probabilities
+        write_row(ro, a, row, id, id >= 0 ? MIS_ROW_OK : MIS_ROW_INVALID, pl.mode, m, row_key(-INFINITY, DT), -1,
+                  SK * exp((double)xm / (double)pl.T - md));
+    } else if (pl.mode == M_TEMP) {
+        // fp16/bf16: chunk weights are exp(y - ymax_c): rescale to the row max m
+        for (int g = tid; g < L.G; g += NT) {
+            sm.chs[g] = csr[g].ymax == -INFINITY ? 0.0 : exp((double)csr[g].ymax - md);
+            sm.cw[g] = csr[g].S * sm.chs[g];
+        }
+        int gsel;
+        double resid, SK;
+        pick_chunk(sm, L.G, pl.u, &gsel, &resid, &SK);
+        int64_t id = -1;
+        if (gsel >= 0) {
+            constexpr float L2E = 1.44269504088896341f;
+            const float yc = csr[gsel].ymax, T = pl.T;
+            id = draw_in_chunk<DT>(sm, c, gsel, resid / sm.chs[gsel], [&](float xv, int64_t) -> double {
+                return (double)exp2f((scale_y<DT>(xv, T) - yc) * L2E);
+            });
+        }
+        write_row(ro, a, row, id, id >= 0 ? MIS_ROW_OK : MIS_ROW_INVALID, pl.mode, m, row_key(-INFINITY, DT), -1, SK);
+    } else if (pl.mode == M_SMALLK) {
+        bool ovf = false;
+        for (int g = 0; g < L.G; ++g) ovf |= (csr[g].ncand == NCAND_OVERFLOW);
+        const Cand *cand = reinterpret_cast<const Cand *>(a.ws + L.cand) + (size_t)row * L.G * CAND_CAP;
+        bool done = false;
+        if (!ovf) done = final_smallk<DT>(sm, c, pl, csr, cand, ro, a);
+        if (!done) final_generic<DT>(sm, c, pl, ro, a);
+    } else {
+        final_generic<DT>(sm, c, pl, ro, a);
+    }
+}
+
+// ------------------------------------------------------------------ the kernel
+
+template <int DT, int EPT>
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(3))) void k_sample(Args a)
+{
+    constexpr int VEC = Traits<DT>::VEC, NV = EPT / VEC, CH = NT * EPT;
+    __shared__ Smem sm;
+    const Layout &L = a.L;
+    const int tid = threadIdx.x;
+    Ctl *ctl = reinterpret_cast<Ctl *>(a.ws + L.ctl);
+
+    // ---- ticket -> (row, chunk)
+    if (tid == 0) {
+        const unsigned long long t = atomicAdd(&ctl->ticket, 1ull);
+        sm.bq[1] = t % (unsigned long long)(L.B * L.G);
+        sm.args = a;
+    }
+    __syncthreads();
+    const uint32_t task = uni((uint32_t)sm.bq[1]);
+    __syncthreads();
+    const uint32_t G = (uint32_t)L.G;
+    const int row = uni((int32_t)(task / G)), chunk = uni((int32_t)(task % G));
+    const int64_t V = a.V;
+    const int64_t base = (int64_t)chunk * CH;
+    const char *rowp = a.logits + (int64_t)row * a.stride_bytes;
+    mis_row_params P = a.params[row];
+    P.temperature = uni(P.temperature); P.top_k = uni(P.top_k); P.top_p = uni(P.top_p); P.uniform = uni(P.uniform);
+    const RowPlan pl = plan_row(P, V);
+    RowCtl *rc = reinterpret_cast<RowCtl *>(a.ws + L.rowctl) + row;
+    RowOut *ro = reinterpret_cast<RowOut *>(a.ws + L.rowout) + row;
+    ChunkSum *csr = reinterpret_cast<ChunkSum *>(a.ws + L.chunks) + (size_t)row * L.G;
+    ChunkSum *cs = csr + chunk;
+
+    // ---- one coalesced read of the chunk into registers
+    float x[EPT];
+    if (a.vec_ok && base + CH <= V) {  // whole chunk inside the row: all loads issued back to back
+#pragma unroll
+        for (int v = 0; v < NV; ++v) loadvec<DT>(rowp, base + ((int64_t)v * NT + tid) * VEC, &x[v * VEC]);
+    } else {
+#pragma unroll
+        for (int v = 0; v < NV; ++v) {
+            const int64_t j0 = base + ((int64_t)v * NT + tid) * VEC;
+            if (a.vec_ok && j0 + VEC <= V) {
+                loadvec<DT>(rowp, j0, &x[v * VEC]);
+            } else {
+#pragma unroll
+                for (int e = 0; e < VEC; ++e) x[v * VEC + e] = (j0 + e < V) ? load1<DT>(rowp, j0 + e) : 0.0f;
+            }
+        }
+    }
+    // element i of this thread sits at base + lofs(i); `valid` has bit i set
+    // when that index is inside the row
+    auto lofs = [&](int i) -> uint32_t { return (uint32_t)(((i / VEC) * NT + tid) * VEC + (i % VEC)); };
+    const int32_t base32 = (int32_t)base;  // V < 2^31
+    auto idx_of = [&](int i) -> int32_t { return base32 + (int32_t)lofs(i); };
+    uint64_t valid = ~0ull;
+    {
+        const int64_t lim = V - base;  // elements of this chunk inside the row
+        if (lim < (int64_t)CH) {
+            valid = 0ull;
+            const uint32_t lim32 = (uint32_t)lim;
+#pragma unroll
+            for (int i = 0; i < EPT; ++i) valid |= (lofs(i) < lim32 ? 1ull : 0ull) << i;
+        }
+    }
+    auto ok_ = [&](int i) -> bool { return (valid >> i) & 1ull; };
+
+    // ---- argmax of the raw logits (NaN ranks first)
+    uint32_t bk = 0u;
+    int32_t bi = IDX_ALL;
+#pragma unroll
+    for (int i = 0; i < EPT; ++i) {
+        if (ok_(i)) {
+            const uint32_t k = argmax_key(x[i]);
+            if (k > bk) { bk = k; bi = idx_of(i); }
+        }
+    }
+    wave_argmax(bk, bi);
+    if (lane_id() == 0) { sm.red.u[wave_id()] = bk; sm.red.l[wave_id()] = bi; }
+    __syncthreads();
+    if (tid == 0) {
+        for (int w = 1; w < NWAVE; ++w) {
+            const uint32_t k2 = sm.red.u[w];
+            const int32_t i2 = (int32_t)sm.red.l[w];
+            if (k2 > bk || (k2 == bk && i2 < bi)) { bk = k2; bi = i2; }
+        }
+        sm.bu[0] = bk;
+        sm.bi[0] = bi;
+    }
+    __syncthreads();
+    bk = sm.bu[0];
+    bi = sm.bi[0];
+    __syncthreads();
+
+    uint32_t flags = 0u;
+    float xmax = -INFINITY, ymax = -INFINITY;
+    if (pl.mode != M_BAD && pl.mode != M_GREEDY) {
+        if (bk == 0xffffffffu) flags |= FLAG_NAN;
+        else {
+            xmax = f32_of_key(bk);
+            ymax = scale_y<DT>(xmax, pl.T);  // scaling is monotone
+            if (ymax == INFINITY) flags |= FLAG_PINF;
+        }
+    }
+    const bool live = (pl.mode != M_BAD && pl.mode != M_GREEDY && flags == 0u);
+    const bool topp32 = (DT == F32 && pl.mode == M_TOPP);
+
+    // ---- phase 1 per mode
+    uint32_t ncand = 0;
+    double Sc = 0.0, below = 0.0, gmc = 0.0;
+    if (live && pl.mode == M_SMALLK) {
+        uint32_t nfin = 0;
+        float xminf = INFINITY;
+#pragma unroll
+        for (int i = 0; i < EPT; ++i)
+            if (ok_(i) && x[i] != -INFINITY) { nfin++; xminf = fminf(xminf, x[i]); }
+        nfin = block_sum<uint32_t>(nfin, sm.red);
+        xminf = block_min<float>(xminf, sm.red);
+        // candidates: finite x >= xlo_c, where xlo_c keeps the chunk's top k'.
+        // Bins are linear in the raw value over [xminf, xmax] (index 255 = top).
+        float xlo_c = -INFINITY;
+        if (nfin > (uint32_t)pl.kk && xmax > xminf) {
+            const float inv = 256.0f / (xmax - xminf);
+            sm.u.h8.cnt[tid] = 0u;
+            __syncthreads();
+#pragma unroll
+            for (int i = 0; i < EPT; ++i) {
+                if (ok_(i) && x[i] != -INFINITY) {
+                    const int b = min(255, (int)((xmax - opaque(x[i])) * inv));
+                    atomicAdd(&sm.u.h8.cnt[255 - b], 1u);
+                }
+            }
+            __syncthreads();
+            if (wave_id() == 0) {
+                uint32_t above;
+                const int d = wave_find_desc<uint32_t>(sm.u.h8.cnt, 256, (uint32_t)pl.kk, &above);
+                if (lane_id() == 0) { sm.bu[0] = (uint32_t)(255 - d); sm.bu[1] = above; sm.bu[2] = sm.u.h8.cnt[d]; }
+            }
+            __syncthreads();
+            const int bstar = (int)sm.bu[0];
+            const uint32_t above_b = sm.bu[1], in_b = sm.bu[2];
+            __syncthreads();
+            int sstar = 255;
+            if (above_b + in_b > (uint32_t)CAND_CAP) {
+                // refine the boundary bin into 256 sub-bins
+                sm.u.h8.cnt[tid] = 0u;
+                __syncthreads();
+#pragma unroll
+                for (int i = 0; i < EPT; ++i) {
+                    if (ok_(i) && x[i] != -INFINITY) {
+                        const float t = (xmax - opaque(x[i])) * inv;
+                        const int b = min(255, (int)t);
+                        if (b == bstar) atomicAdd(&sm.u.h8.cnt[255 - min(255, (int)((t - (float)b) * 256.0f))], 1u);
+                    }
+                }
+                __syncthreads();
+                if (wave_id() == 0) {
+                    uint32_t above;
+                    const int d = wave_find_desc<uint32_t>(sm.u.h8.cnt, 256, (uint32_t)pl.kk - above_b, &above);
+                    if (lane_id() == 0) sm.bu[0] = (uint32_t)(255 - d);
+                }
+                __syncthreads();
+                sstar = (int)sm.bu[0];
+                __syncthreads();
+            }
+            // smallest raw value inside the selected bins
+            float xb = INFINITY;
+#pragma unroll
+            for (int i = 0; i < EPT; ++i) {
+                if (ok_(i) && x[i] != -INFINITY) {
+                    const float t = (xmax - opaque(x[i])) * inv;
+                    const int b = min(255, (int)t);
+                    if (b < bstar || (b == bstar && min(255, (int)((t - (float)b) * 256.0f)) <= sstar))
+                        xb = fminf(xb, opaque(x[i]));
+                }
+            }
+            xb = block_min<float>(xb, sm.red);
+            // close the set under the ties the scaling creates: every x whose
+            // scaled key equals that of xb is a candidate too
+            uint32_t xlo, xhi;
+            const uint32_t kb = row_key(scale_y<DT>(xb, pl.T), DT);
+            x_interval<DT>(sm, kb, kb, pl.T, &xlo, &xhi);
+            xlo_c = f32_of_key(xlo);
+        }
+        uint32_t mine = 0;
+#pragma unroll
+        for (int i = 0; i < EPT; ++i)
+            if (ok_(i) && x[i] != -INFINITY && x[i] >= xlo_c) mine++;
+        uint32_t total;
+        uint32_t off = block_excl_scan<uint32_t>(mine, sm.red, &total);
+        if (total <= (uint32_t)CAND_CAP) {
+            Cand *cand = reinterpret_cast<Cand *>(a.ws + L.cand) + ((size_t)row * L.G + chunk) * CAND_CAP;
+#pragma unroll
+            for (int i = 0; i < EPT; ++i) {
+                if (ok_(i) && x[i] != -INFINITY && x[i] >= xlo_c) {
+                    Cand cd; cd.x = x[i]; cd.idx = idx_of(i);
+                    cand[off++] = cd;
+                }
+            }
+            ncand = total;
+        } else {
+            ncand = NCAND_OVERFLOW;
+        }
+    } else if (live && pl.mode == M_TEMP) {
+        // draw weights in f32 (within the draw's tolerance), float64 sums.
+        // fp32: exp((x - xmax_c) / T), which equals exp(y - ymax_c) to a few
+        // ulp.  fp16/bf16: the scaled values are rounded to the dtype, so
+        // the weights are taken on them, exp(y - ymax_c).
+        double s = 0.0;
+        if (DT == F32) {
+            const float l2e = (float)(1.4426950408889634 / (double)pl.T);
+            if (xmax != -INFINITY) {
+#pragma unroll
+                for (int i = 0; i < EPT; ++i)
+                    if (ok_(i)) s += (double)exp2f((x[i] - xmax) * l2e);
+            }
+        } else if (ymax != -INFINITY) {
+            constexpr float L2E = 1.44269504088896341f;
+#pragma unroll
+            for (int i = 0; i < EPT; ++i)
+                if (ok_(i)) s += (double)exp2f((scale_y<DT>(x[i], pl.T) - ymax) * L2E);
+        }
+        Sc = block_sum<double>(s, sm.red);
+    } else if (live && topp32) {
+        // exact y, float64 weights relative to the chunk max, fine bins on the
+        // global grid floor(y * FB_W)
+        for (int i = tid; i < FB_N; i += NT) { sm.u.p1.cnt[i] = 0u; sm.u.p1.mass[i] = 0.0; }
+        __syncthreads();
+        const double ym = (double)ymax;
+        gmc = ymax == -INFINITY ? 0.0 : floor(ym * (double)FB_W);
+        double s = 0.0, bl = 0.0;
+        if (ymax != -INFINITY) {
+#pragma unroll
+            for (int i = 0; i < EPT; ++i) {
+                if (ok_(i)) {
+                    const float y = scale_y<DT>(x[i], pl.T);
+                    if (y != -INFINITY) {
+                        const double e = exp((double)y - ym);
+                        s += e;
+                        const double rb = gmc - floor((double)y * (double)FB_W);
+                        if (rb < (double)FB_N) {
+                            const int b = (int)rb;
+                            atomicAdd(&sm.u.p1.cnt[b], 1u);
+                            atomicAdd(&sm.u.p1.mass[b], e);
+                        } else {
+                            bl += e;
+                        }
+                    }
+                }
+            }
+        }
+        Sc = block_sum<double>(s, sm.red);
+        below = block_sum<double>(bl, sm.red);
+        uint32_t *gc = reinterpret_cast<uint32_t *>(a.ws + L.fbc) + ((size_t)row * L.G + chunk) * FB_N;
+        double *gm = reinterpret_cast<double *>(a.ws + L.fbm) + ((size_t)row * L.G + chunk) * FB_N;
+        for (int i = tid; i < FB_N; i += NT) { gc[i] = sm.u.p1.cnt[i]; gm[i] = sm.u.p1.mass[i]; }
+    } else if (live) {
+        // large k' and fp16/bf16 top-p: the leader re-reads the row
+        double s = 0.0;
+        if (ymax != -INFINITY) {
+            const double ym = (double)ymax;
+#pragma unroll
+            for (int i = 0; i < EPT; ++i) {
+                if (ok_(i)) {
+                    const float y = scale_y<DT>(x[i], pl.T);
+                    if (y != -INFINITY) s += exp((double)y - ym);
+                }
+            }
+        }
+        Sc = block_sum<double>(s, sm.red);
+    }
+    if (tid == 0) {
+        cs->xkey = bk; cs->xarg = bi; cs->ymax = ymax; cs->flags = flags; cs->ncand = ncand;
+        cs->xmax = xmax; cs->S = Sc; cs->gmc = gmc; cs->below = below;
+    }
+
+    // ---- arrive; the last arrival leads the row
+    const uint32_t old = block_release_add(sm, &rc->arrive, 1u);
+    const bool leader = (old == G - 1u);
+    if (leader) fence_acquire();
+    __syncthreads();
+
+    // the row context in LDS is filled in the leader only: code that every
+    // workgroup runs takes what it needs from the launch arguments
+    RowCx &c = sm.cx;
+    RowPlan &spl = sm.pl;
+    uint32_t *const subc_row = reinterpret_cast<uint32_t *>(a.ws + L.subc) + (size_t)row * SUB_N;
+    double *const subm_row = reinterpret_cast<double *>(a.ws + L.subm) + (size_t)row * SUB_N;
+    if (leader && tid == 0) {
+        c.rowp = rowp; c.V = V; c.vec_ok = a.vec_ok; c.T = pl.T; c.m = 0.0f; c.G = L.G; c.CH = CH; c.row = row;
+        c.fbc = reinterpret_cast<const uint32_t *>(a.ws + L.fbc) + (size_t)row * L.G * FB_N;
+        c.fbm = reinterpret_cast<const double *>(a.ws + L.fbm) + (size_t)row * L.G * FB_N;
+        c.subc = reinterpret_cast<uint32_t *>(a.ws + L.subc) + (size_t)row * SUB_N;
+        c.subm = reinterpret_cast<double *>(a.ws + L.subm) + (size_t)row * SUB_N;
+        spl = pl;
+    }
+    __syncthreads();
+    const Args &sa = sm.args;
+
+    if (topp32) {
+        // ============================================ fp32 top-p: refinement rounds
+        int state = 0;  // leader: 0 rounds pending, 1 invalid, 2 fallback, 3 collected
+        if (leader) state = topp_plan<DT>(sm, c, spl, csr, rc);
+        uint32_t seen = 0;
+        bool ok = true;
+        for (;;) {
+            if (!block_wait_ge(sm, &rc->round, seen + 1u, ctl)) { ok = false; break; }
+            seen += 1u;
+            const uint32_t rtype = rc->rtype;
+            if (rtype == R_DONE) break;
+            const uint32_t klo = rc->klo, khi = rc->khi, kahi = rc->kahi;
+            const float hlo = rc->hlo, hhi = rc->hhi;
+            const double md = (double)rc->m;
+            uint32_t xlo, xhi;
+            x_interval<DT>(sm, klo, kahi, pl.T, &xlo, &xhi);
+            // stage the few elements whose raw key can map into the round's
+            // range; the register-resident chunk is only compared here
+            if (tid == 0) sm.bu[3] = 0u;
+            __syncthreads();
+#pragma unroll
+            for (int i = 0; i < EPT; ++i) {
+                if (ok_(i)) {
+                    const uint32_t xk = key_of_f32(x[i]);
+                    if (xk >= xlo && xk <= xhi) {
+                        const uint32_t p = atomicAdd(&sm.bu[3], 1u);
+                        if (p < (uint32_t)STAGE_CAP) { sm.u.st.x[p] = x[i]; sm.u.st.j[p] = lofs(i); }
+                    }
+                }
+            }
+            __syncthreads();
+            const uint32_t nst0 = sm.bu[3];
+            const uint32_t nst = nst0 < (uint32_t)STAGE_CAP ? nst0 : (uint32_t)STAGE_CAP;
+            if (nst0 > (uint32_t)STAGE_CAP && tid == 0) atomicOr(&rc->ovf, 1u);
+            if (rtype == R_HIST) {
+                for (int i = tid; i < SUB_N; i += NT) { sm.sub_c[i] = 0u; sm.sub_m[i] = 0.0; }
+                __syncthreads();
+                const float inv = (float)SUB_N / (hhi - hlo);
+                for (uint32_t q = tid; q < nst; q += NT) {
+                    const float y = scale_y<DT>(sm.u.st.x[q], pl.T);
+                    const uint32_t k = row_key(y, DT);
+                    if (k >= klo && k <= khi) {
+                        const int sb = min(SUB_N - 1, (int)((hhi - y) * inv));
+                        atomicAdd(&sm.sub_c[sb], 1u);
+                        atomicAdd(&sm.sub_m[sb], exp((double)y - md));
+                    }
+                }
+                __syncthreads();
+                for (int i = tid; i < SUB_N; i += NT)
+                    if (sm.sub_c[i]) { atomicAdd(&subc_row[i], sm.sub_c[i]); atomicAdd(&subm_row[i], sm.sub_m[i]); }
+            } else {  // R_COLLECT
+                uint32_t mine = 0;
+                double am = 0.0;
+                for (uint32_t q = tid; q < nst; q += NT) {
+                    const float y = scale_y<DT>(sm.u.st.x[q], pl.T);
+                    const uint32_t k = row_key(y, DT);
+                    if (k >= klo && k <= khi) mine++;
+                    else if (k > khi && k <= kahi) am += exp((double)y - md);
+                }
+                uint32_t total;
+                const uint32_t off = block_excl_scan<uint32_t>(mine, sm.red, &total);
+                if (tid == 0) sm.bu[2] = total ? atomicAdd(&rc->wcount, total) : 0u;
+                __syncthreads();
+                uint32_t pos = sm.bu[2] + off;
+                __syncthreads();
+                Elem *win = reinterpret_cast<Elem *>(a.ws + L.win) + (size_t)row * WCAP;
+                for (uint32_t q = tid; q < nst; q += NT) {
+                    const uint32_t k = row_key(scale_y<DT>(sm.u.st.x[q], pl.T), DT);
+                    if (k >= klo && k <= khi) {
+                        if (pos < (uint32_t)WCAP) {
+                            Elem el;
+                            el.key = k;
+                            el.idx = (int32_t)(base + (int64_t)sm.u.st.j[q]);
+                            win[pos] = el;
+                        }
+                        pos++;
+                    }
+                }
+                am = block_sum<double>(am, sm.red);
+                if (tid == 0) reinterpret_cast<double *>(a.ws + L.amass)[(size_t)row * G_MAX + chunk] = am;
+            }
+            (void)block_release_add(sm, &rc->rarrive, 1u);
+            if (!leader) {
+                if (rtype == R_COLLECT) break;  // no round follows a collect round
+                continue;
+            }
+            // ---- leader: wait for every workgroup's part, then decide
+            if (!block_wait_ge(sm, &rc->rarrive, G * seen, ctl)) { ok = false; break; }
+            if (rc->ovf != 0u || (rtype == R_COLLECT && rc->wcount > (uint32_t)WCAP)) {
+                // a buffer overflowed: release the followers, take the re-read path
+                if (tid == 0) rc->rtype = R_DONE;
+                (void)block_release_add(sm, &rc->round, 1u);
+                state = 2;
+                break;
+            }
+            if (rtype == R_COLLECT) { state = 3; break; }
+            state = topp_after_hist<DT>(sm, c, rc);  // publishes the next round
+            if (state != 0) break;
+        }
+        if (leader) {
+            if (!ok) write_row(ro, a, row, -1, ROW_INTERNAL, pl.mode, 0.0f, 0u, 0, 0.0);
+            else if (state == 1) write_row(ro, a, row, -1, MIS_ROW_INVALID, pl.mode, 0.0f, 0u, 0, 0.0);
+            else if (state == 2) {
+                const float m = rc->m;
+                __syncthreads();
+                if (tid == 0) c.m = m;
+                __syncthreads();
+                final_generic<DT>(sm, c, spl, ro, sa);
+            } else if (state == 3) {
+                final_topp_window<DT>(sm, c, spl, csr, rc, ro, sa);
+            }
+        }
+    } else if (leader) {
+        final_row<DT>(sm, c, spl, csr, ro, sa);
+    }
+
+    // ---- leave the row; the last workgroup out resets its control words
+    const uint32_t ex = block_release_add(sm, &rc->exited, 1u);
+    if (ex == G - 1u && tid == 0) {
+        rc->arrive = 0u; rc->round = 0u; rc->rarrive = 0u; rc->wcount = 0u; rc->rtype = 0u; rc->ovf = 0u;
+        fence_release();
+        rc->exited = 0u;
+    }
+}
+
+// ------------------------------------------------------------------ debug emit
 
 template <int DT>
-__global__ __launch_bounds__(K3_THREADS) void k_emit(const char *__restrict__ logits, int64_t V, int64_t stride_bytes,
-                                                     const mis_row_params *__restrict__ params, Layout L,
-                                                     const char *__restrict__ ws, float *__restrict__ out_probs,
-                                                     uint32_t *__restrict__ out_keep)
+__global__ __launch_bounds__(NT) void k_emit(const char *__restrict__ logits, int64_t V, int64_t stride_bytes,
+                                             const mis_row_params *__restrict__ params, Layout L,
+                                             const char *__restrict__ ws, float *__restrict__ out_probs,
+                                             uint32_t *__restrict__ out_keep)
 {
     constexpr int PER = 8;
     const int row = blockIdx.y;
@@ -1357,7 +1788,7 @@ __global__ __launch_bounds__(K3_THREADS) void k_emit(const char *__restrict__ lo
     const int64_t words = (V + 31) / 32;
     const double md = (double)ro.m;
     for (int it = 0; it < PER; ++it) {
-        const int64_t j = (int64_t)blockIdx.x * K3_THREADS * PER + (int64_t)it * K3_THREADS + threadIdx.x;
+        const int64_t j = (int64_t)blockIdx.x * NT * PER + (int64_t)it * NT + threadIdx.x;
         bool kept = false;
         float prob = 0.0f;
         if (j < V && ro.status == MIS_ROW_OK) {
@@ -1368,16 +1799,13 @@ __global__ __launch_bounds__(K3_THREADS) void k_emit(const char *__restrict__ lo
                 const float y = scale_y<DT>(load1<DT>(rowp, j), pl.T);
                 const uint32_t key = row_key(y, DT);
                 kept = (y != -INFINITY) && kept_by_cut(key, j, ro.cut_key, ro.cut_i);
-                if (kept) {
-                    const double q = exp((double)y - md) / ro.S;
-                    prob = rn_dtype((float)q, DT);
-                }
+                if (kept) prob = rn_dtype((float)(exp((double)y - md) / ro.S), DT);
             }
         }
         if (out_probs && j < V) out_probs[(size_t)row * V + j] = prob;
         const uint64_t ball = __ballot(kept);
         if (out_keep && (threadIdx.x & 63) == 0) {
-            const int64_t w0 = j / 32;  // j is a multiple of 64 for lane 0
+            const int64_t w0 = j / 32;
             if (w0 < words) out_keep[(size_t)row * words + w0] = (uint32_t)ball;
             if (w0 + 1 < words) out_keep[(size_t)row * words + w0 + 1] = (uint32_t)(ball >> 32);
         }
@@ -1389,44 +1817,37 @@ __global__ __launch_bounds__(K3_THREADS) void k_emit(const char *__restrict__ lo
 static thread_local int g_last_hip = 0;
 
 template <int DT, int EPT>
-static hipError_t launch_main(const void *logits, int64_t B, int64_t V, int64_t stride_bytes, int vec_ok,
-                              const mis_row_params *params, int64_t *ids, int32_t *status, const Layout &L,
-                              char *ws, hipStream_t st, void *const *events)
+static hipError_t launch_main(const Args &a, hipStream_t st, void *const *events)
 {
     hipError_t e;
     if (events && (e = hipEventRecord((hipEvent_t)events[0], st)) != hipSuccess) return e;
-    hipLaunchKernelGGL((k_chunk<DT, EPT>), dim3(L.G, (unsigned)B), dim3(K1_THREADS), 0, st,
-                       (const char *)logits, V, stride_bytes, vec_ok, params, L, ws);
+    const unsigned grid = (unsigned)(a.L.B * a.L.G);
+    hipLaunchKernelGGL((k_sample<DT, EPT>), dim3(grid), dim3(NT), 0, st, a);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
-    if (events && (e = hipEventRecord((hipEvent_t)events[1], st)) != hipSuccess) return e;
-    hipLaunchKernelGGL((k_final<DT>), dim3((unsigned)B), dim3(K2_THREADS), 0, st,
-                       (const char *)logits, V, stride_bytes, vec_ok, params, L, ws, ids, status);
-    e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    if (events) e = hipEventRecord((hipEvent_t)events[2], st);
+    if (events) e = hipEventRecord((hipEvent_t)events[1], st);
     return e;
 }
 
 template <int DT>
-static hipError_t launch_dt(const void *logits, int64_t B, int64_t V, int64_t stride_bytes, int vec_ok,
-                            const mis_row_params *params, int64_t *ids, int32_t *status, float *probs,
-                            uint32_t *keep, const Layout &L, char *ws, hipStream_t st, void *const *ev)
+static hipError_t launch_dt(const Args &a, float *probs, uint32_t *keep, hipStream_t st, void *const *ev)
 {
     hipError_t e;
-    switch (L.ept) {
-    case 64: e = launch_main<DT, 64>(logits, B, V, stride_bytes, vec_ok, params, ids, status, L, ws, st, ev); break;
-    case 32: e = launch_main<DT, 32>(logits, B, V, stride_bytes, vec_ok, params, ids, status, L, ws, st, ev); break;
-    case 16: e = launch_main<DT, 16>(logits, B, V, stride_bytes, vec_ok, params, ids, status, L, ws, st, ev); break;
-    default: e = launch_main<DT, 8>(logits, B, V, stride_bytes, vec_ok, params, ids, status, L, ws, st, ev); break;
+    switch (a.L.ept) {
+    case 64: e = launch_main<DT, 64>(a, st, ev); break;
+    case 32: e = launch_main<DT, 32>(a, st, ev); break;
+    case 16: e = launch_main<DT, 16>(a, st, ev); break;
+    default: e = launch_main<DT, 8>(a, st, ev); break;
     }
     if (e != hipSuccess) return e;
     if (probs || keep) {
-        const unsigned gx = (unsigned)((V + (int64_t)K3_THREADS * 8 - 1) / ((int64_t)K3_THREADS * 8));
-        hipLaunchKernelGGL((k_emit<DT>), dim3(gx, (unsigned)B), dim3(K3_THREADS), 0, st,
-                           (const char *)logits, V, stride_bytes, params, L, (const char *)ws, probs, keep);
+        const unsigned gx = (unsigned)((a.V + (int64_t)NT * 8 - 1) / ((int64_t)NT * 8));
+        hipLaunchKernelGGL((k_emit<DT>), dim3(gx, (unsigned)a.L.B), dim3(NT), 0, st, a.logits, a.V, a.stride_bytes,
+                           a.params, a.L, (const char *)a.ws, probs, keep);
         e = hipGetLastError();
+        if (e != hipSuccess) return e;
     }
+    if (ev) e = hipEventRecord((hipEvent_t)ev[2], st);
     return e;
 }
 
@@ -1438,7 +1859,16 @@ size_t mis_workspace_bytes(int64_t B, int64_t V, int dtype)
 {
     (void)dtype;
     if (B <= 0 || V <= 0) return 256;
-    return mis::make_layout(B, V).total;
+    return mis::make_layout(B, V, dtype).total;
+}
+
+int mis_workspace_init(void *workspace, size_t workspace_bytes, void *stream)
+{
+    if (!workspace) return MIS_ERR_INVALID_ARG;
+    if (((uintptr_t)workspace & 255u) != 0 || workspace_bytes < mis::CTL_PREFIX) return MIS_ERR_WORKSPACE;
+    const hipError_t e = hipMemsetAsync(workspace, 0, mis::CTL_PREFIX, (hipStream_t)stream);
+    if (e != hipSuccess) { mis::g_last_hip = (int)e; return MIS_ERR_HIP; }
+    return MIS_OK;
 }
 
 static int sample_impl(const void *logits, int dtype, int64_t B, int64_t V, int64_t row_stride,
@@ -1450,22 +1880,26 @@ static int sample_impl(const void *logits, int dtype, int64_t B, int64_t V, int6
     if (dtype < 0 || dtype > 2 || B < 0 || V <= 0 || row_stride < V) return MIS_ERR_INVALID_ARG;
     if (B == 0) return MIS_OK;
     if (!logits || !params || !out_ids || !workspace) return MIS_ERR_INVALID_ARG;
-    if (V > (int64_t)1 << 30 || B > 65535) return MIS_ERR_UNSUPPORTED;
-    const Layout L = make_layout(B, V);
-    if (L.G > G_MAX) return MIS_ERR_UNSUPPORTED;
+    if (V > (int64_t)1 << 30 || B > B_MAX) return MIS_ERR_UNSUPPORTED;
+    const Layout L = make_layout(B, V, dtype);
+    if (L.G > G_MAX || (int64_t)L.B * L.G > 0x7fffffff) return MIS_ERR_UNSUPPORTED;
     if (workspace_bytes < L.total || ((uintptr_t)workspace & 255u) != 0) return MIS_ERR_WORKSPACE;
     const int esz = dtype == MIS_DTYPE_F32 ? 4 : 2;
-    const int64_t stride_bytes = row_stride * esz;
-    const int vec_ok = (((uintptr_t)logits & 15u) == 0 && (stride_bytes & 15) == 0) ? 1 : 0;
+    Args a;
+    a.logits = (const char *)logits;
+    a.V = V;
+    a.stride_bytes = row_stride * esz;
+    a.vec_ok = (((uintptr_t)logits & 15u) == 0 && (a.stride_bytes & 15) == 0) ? 1 : 0;
+    a.params = params;
+    a.L = L;
+    a.ws = (char *)workspace;
+    a.out_ids = out_ids;
+    a.out_status = out_status;
     hipStream_t st = (hipStream_t)stream;
-    char *ws = (char *)workspace;
     hipError_t e;
-    if (dtype == MIS_DTYPE_F32)
-        e = launch_dt<F32>(logits, B, V, stride_bytes, vec_ok, params, out_ids, out_status, out_probs, out_keep, L, ws, st, events);
-    else if (dtype == MIS_DTYPE_F16)
-        e = launch_dt<F16>(logits, B, V, stride_bytes, vec_ok, params, out_ids, out_status, out_probs, out_keep, L, ws, st, events);
-    else
-        e = launch_dt<BF16>(logits, B, V, stride_bytes, vec_ok, params, out_ids, out_status, out_probs, out_keep, L, ws, st, events);
+    if (dtype == MIS_DTYPE_F32) e = launch_dt<F32>(a, out_probs, out_keep, st, events);
+    else if (dtype == MIS_DTYPE_F16) e = launch_dt<F16>(a, out_probs, out_keep, st, events);
+    else e = launch_dt<BF16>(a, out_probs, out_keep, st, events);
     if (e != hipSuccess) { g_last_hip = (int)e; return MIS_ERR_HIP; }
     return MIS_OK;
 }

@@ -91,6 +91,9 @@ class Sampler:
         ws = self._workspace.get(idx)
         if ws is None or ws.numel() < need:
             ws = torch.empty(need, dtype=torch.uint8, device=device)
+            # the kernels keep per-row arrival counters at the start of the
+            # workspace; they must start at zero and every call leaves them so
+            _native.workspace_init(ws.data_ptr(), ws.numel(), torch.cuda.current_stream(device).cuda_stream)
             self._workspace[idx] = ws
         return ws
 
@@ -151,6 +154,10 @@ class Sampler:
                 raise ValueError("invalid sampling parameters")
             if s == _native.ROW_INVALID:
                 raise RuntimeError("invalid probability distribution (NaN/inf logits or nothing left to sample)")
+            if s == _native.ROW_UNSUPPORTED:
+                raise NotImplementedError("fp16/bf16 logits with 1024 < top_k < V are not served by this build")
+            if s != _native.ROW_OK:
+                raise _native.MisError(f"sampler row status {s}")
         return ids.tolist()
 
     def sample(self, logits: torch.Tensor, sampling_params: SamplingParams) -> int:
