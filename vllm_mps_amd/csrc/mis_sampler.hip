@@ -1266,13 +1266,12 @@ __device__ __noinline__ void final_row(Smem &sm, RowCx &c, const RowPlan &pl, co
     uint32_t k2 = 0u;
     int32_t i2 = IDX_ALL;
     uint32_t anyflag = 0u;
-    float m = -INFINITY, xm = -INFINITY;
+    float m = -INFINITY;
     for (int g = tid; g < L.G; g += NT) {
         const ChunkSum s = csr[g];
         if (s.xkey > k2 || (s.xkey == k2 && s.xarg < i2)) { k2 = s.xkey; i2 = s.xarg; }
         anyflag |= s.flags;
         m = fmaxf(m, s.ymax);
-        xm = fmaxf(xm, s.xmax);
     }
     wave_argmax(k2, i2);
     if (lane_id() == 0) { sm.red.u[wave_id()] = k2; sm.red.l[wave_id()] = i2; }
@@ -1290,36 +1289,14 @@ __device__ __noinline__ void final_row(Smem &sm, RowCx &c, const RowPlan &pl, co
     __syncthreads();
     anyflag = block_sum<uint32_t>(anyflag ? 1u : 0u, sm.red);
     m = block_max<float>(m, sm.red);
-    xm = block_max<float>(xm, sm.red);
     c.m = m;
     const double md = (double)m;
     if (pl.mode == M_GREEDY) {
         write_row(ro, a, row, i2, MIS_ROW_OK, pl.mode, 0.0f, 0u, i2, 1.0);
     } else if (anyflag != 0u || m == -INFINITY) {
         write_row(ro, a, row, -1, MIS_ROW_INVALID, pl.mode, m, 0u, 0, 0.0);
-    } else if (pl.mode == M_TEMP && DT == F32) {
-        // chunk weights are exp((x - xmax_c)/T): rescale to the row's raw max
-        const double l2e_d = 1.4426950408889634 / (double)pl.T;
-        for (int g = tid; g < L.G; g += NT) {
-            sm.chs[g] = csr[g].xmax == -INFINITY ? 0.0 : exp2(((double)csr[g].xmax - (double)xm) * l2e_d);
-            sm.cw[g] = csr[g].S * sm.chs[g];
-        }
-        int gsel;
-        double resid, SK;
-        pick_chunk(sm, L.G, pl.u, &gsel, &resid, &SK);
-        int64_t id = -1;
-        if (gsel >= 0) {
-            const float l2e = (float)l2e_d;
-            const float xc = csr[gsel].xmax;
-            id = draw_in_chunk<DT>(sm, c, gsel, resid / sm.chs[gsel], [&](float xv, int64_t) -> double {
-                return (double)exp2f((xv - xc) * l2e);
-            });
-        }
-        // kept weights relative to m = scale(xm), for the debug probabilities
-        write_row(ro, a, row, id, id >= 0 ? MIS_ROW_OK : MIS_ROW_INVALID, pl.mode, m, row_key(-INFINITY, DT), -1,
-                  SK * exp((double)xm / (double)pl.T - md));
     } else if (pl.mode == M_TEMP) {
-        // fp16/bf16: chunk weights are exp(y - ymax_c): rescale to the row max m
+        // chunk weights are exp(y - ymax_c): rescale to the row max m
         for (int g = tid; g < L.G; g += NT) {
             sm.chs[g] = csr[g].ymax == -INFINITY ? 0.0 : exp((double)csr[g].ymax - md);
             sm.cw[g] = csr[g].S * sm.chs[g];
@@ -1552,19 +1529,11 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(3))) void k_
             ncand = NCAND_OVERFLOW;
         }
     } else if (live && pl.mode == M_TEMP) {
-        // draw weights in f32 (within the draw's tolerance), float64 sums.
-        // fp32: exp((x - xmax_c) / T), which equals exp(y - ymax_c) to a few
-        // ulp.  fp16/bf16: the scaled values are rounded to the dtype, so
-        // the weights are taken on them, exp(y - ymax_c).
+        // draw weights exp(y - ymax_c) in f32 on the scaled values y =
+        // dtype(x / T) (within the draw's tolerance), float64 sums.  Weights
+        // taken on x / T before its rounding would be off by |y| ulps.
         double s = 0.0;
-        if (DT == F32) {
-            const float l2e = (float)(1.4426950408889634 / (double)pl.T);
-            if (xmax != -INFINITY) {
-#pragma unroll
-                for (int i = 0; i < EPT; ++i)
-                    if (ok_(i)) s += (double)exp2f((x[i] - xmax) * l2e);
-            }
-        } else if (ymax != -INFINITY) {
+        if (ymax != -INFINITY) {
             constexpr float L2E = 1.44269504088896341f;
 #pragma unroll
             for (int i = 0; i < EPT; ++i)
