@@ -262,25 +262,57 @@ __device__ __forceinline__ float opaque(float v)
 
 // ------------------------------------------------------------------ cross-workgroup sync
 //
-// Release: every wave makes its own stores visible at agent scope (L2
-// write-back, wait for completion), then after the barrier one thread bumps
-// the counter.  Acquire: one thread observes the counter with an agent-scope
-// acquire load; every wave then invalidates its view before reading what
-// other workgroups wrote.
+// Everything one workgroup hands to another (chunk summaries, fine bins,
+// candidates, window elements, round parameters) is written and read with
+// device-coherent (agent-scope, relaxed) accesses: the stores write through
+// to the device coherence point and the loads never return a stale copy held
+// by this XCD's L2 or the CU's L1.  Publishing then needs only that every
+// wave has its own stores acknowledged (s_waitcnt) before the barrier that
+// precedes the counter bump; no L2 write-back or invalidate is issued.
 
-__device__ __forceinline__ void fence_acquire() { __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent"); }
-__device__ __forceinline__ void fence_release() { __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent"); }
-
-__device__ __forceinline__ uint32_t ld_acq(const uint32_t *p)
+template <class T> struct same_t { typedef T type; };
+template <class T> __device__ __forceinline__ void st_dev(T *p, typename same_t<T>::type v)
 {
-    return __hip_atomic_load(p, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+template <class T> __device__ __forceinline__ T ld_dev(const T *p)
+{
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_dev_elem(Elem *p, uint32_t key, int32_t idx)
+{
+    st_dev(reinterpret_cast<uint64_t *>(p), ((uint64_t)(uint32_t)idx << 32) | key);
+}
+__device__ __forceinline__ Elem ld_dev_elem(const Elem *p)
+{
+    const uint64_t v = ld_dev(reinterpret_cast<const uint64_t *>(p));
+    Elem e; e.key = (uint32_t)v; e.idx = (int32_t)(uint32_t)(v >> 32);
+    return e;
+}
+__device__ __forceinline__ void st_dev_cand(Cand *p, float x, int32_t idx)
+{
+    st_dev(reinterpret_cast<uint64_t *>(p), ((uint64_t)(uint32_t)idx << 32) | f32_bits(x));
+}
+__device__ __forceinline__ Cand ld_dev_cand(const Cand *p)
+{
+    const uint64_t v = ld_dev(reinterpret_cast<const uint64_t *>(p));
+    Cand c; c.x = bits_f32((uint32_t)v); c.idx = (int32_t)(uint32_t)(v >> 32);
+    return c;
+}
+// candidates a chunk wrote (its summary says so; never more than the buffer)
+__device__ __forceinline__ uint32_t ncand_of(const ChunkSum *cs)
+{
+    const uint32_t n = ld_dev(&cs->ncand);
+    return n < (uint32_t)CAND_CAP ? n : (uint32_t)CAND_CAP;
+}
+// this wave's memory operations are complete (stores acknowledged)
+__device__ __forceinline__ void wait_mem() { __builtin_amdgcn_s_waitcnt(0); }
 
 // one thread: wait until *p >= target; false on timeout
 __device__ bool spin_ge(const uint32_t *p, uint32_t target)
 {
     for (uint32_t it = 0; it < SPIN_MAX; ++it) {
-        if (ld_acq(p) >= target) return true;
+        if (ld_dev(p) >= target) return true;
         __builtin_amdgcn_s_sleep(1);
     }
     return false;
@@ -298,16 +330,15 @@ __device__ bool block_wait_ge(Smem &sm, const uint32_t *p, uint32_t target, Ctl 
     }
     __syncthreads();
     const bool ok = sm.bu[7] != 0u;
-    fence_acquire();
     __syncthreads();
     return ok;
 }
 
-// Whole block: publish the block's global writes, then add v to *p.  Returns
-// the old value to every thread.
+// Whole block: publish the block's device-coherent writes, then add v to
+// *p.  Returns the old value to every thread.
 __device__ uint32_t block_release_add(Smem &sm, uint32_t *p, uint32_t v)
 {
-    fence_release();
+    wait_mem();
     __syncthreads();
     if (threadIdx.x == 0) sm.bu[6] = atomicAdd(p, v);
     __syncthreads();
@@ -854,7 +885,7 @@ __device__ __noinline__ bool final_smallk(Smem &sm, const RowCx &c, const RowPla
 {
     const double md = (double)c.m;
     uint32_t ntot = 0;
-    for (int g = threadIdx.x; g < c.G; g += NT) ntot += cs[g].ncand;
+    for (int g = threadIdx.x; g < c.G; g += NT) ntot += ncand_of(&cs[g]);
     ntot = block_sum<uint32_t>(ntot, sm.red);
     // k'-th largest raw key over the candidates: 11 / 11 / 10-bit digits.  Fewer
     // candidates than k' means fewer finite elements than k' in the row.
@@ -870,10 +901,10 @@ __device__ __noinline__ bool final_smallk(Smem &sm, const RowCx &c, const RowPla
             for (int i = threadIdx.x; i < 2048; i += NT) sm.u.h11.cnt[i] = 0u;
             __syncthreads();
             for (int g = 0; g < c.G; ++g) {
-                const uint32_t n = cs[g].ncand;
+                const uint32_t n = ncand_of(&cs[g]);
                 const Cand *cg = cand + (size_t)g * CAND_CAP;
                 for (uint32_t i = threadIdx.x; i < n; i += NT) {
-                    const uint32_t k = key_of_f32(cg[i].x);
+                    const uint32_t k = key_of_f32(ld_dev_cand(&cg[i]).x);
                     if ((k & hmask) == (prefix & hmask)) atomicAdd(&sm.u.h11.cnt[(k >> sh) & (uint32_t)(nb - 1)], 1u);
                 }
             }
@@ -896,10 +927,10 @@ __device__ __noinline__ bool final_smallk(Smem &sm, const RowCx &c, const RowPla
     if (threadIdx.x == 0) sm.bu[3] = 0u;
     __syncthreads();
     for (int g = 0; g < c.G; ++g) {
-        const uint32_t n = cs[g].ncand;
+        const uint32_t n = ncand_of(&cs[g]);
         const Cand *cg = cand + (size_t)g * CAND_CAP;
         for (uint32_t i = threadIdx.x; i < n; i += NT) {
-            const Cand cd = cg[i];
+            const Cand cd = ld_dev_cand(&cg[i]);
             const float y = scale_y<DT>(cd.x, c.T);
             const uint32_t k = row_key(y, DT);
             if (k >= thr_key) {
@@ -1036,15 +1067,15 @@ __device__ __noinline__ void final_topp_window(Smem &sm, RowCx &c, const RowPlan
 {
     const Layout &L = a.L;
     const int tid = threadIdx.x, row = c.row;
-    const float mrow = rc->m;
+    const float mrow = ld_dev(&rc->m);
     const double md = (double)mrow;
     const double A = sm.bd[6], A_above = sm.bd[7];
     c.m = mrow;
-    const uint32_t nw0 = ld_acq(&rc->wcount);
+    const uint32_t nw0 = ld_dev(&rc->wcount);
     const uint32_t nw = nw0 < (uint32_t)WCAP ? nw0 : (uint32_t)WCAP;
     const Elem *win = reinterpret_cast<const Elem *>(a.ws + L.win) + (size_t)row * WCAP;
     for (uint32_t i = tid; i < nw; i += NT) {
-        const Elem el = win[i];
+        const Elem el = ld_dev_elem(&win[i]);
         sm.u.s.key[i] = el.key;
         sm.u.s.idx[i] = el.idx;
         sm.u.s.e[i] = exp((double)value_of_row_key(el.key, DT) - md);
@@ -1061,18 +1092,18 @@ __device__ __noinline__ void final_topp_window(Smem &sm, RowCx &c, const RowPlan
     // the window's row bin, as published with round 1 (deriving it from the
     // window's top key would be off by one for the bin just below zero,
     // whose top key is that of -0.0)
-    const double rbw = (double)rc->rbin;
+    const double rbw = (double)ld_dev(&rc->rbin);
     for (int g = tid; g < L.G; g += NT) {
         double w = 0.0;
-        if (csr[g].ymax != -INFINITY) {
-            const double off = gm - csr[g].gmc;
+        if (ld_dev(&csr[g].ymax) != -INFINITY) {
+            const double off = gm - ld_dev(&csr[g].gmc);
             for (int rb = 0; rb < (int)rbw && rb < FB_N; ++rb) {
                 const double cb = (double)rb - off;
-                if (cb >= 0.0) w += gmm[(size_t)g * FB_N + (int)cb];
+                if (cb >= 0.0) w += ld_dev(&gmm[(size_t)g * FB_N + (int)cb]);
             }
             w *= sm.chs[g];
         }
-        sm.cw[g] = w + amass[g];
+        sm.cw[g] = w + ld_dev(&amass[g]);
     }
     __syncthreads();
     for (uint32_t i = tid; i < nw; i += NT)
@@ -1103,7 +1134,7 @@ __device__ __forceinline__ int topp_plan(Smem &sm, RowCx &c, const RowPlan &pl, 
     const int tid = threadIdx.x;
     uint32_t anyflag = 0;
     float m = -INFINITY;
-    for (int g = tid; g < c.G; g += NT) { anyflag |= csr[g].flags; m = fmaxf(m, csr[g].ymax); }
+    for (int g = tid; g < c.G; g += NT) { anyflag |= ld_dev(&csr[g].flags); m = fmaxf(m, ld_dev(&csr[g].ymax)); }
     anyflag = block_sum<uint32_t>(anyflag ? 1u : 0u, sm.red);
     m = block_max<float>(m, sm.red);
     int state = 0;
@@ -1113,20 +1144,20 @@ __device__ __forceinline__ int topp_plan(Smem &sm, RowCx &c, const RowPlan &pl, 
     double S = 0.0, A = 0.0, A_above = 0.0;
     if (state == 0) {
         const double gm = floor(md * (double)FB_W);
-        for (int g = tid; g < c.G; g += NT) sm.chs[g] = exp((double)csr[g].ymax - md);
+        for (int g = tid; g < c.G; g += NT) sm.chs[g] = exp((double)ld_dev(&csr[g].ymax) - md);
         __syncthreads();
         double s = 0.0;
-        for (int g = tid; g < c.G; g += NT) if (csr[g].ymax != -INFINITY) s += csr[g].S * sm.chs[g];
+        for (int g = tid; g < c.G; g += NT) if (ld_dev(&csr[g].ymax) != -INFINITY) s += ld_dev(&csr[g].S) * sm.chs[g];
         S = block_sum<double>(s, sm.red);
         for (int rb = tid; rb < FB_N; rb += NT) {
             double mm = 0.0;
             uint32_t cc = 0;
             for (int g = 0; g < c.G; ++g) {
-                if (csr[g].ymax == -INFINITY) continue;
-                const double cb = (double)rb - (gm - csr[g].gmc);
-                if (cb >= 0.0) {
-                    mm += c.fbm[(size_t)g * FB_N + (int)cb] * sm.chs[g];
-                    cc += c.fbc[(size_t)g * FB_N + (int)cb];
+                if (ld_dev(&csr[g].ymax) == -INFINITY) continue;
+                const double cb = (double)rb - (gm - ld_dev(&csr[g].gmc));
+                if (cb >= 0.0 && cb < (double)FB_N) {
+                    mm += ld_dev(&c.fbm[(size_t)g * FB_N + (int)cb]) * sm.chs[g];
+                    cc += ld_dev(&c.fbc[(size_t)g * FB_N + (int)cb]);
                 }
             }
             sm.v.rb.m[FB_N - 1 - rb] = mm;
@@ -1160,17 +1191,18 @@ __device__ __forceinline__ int topp_plan(Smem &sm, RowCx &c, const RowPlan &pl, 
             const uint32_t klo = key_of_f32(lo);
             const uint32_t khi = key_of_f32(hi) - 1u;
             if (wcnt > (uint32_t)WCAP)
-                for (int i = tid; i < SUB_N; i += NT) { c.subc[i] = 0u; c.subm[i] = 0.0; }
+                for (int i = tid; i < SUB_N; i += NT) { st_dev(&c.subc[i], 0u); st_dev(&c.subm[i], 0.0); }
             if (tid == 0) {
-                rc->hlo = lo; rc->hhi = hi; rc->klo = klo; rc->khi = khi; rc->kahi = khi; rc->rbin = rbstar;
-                rc->wcount = 0u;
-                rc->rtype = wcnt > (uint32_t)WCAP ? R_HIST : R_COLLECT;
+                st_dev(&rc->hlo, lo); st_dev(&rc->hhi, hi); st_dev(&rc->klo, klo); st_dev(&rc->khi, khi);
+                st_dev(&rc->kahi, khi); st_dev(&rc->rbin, rbstar);
+                st_dev(&rc->wcount, 0u);
+                st_dev(&rc->rtype, wcnt > (uint32_t)WCAP ? R_HIST : R_COLLECT);
             }
         }
     }
     if (tid == 0) {
-        rc->m = m;
-        if (state != 0) rc->rtype = R_DONE;
+        st_dev(&rc->m, m);
+        if (state != 0) st_dev(&rc->rtype, R_DONE);
         sm.bd[5] = S; sm.bd[6] = A; sm.bd[7] = A_above;
     }
     (void)block_release_add(sm, &rc->round, 1u);  // publish round 1
@@ -1184,11 +1216,11 @@ template <int DT>
 __device__ __forceinline__ int topp_after_hist(Smem &sm, const RowCx &c, RowCtl *rc)
 {
     const int tid = threadIdx.x;
-    const uint32_t klo = rc->klo, khi = rc->khi;
-    const float hlo = rc->hlo, hhi = rc->hhi;
+    const uint32_t klo = ld_dev(&rc->klo), khi = ld_dev(&rc->khi);
+    const float hlo = ld_dev(&rc->hlo), hhi = ld_dev(&rc->hhi);
     const double A = sm.bd[6];
     double A_above = sm.bd[7];
-    for (int i = tid; i < SUB_N; i += NT) { sm.sub_m[SUB_N - 1 - i] = c.subm[i]; sm.sub_c[SUB_N - 1 - i] = c.subc[i]; }
+    for (int i = tid; i < SUB_N; i += NT) { sm.sub_m[SUB_N - 1 - i] = ld_dev(&c.subm[i]); sm.sub_c[SUB_N - 1 - i] = ld_dev(&c.subc[i]); }
     __syncthreads();
     if (wave_id() == 0) {
         double ab;
@@ -1244,8 +1276,11 @@ __device__ __forceinline__ int topp_after_hist(Smem &sm, const RowCx &c, RowCtl 
     const bool give_up = (scnt > (uint32_t)WCAP || skl > skh);
     __syncthreads();
     if (tid == 0) {
-        if (give_up) rc->rtype = R_DONE;
-        else { rc->rtype = R_COLLECT; rc->klo = skl; rc->khi = skh; rc->kahi = khi; rc->wcount = 0u; }
+        if (give_up) st_dev(&rc->rtype, R_DONE);
+        else {
+            st_dev(&rc->rtype, R_COLLECT); st_dev(&rc->klo, skl); st_dev(&rc->khi, skh); st_dev(&rc->kahi, khi);
+            st_dev(&rc->wcount, 0u);
+        }
     }
     (void)block_release_add(sm, &rc->round, 1u);
     return give_up ? 2 : 0;
@@ -1268,7 +1303,9 @@ __device__ __noinline__ void final_row(Smem &sm, RowCx &c, const RowPlan &pl, co
     uint32_t anyflag = 0u;
     float m = -INFINITY;
     for (int g = tid; g < L.G; g += NT) {
-        const ChunkSum s = csr[g];
+        ChunkSum s;
+        s.xkey = ld_dev(&csr[g].xkey); s.xarg = ld_dev(&csr[g].xarg);
+        s.flags = ld_dev(&csr[g].flags); s.ymax = ld_dev(&csr[g].ymax);
         if (s.xkey > k2 || (s.xkey == k2 && s.xarg < i2)) { k2 = s.xkey; i2 = s.xarg; }
         anyflag |= s.flags;
         m = fmaxf(m, s.ymax);
@@ -1298,8 +1335,9 @@ __device__ __noinline__ void final_row(Smem &sm, RowCx &c, const RowPlan &pl, co
     } else if (pl.mode == M_TEMP) {
         // chunk weights are exp(y - ymax_c): rescale to the row max m
         for (int g = tid; g < L.G; g += NT) {
-            sm.chs[g] = csr[g].ymax == -INFINITY ? 0.0 : exp((double)csr[g].ymax - md);
-            sm.cw[g] = csr[g].S * sm.chs[g];
+            const float yg = ld_dev(&csr[g].ymax);
+            sm.chs[g] = yg == -INFINITY ? 0.0 : exp((double)yg - md);
+            sm.cw[g] = ld_dev(&csr[g].S) * sm.chs[g];
         }
         int gsel;
         double resid, SK;
@@ -1307,7 +1345,7 @@ __device__ __noinline__ void final_row(Smem &sm, RowCx &c, const RowPlan &pl, co
         int64_t id = -1;
         if (gsel >= 0) {
             constexpr float L2E = 1.44269504088896341f;
-            const float yc = csr[gsel].ymax, T = pl.T;
+            const float yc = ld_dev(&csr[gsel].ymax), T = pl.T;
             id = draw_in_chunk<DT>(sm, c, gsel, resid / sm.chs[gsel], [&](float xv, int64_t) -> double {
                 return (double)exp2f((scale_y<DT>(xv, T) - yc) * L2E);
             });
@@ -1315,7 +1353,7 @@ __device__ __noinline__ void final_row(Smem &sm, RowCx &c, const RowPlan &pl, co
         write_row(ro, a, row, id, id >= 0 ? MIS_ROW_OK : MIS_ROW_INVALID, pl.mode, m, row_key(-INFINITY, DT), -1, SK);
     } else if (pl.mode == M_SMALLK) {
         bool ovf = false;
-        for (int g = 0; g < L.G; ++g) ovf |= (csr[g].ncand == NCAND_OVERFLOW);
+        for (int g = 0; g < L.G; ++g) ovf |= (ld_dev(&csr[g].ncand) == NCAND_OVERFLOW);
         const Cand *cand = reinterpret_cast<const Cand *>(a.ws + L.cand) + (size_t)row * L.G * CAND_CAP;
         bool done = false;
         if (!ovf) done = final_smallk<DT>(sm, c, pl, csr, cand, ro, a);
@@ -1520,8 +1558,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(3))) void k_
 #pragma unroll
             for (int i = 0; i < EPT; ++i) {
                 if (ok_(i) && x[i] != -INFINITY && x[i] >= xlo_c) {
-                    Cand cd; cd.x = x[i]; cd.idx = idx_of(i);
-                    cand[off++] = cd;
+                    st_dev_cand(&cand[off++], x[i], idx_of(i));
                 }
             }
             ncand = total;
@@ -1572,7 +1609,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(3))) void k_
         below = block_sum<double>(bl, sm.red);
         uint32_t *gc = reinterpret_cast<uint32_t *>(a.ws + L.fbc) + ((size_t)row * L.G + chunk) * FB_N;
         double *gm = reinterpret_cast<double *>(a.ws + L.fbm) + ((size_t)row * L.G + chunk) * FB_N;
-        for (int i = tid; i < FB_N; i += NT) { gc[i] = sm.u.p1.cnt[i]; gm[i] = sm.u.p1.mass[i]; }
+        for (int i = tid; i < FB_N; i += NT) { st_dev(&gc[i], sm.u.p1.cnt[i]); st_dev(&gm[i], sm.u.p1.mass[i]); }
     } else if (live) {
         // large k' and fp16/bf16 top-p: the leader re-reads the row
         double s = 0.0;
@@ -1589,14 +1626,14 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(3))) void k_
         Sc = block_sum<double>(s, sm.red);
     }
     if (tid == 0) {
-        cs->xkey = bk; cs->xarg = bi; cs->ymax = ymax; cs->flags = flags; cs->ncand = ncand;
-        cs->xmax = xmax; cs->S = Sc; cs->gmc = gmc; cs->below = below;
+        st_dev(&cs->xkey, bk); st_dev(&cs->xarg, bi); st_dev(&cs->ymax, ymax); st_dev(&cs->flags, flags);
+        st_dev(&cs->ncand, ncand); st_dev(&cs->xmax, xmax); st_dev(&cs->S, Sc); st_dev(&cs->gmc, gmc);
+        st_dev(&cs->below, below);
     }
 
     // ---- arrive; the last arrival leads the row
     const uint32_t old = block_release_add(sm, &rc->arrive, 1u);
     const bool leader = (old == G - 1u);
-    if (leader) fence_acquire();
     __syncthreads();
 
     // the row context in LDS is filled in the leader only: code that every
@@ -1625,11 +1662,11 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(3))) void k_
         for (;;) {
             if (!block_wait_ge(sm, &rc->round, seen + 1u, ctl)) { ok = false; break; }
             seen += 1u;
-            const uint32_t rtype = rc->rtype;
+            const uint32_t rtype = ld_dev(&rc->rtype);
             if (rtype == R_DONE) break;
-            const uint32_t klo = rc->klo, khi = rc->khi, kahi = rc->kahi;
-            const float hlo = rc->hlo, hhi = rc->hhi;
-            const double md = (double)rc->m;
+            const uint32_t klo = ld_dev(&rc->klo), khi = ld_dev(&rc->khi), kahi = ld_dev(&rc->kahi);
+            const float hlo = ld_dev(&rc->hlo), hhi = ld_dev(&rc->hhi);
+            const double md = (double)ld_dev(&rc->m);
             uint32_t xlo, xhi;
             x_interval<DT>(sm, klo, kahi, pl.T, &xlo, &xhi);
             // stage the few elements whose raw key can map into the round's
@@ -1686,16 +1723,13 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(3))) void k_
                     const uint32_t k = row_key(scale_y<DT>(sm.u.st.x[q], pl.T), DT);
                     if (k >= klo && k <= khi) {
                         if (pos < (uint32_t)WCAP) {
-                            Elem el;
-                            el.key = k;
-                            el.idx = (int32_t)(base + (int64_t)sm.u.st.j[q]);
-                            win[pos] = el;
+                            st_dev_elem(&win[pos], k, (int32_t)(base + (int64_t)sm.u.st.j[q]));
                         }
                         pos++;
                     }
                 }
                 am = block_sum<double>(am, sm.red);
-                if (tid == 0) reinterpret_cast<double *>(a.ws + L.amass)[(size_t)row * G_MAX + chunk] = am;
+                if (tid == 0) st_dev(reinterpret_cast<double *>(a.ws + L.amass) + (size_t)row * G_MAX + chunk, am);
             }
             (void)block_release_add(sm, &rc->rarrive, 1u);
             if (!leader) {
@@ -1704,9 +1738,9 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(3))) void k_
             }
             // ---- leader: wait for every workgroup's part, then decide
             if (!block_wait_ge(sm, &rc->rarrive, G * seen, ctl)) { ok = false; break; }
-            if (rc->ovf != 0u || (rtype == R_COLLECT && rc->wcount > (uint32_t)WCAP)) {
+            if (ld_dev(&rc->ovf) != 0u || (rtype == R_COLLECT && ld_dev(&rc->wcount) > (uint32_t)WCAP)) {
                 // a buffer overflowed: release the followers, take the re-read path
-                if (tid == 0) rc->rtype = R_DONE;
+                if (tid == 0) st_dev(&rc->rtype, R_DONE);
                 (void)block_release_add(sm, &rc->round, 1u);
                 state = 2;
                 break;
@@ -1719,7 +1753,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(3))) void k_
             if (!ok) write_row(ro, a, row, -1, ROW_INTERNAL, pl.mode, 0.0f, 0u, 0, 0.0);
             else if (state == 1) write_row(ro, a, row, -1, MIS_ROW_INVALID, pl.mode, 0.0f, 0u, 0, 0.0);
             else if (state == 2) {
-                const float m = rc->m;
+                const float m = ld_dev(&rc->m);
                 __syncthreads();
                 if (tid == 0) c.m = m;
                 __syncthreads();
@@ -1735,9 +1769,8 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(3))) void k_
     // ---- leave the row; the last workgroup out resets its control words
     const uint32_t ex = block_release_add(sm, &rc->exited, 1u);
     if (ex == G - 1u && tid == 0) {
-        rc->arrive = 0u; rc->round = 0u; rc->rarrive = 0u; rc->wcount = 0u; rc->rtype = 0u; rc->ovf = 0u;
-        fence_release();
-        rc->exited = 0u;
+        st_dev(&rc->arrive, 0u); st_dev(&rc->round, 0u); st_dev(&rc->rarrive, 0u); st_dev(&rc->wcount, 0u);
+        st_dev(&rc->rtype, 0u); st_dev(&rc->ovf, 0u); st_dev(&rc->exited, 0u);
     }
 }
 
