@@ -113,8 +113,9 @@ int mis_sample(const void *logits, int dtype, int64_t B, int64_t V, int64_t row_
 
 /*
  * Instrumented mis_sample(): identical results, and additionally records the
- * caller's hipEvent_t handles events[0] before the sampling kernel, events[1]
- * after it and events[2] after the optional debug emit, all on `stream`.  No counterpart in the reference: it exists so benchmarks can
+ * caller's hipEvent_t handles events[0] before the chunk pass, events[1]
+ * between the chunk pass and the row pass, events[2] after the row pass, all
+ * on `stream`.  No counterpart in the reference: it exists so benchmarks can
  * time each kernel on the stream it runs on.
  */
 int mis_sample_profiled(const void *logits, int dtype, int64_t B, int64_t V, int64_t row_stride,

@@ -55,12 +55,10 @@ constexpr int TIE_CAP = 2048;
 constexpr int STAGE_CAP = 4096;      // elements one workgroup stages per round
 constexpr uint32_t NCAND_OVERFLOW = 0xffffffffu;
 constexpr int32_t IDX_ALL = 0x7fffffff;
-constexpr uint32_t SPIN_MAX = 1u << 22;  // bounded waits (well under a second)
 
 enum : int { M_BAD = 0, M_GREEDY = 1, M_SMALLK = 2, M_LARGEK = 3, M_TOPP = 4, M_TEMP = 5 };
 enum : uint32_t { FLAG_NAN = 1u, FLAG_PINF = 2u };
 enum : uint32_t { R_COLLECT = 1u, R_HIST = 2u, R_DONE = 3u };
-constexpr int ROW_INTERNAL = MIS_ROW_INTERNAL;
 
 // ------------------------------------------------------------------ workspace
 
@@ -134,11 +132,10 @@ static Layout make_layout(int64_t B, int64_t V, int dtype)
 {
     Layout L;
     L.B = B; L.V = V;
-    // fp32 chunks hold at most 32 elements per thread: with 64 the fp32
-    // top-p refinement rounds exceed the register budget of three waves/SIMD
+    (void)dtype;
     static const int opts[4] = {64, 32, 16, 8};
     L.ept = 8;
-    for (int i = dtype == MIS_DTYPE_F32 ? 1 : 0; i < 4; ++i) {
+    for (int i = 0; i < 4; ++i) {
         const int64_t G = (V + (int64_t)NT * opts[i] - 1) / ((int64_t)NT * opts[i]);
         if (B * G >= 1024 && G <= G_MAX) { L.ept = opts[i]; break; }
     }
@@ -247,6 +244,18 @@ struct Smem {
     RowPlan pl;                // memory, which would otherwise hold a copy per lane)
 };
 
+// LDS of the chunk pass: only what its per-mode reductions need, so that
+// several workgroups fit on a CU
+struct ChunkSmem {
+    union {
+        struct { uint32_t cnt[FB_N]; double mass[FB_N]; } p1;  // fine bins (fp32 top-p)
+        struct { uint32_t cnt[256]; double mass[256]; } h8;    // candidate threshold histogram
+    } u;
+    Red red;
+    uint32_t bu[8];
+    int32_t bi[8];
+};
+
 __device__ __forceinline__ bool kept_by_cut(uint32_t key, int64_t j, uint32_t cut_key, int32_t cut_i)
 {
     return key > cut_key || (key == cut_key && j <= (int64_t)cut_i);
@@ -260,35 +269,15 @@ __device__ __forceinline__ float opaque(float v)
     return v;
 }
 
-// ------------------------------------------------------------------ cross-workgroup sync
+// ------------------------------------------------------------------ chunk -> row hand-off
 //
-// Everything one workgroup hands to another (chunk summaries, fine bins,
-// candidates, window elements, round parameters) is written and read with
-// device-coherent (agent-scope, relaxed) accesses: the stores write through
-// to the device coherence point and the loads never return a stale copy held
-// by this XCD's L2 or the CU's L1.  Publishing then needs only that every
-// wave has its own stores acknowledged (s_waitcnt) before the barrier that
-// precedes the counter bump; no L2 write-back or invalidate is issued.
+// The chunk pass (k_chunk) writes per-chunk summaries, fine bins and
+// candidates; the row pass (k_final) reads them in the next launch on the
+// same stream, so the kernel boundary orders and publishes them.
 
 template <class T> struct same_t { typedef T type; };
-template <class T> __device__ __forceinline__ void st_dev(T *p, typename same_t<T>::type v)
-{
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-template <class T> __device__ __forceinline__ T ld_dev(const T *p)
-{
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void st_dev_elem(Elem *p, uint32_t key, int32_t idx)
-{
-    st_dev(reinterpret_cast<uint64_t *>(p), ((uint64_t)(uint32_t)idx << 32) | key);
-}
-__device__ __forceinline__ Elem ld_dev_elem(const Elem *p)
-{
-    const uint64_t v = ld_dev(reinterpret_cast<const uint64_t *>(p));
-    Elem e; e.key = (uint32_t)v; e.idx = (int32_t)(uint32_t)(v >> 32);
-    return e;
-}
+template <class T> __device__ __forceinline__ void st_dev(T *p, typename same_t<T>::type v) { *p = v; }
+template <class T> __device__ __forceinline__ T ld_dev(const T *p) { return *p; }
 __device__ __forceinline__ void st_dev_cand(Cand *p, float x, int32_t idx)
 {
     st_dev(reinterpret_cast<uint64_t *>(p), ((uint64_t)(uint32_t)idx << 32) | f32_bits(x));
@@ -305,50 +294,9 @@ __device__ __forceinline__ uint32_t ncand_of(const ChunkSum *cs)
     const uint32_t n = ld_dev(&cs->ncand);
     return n < (uint32_t)CAND_CAP ? n : (uint32_t)CAND_CAP;
 }
-// this wave's memory operations are complete (stores acknowledged)
-__device__ __forceinline__ void wait_mem() { __builtin_amdgcn_s_waitcnt(0); }
-
-// one thread: wait until *p >= target; false on timeout
-__device__ bool spin_ge(const uint32_t *p, uint32_t target)
-{
-    for (uint32_t it = 0; it < SPIN_MAX; ++it) {
-        if (ld_dev(p) >= target) return true;
-        __builtin_amdgcn_s_sleep(1);
-    }
-    return false;
-}
-
-// Whole block: wait until *p >= target.  False on timeout (also recorded in
-// the control block).
-__device__ bool block_wait_ge(Smem &sm, const uint32_t *p, uint32_t target, Ctl *ctl)
-{
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const bool ok = spin_ge(p, target);
-        if (!ok) atomicOr(&ctl->error, 1u);
-        sm.bu[7] = ok ? 1u : 0u;
-    }
-    __syncthreads();
-    const bool ok = sm.bu[7] != 0u;
-    __syncthreads();
-    return ok;
-}
-
-// Whole block: publish the block's device-coherent writes, then add v to
-// *p.  Returns the old value to every thread.
-__device__ uint32_t block_release_add(Smem &sm, uint32_t *p, uint32_t v)
-{
-    wait_mem();
-    __syncthreads();
-    if (threadIdx.x == 0) sm.bu[6] = atomicAdd(p, v);
-    __syncthreads();
-    const uint32_t old = sm.bu[6];
-    __syncthreads();
-    return old;
-}
 
 // raw-key interval for a scaled-key interval, computed by wave 0
-template <int DT> __device__ void x_interval(Smem &sm, uint32_t klo, uint32_t khi, float T, uint32_t *xlo, uint32_t *xhi)
+template <int DT, class S> __device__ void x_interval(S &sm, uint32_t klo, uint32_t khi, float T, uint32_t *xlo, uint32_t *xhi)
 {
     __syncthreads();
     if (wave_id() == 0) {
@@ -386,16 +334,35 @@ __device__ void write_row(RowOut *ro, const Args &a, int row, int64_t id, int st
 template <int DT, class WF>
 __device__ int64_t draw_in_chunk(Smem &sm, const RowCx &c, int g, double resid, WF &&wfun)
 {
+    // Thread t takes the contiguous elements [cbeg + t*per, cbeg + (t+1)*per)
+    // of the chunk, loaded up front (16-byte vectors where aligned), so the
+    // weights are computed from registers in both passes.
+    constexpr int VEC = Traits<DT>::VEC, MAXPER = 64;
     const int64_t cbeg = (int64_t)g * c.CH;
     const int64_t cend = cbeg + c.CH < c.V ? cbeg + c.CH : c.V;
-    const int64_t per = (c.CH + NT - 1) / NT;
+    const int per = (int)(c.CH / NT);  // 8..64, a multiple of VEC
     const int64_t jb = cbeg + (int64_t)threadIdx.x * per;
-    const int64_t je = jb + per < cend ? jb + per : cend;
+    float xs[MAXPER];
+#pragma unroll
+    for (int v = 0; v < MAXPER / VEC; ++v) {
+        if (v * VEC < per) {
+            const int64_t j0 = jb + (int64_t)v * VEC;
+            if (c.vec_ok && j0 + VEC <= cend) {
+                loadvec<DT>(c.rowp, j0, &xs[v * VEC]);
+            } else {
+#pragma unroll
+                for (int e = 0; e < VEC; ++e) xs[v * VEC + e] = (j0 + e < cend) ? load1<DT>(c.rowp, j0 + e) : 0.0f;
+            }
+        }
+    }
     double local = 0.0;
     int64_t lastk = -1;
-    for (int64_t j = jb; j < je; ++j) {
-        const double w = wfun(load1<DT>(c.rowp, j), j);
-        if (w > 0.0) { local += w; lastk = j; }
+#pragma unroll
+    for (int i = 0; i < MAXPER; ++i) {
+        if (i < per && jb + i < cend) {
+            const double w = wfun(xs[i], jb + i);
+            if (w > 0.0) { local += w; lastk = jb + i; }
+        }
     }
     double tot;
     const double before = block_excl_scan<double>(local, sm.red, &tot);
@@ -404,11 +371,15 @@ __device__ int64_t draw_in_chunk(Smem &sm, const RowCx &c, int g, double resid, 
     if (local > 0.0 && before <= resid && resid < before + local) {
         double run = before;
         int64_t pick = lastk;
-        for (int64_t j = jb; j < je; ++j) {
-            const double w = wfun(load1<DT>(c.rowp, j), j);
-            if (w > 0.0) {
-                run += w;
-                if (run > resid) { pick = j; break; }
+        bool done = false;
+#pragma unroll
+        for (int i = 0; i < MAXPER; ++i) {
+            if (!done && i < per && jb + i < cend) {
+                const double w = wfun(xs[i], jb + i);
+                if (w > 0.0) {
+                    run += w;
+                    if (run > resid) { pick = jb + i; done = true; }
+                }
             }
         }
         atomicMin(&sm.bq[0], (unsigned long long)pick);
@@ -884,28 +855,57 @@ __device__ __noinline__ bool final_smallk(Smem &sm, const RowCx &c, const RowPla
                                           const Cand *cand, RowOut *ro, const Args &a)
 {
     const double md = (double)c.m;
-    uint32_t ntot = 0;
-    for (int g = threadIdx.x; g < c.G; g += NT) ntot += ncand_of(&cs[g]);
-    ntot = block_sum<uint32_t>(ntot, sm.red);
+    // candidate counts -> prefix offsets (thread 0, G <= 256); candidate f of
+    // the row is candidate f - pre[g] of the chunk g with pre[g] <= f < pre[g+1]
+    uint32_t *pre = reinterpret_cast<uint32_t *>(sm.chs);
+    for (int g = threadIdx.x; g < c.G; g += NT) sm.sub_c[g] = ncand_of(&cs[g]);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t run = 0;
+        for (int g = 0; g < c.G; ++g) { pre[g] = run; run += sm.sub_c[g]; }
+        pre[c.G] = run;
+    }
+    __syncthreads();
+    const uint32_t ntot = pre[c.G];
+    const int G = c.G;
+    auto cand_ptr = [&](uint32_t f) -> const Cand * {
+        int lo = 0, hi = G - 1;  // last g with pre[g] <= f
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (pre[mid] <= f) lo = mid; else hi = mid - 1;
+        }
+        return cand + (size_t)lo * CAND_CAP + (f - pre[lo]);
+    };
+    constexpr int BATCH = 8;  // candidate loads in flight per thread
     // k'-th largest raw key over the candidates: 11 / 11 / 10-bit digits.  Fewer
     // candidates than k' means fewer finite elements than k' in the row.
     uint32_t xk_thr = 0u;
     if (ntot >= (uint32_t)pl.kk) {
         uint32_t prefix = 0u, rem = (uint32_t)pl.kk;
-        const int shifts[3] = {21, 10, 0};
-        const int bits[3] = {11, 11, 10};
         for (int lev = 0; lev < 3; ++lev) {
-            const int sh = shifts[lev], nb = 1 << bits[lev];
-            const uint32_t hmask = lev == 0 ? 0u : ~((1u << (sh + bits[lev])) - 1u);
+            const int sh = lev == 0 ? 21 : (lev == 1 ? 10 : 0);
+            const int nbits = lev == 2 ? 10 : 11;
+            const int nb = 1 << nbits;
+            const uint32_t hmask = lev == 0 ? 0u : ~((1u << (sh + nbits)) - 1u);
             __syncthreads();
             for (int i = threadIdx.x; i < 2048; i += NT) sm.u.h11.cnt[i] = 0u;
             __syncthreads();
-            for (int g = 0; g < c.G; ++g) {
-                const uint32_t n = ncand_of(&cs[g]);
-                const Cand *cg = cand + (size_t)g * CAND_CAP;
-                for (uint32_t i = threadIdx.x; i < n; i += NT) {
-                    const uint32_t k = key_of_f32(ld_dev_cand(&cg[i]).x);
-                    if ((k & hmask) == (prefix & hmask)) atomicAdd(&sm.u.h11.cnt[(k >> sh) & (uint32_t)(nb - 1)], 1u);
+            for (uint32_t f0 = 0; f0 < ntot; f0 += NT * BATCH) {
+                // addresses first (LDS reads), then the loads back to back
+                const Cand *cp[BATCH];
+#pragma unroll
+                for (int u = 0; u < BATCH; ++u) {
+                    const uint32_t f = f0 + (uint32_t)(u * NT) + threadIdx.x;
+                    cp[u] = cand_ptr(f < ntot ? f : 0u);
+                }
+                uint32_t kv[BATCH];
+#pragma unroll
+                for (int u = 0; u < BATCH; ++u) kv[u] = key_of_f32(ld_dev_cand(cp[u]).x);
+#pragma unroll
+                for (int u = 0; u < BATCH; ++u) {
+                    const uint32_t f = f0 + (uint32_t)(u * NT) + threadIdx.x;
+                    if (f < ntot && (kv[u] & hmask) == (prefix & hmask))
+                        atomicAdd(&sm.u.h11.cnt[(kv[u] >> sh) & (uint32_t)(nb - 1)], 1u);
                 }
             }
             __syncthreads();
@@ -926,16 +926,26 @@ __device__ __noinline__ bool final_smallk(Smem &sm, const RowCx &c, const RowPla
     const uint32_t thr_key = xk_thr ? row_key(scale_y<DT>(f32_of_key(xk_thr), c.T), DT) : 0u;
     if (threadIdx.x == 0) sm.bu[3] = 0u;
     __syncthreads();
-    for (int g = 0; g < c.G; ++g) {
-        const uint32_t n = ncand_of(&cs[g]);
-        const Cand *cg = cand + (size_t)g * CAND_CAP;
-        for (uint32_t i = threadIdx.x; i < n; i += NT) {
-            const Cand cd = ld_dev_cand(&cg[i]);
-            const float y = scale_y<DT>(cd.x, c.T);
-            const uint32_t k = row_key(y, DT);
-            if (k >= thr_key) {
-                const uint32_t p = atomicAdd(&sm.bu[3], 1u);
-                if (p < (uint32_t)SURV_CAP) { sm.u.s.key[p] = k; sm.u.s.idx[p] = cd.idx; sm.u.s.e[p] = exp((double)y - md); }
+    for (uint32_t f0 = 0; f0 < ntot; f0 += NT * BATCH) {
+        const Cand *cp[BATCH];
+#pragma unroll
+        for (int u = 0; u < BATCH; ++u) {
+            const uint32_t f = f0 + (uint32_t)(u * NT) + threadIdx.x;
+            cp[u] = cand_ptr(f < ntot ? f : 0u);
+        }
+        Cand cv[BATCH];
+#pragma unroll
+        for (int u = 0; u < BATCH; ++u) cv[u] = ld_dev_cand(cp[u]);
+#pragma unroll
+        for (int u = 0; u < BATCH; ++u) {
+            const uint32_t f = f0 + (uint32_t)(u * NT) + threadIdx.x;
+            if (f < ntot) {
+                const float y = scale_y<DT>(cv[u].x, c.T);
+                const uint32_t k = row_key(y, DT);
+                if (k >= thr_key) {
+                    const uint32_t p = atomicAdd(&sm.bu[3], 1u);
+                    if (p < (uint32_t)SURV_CAP) { sm.u.s.key[p] = k; sm.u.s.idx[p] = cv[u].idx; sm.u.s.e[p] = exp((double)y - md); }
+                }
             }
         }
     }
@@ -1057,61 +1067,211 @@ __device__ __noinline__ bool final_smallk(Smem &sm, const RowCx &c, const RowPla
     return true;
 }
 
-// fp32 top-p, after the collect round: the exact cut inside the window
-// (mass descent over the collected keys), per-chunk kept weights, the draw.
-// sm.bd[6] = A (top_p * S), sm.bd[7] = mass above the window, sm.chs[] the
-// per-chunk rescale, all set by the leader before the rounds.
+// fp32 top-p.  Merge the chunks' fine bins (16 per unit of y below each
+// chunk max, float64 masses) on the row grid and find the bin holding the
+// cut.  Re-read the row -- it has just been read, so it comes from the
+// Infinity Cache -- to collect that bin's elements into LDS, histogramming
+// the bin first (256 sub-bins) when it is crowded.  The exact cut is then a
+// mass descent over at most SURV_CAP elements.  Per-chunk kept weights: the
+// chunk's whole bins above the window plus its part of the window.
 template <int DT>
-__device__ __noinline__ void final_topp_window(Smem &sm, RowCx &c, const RowPlan &pl, const ChunkSum *csr,
-                                               const RowCtl *rc, RowOut *ro, const Args &a)
+__device__ __noinline__ void final_topp32(Smem &sm, RowCx &c, const RowPlan &pl, const ChunkSum *csr, RowOut *ro,
+                                          const Args &a)
 {
-    const Layout &L = a.L;
-    const int tid = threadIdx.x, row = c.row;
-    const float mrow = ld_dev(&rc->m);
-    const double md = (double)mrow;
-    const double A = sm.bd[6], A_above = sm.bd[7];
-    c.m = mrow;
-    const uint32_t nw0 = ld_dev(&rc->wcount);
-    const uint32_t nw = nw0 < (uint32_t)WCAP ? nw0 : (uint32_t)WCAP;
-    const Elem *win = reinterpret_cast<const Elem *>(a.ws + L.win) + (size_t)row * WCAP;
-    for (uint32_t i = tid; i < nw; i += NT) {
-        const Elem el = ld_dev_elem(&win[i]);
-        sm.u.s.key[i] = el.key;
-        sm.u.s.idx[i] = el.idx;
-        sm.u.s.e[i] = exp((double)value_of_row_key(el.key, DT) - md);
+    const int tid = threadIdx.x, G = c.G;
+    uint32_t anyflag = 0;
+    float m = -INFINITY;
+    for (int g = tid; g < G; g += NT) { anyflag |= csr[g].flags; m = fmaxf(m, csr[g].ymax); }
+    anyflag = block_sum<uint32_t>(anyflag ? 1u : 0u, sm.red);
+    m = block_max<float>(m, sm.red);
+    c.m = m;
+    if (anyflag != 0u || m == -INFINITY) {
+        write_row(ro, a, c.row, -1, MIS_ROW_INVALID, pl.mode, m, 0u, 0, 0.0);
+        return;
+    }
+    const double md = (double)m;
+    const double gm = floor(md * (double)FB_W);
+    // chunk g's bin 0 sits offg[g] row bins below the row's bin 0 (-1: empty chunk)
+    int *offg = reinterpret_cast<int *>(sm.sub_c);
+    for (int g = tid; g < G; g += NT) {
+        const float yg = csr[g].ymax;
+        sm.chs[g] = yg == -INFINITY ? 0.0 : exp((double)yg - md);
+        offg[g] = yg == -INFINITY ? -1 : (int)(gm - csr[g].gmc);
     }
     __syncthreads();
+    double s = 0.0;
+    for (int g = tid; g < G; g += NT) if (offg[g] >= 0) s += csr[g].S * sm.chs[g];
+    const double S = block_sum<double>(s, sm.red);
+    const double A = (double)pl.top_p * S;
+    for (int rb = tid; rb < FB_N; rb += NT) {
+        double mm = 0.0;
+        uint32_t cc = 0;
+        for (int g0 = 0; g0 < G; g0 += 8) {
+            int off[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) off[u] = g0 + u < G ? offg[g0 + u] : -1;
+            double mv[8];
+            uint32_t cv[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int cb = rb - off[u];
+                const bool in = off[u] >= 0 && cb >= 0 && cb < FB_N;
+                const size_t at = (size_t)(g0 + u < G ? g0 + u : 0) * FB_N + (in ? cb : 0);
+                mv[u] = in ? c.fbm[at] : 0.0;
+                cv[u] = in ? c.fbc[at] : 0u;
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) { mm += mv[u] * (g0 + u < G ? sm.chs[g0 + u] : 0.0); cc += cv[u]; }
+        }
+        sm.v.rb.m[FB_N - 1 - rb] = mm;
+        sm.v.rb.c[FB_N - 1 - rb] = cc;
+    }
+    __syncthreads();
+    if (wave_id() == 0) {
+        double ab;
+        const int d = wave_find_desc<double>(sm.v.rb.m, FB_N, A, &ab);
+        double tot = 0.0;
+        for (int q = lane_id(); q < FB_N; q += 64) tot += sm.v.rb.m[q];
+        tot = wave_sum(tot);
+        if (lane_id() == 0) {
+            sm.bi[2] = (tot >= A) ? (FB_N - 1 - d) : -1;  // -1: the cut lies below the bins
+            sm.bd[4] = ab;
+            sm.bu[2] = sm.v.rb.c[d];
+        }
+    }
+    __syncthreads();
+    const int rbstar = sm.bi[2];
+    double A_above = sm.bd[4];
+    const uint32_t wcnt = sm.bu[2];
+    __syncthreads();
+    if (rbstar < 0) {
+        final_generic<DT>(sm, c, pl, ro, a);
+        return;
+    }
+    const double gb = gm - (double)rbstar;  // the bin is [gb/FB_W, (gb+1)/FB_W)
+    const float hlo = (float)(gb / (double)FB_W), hhi = (float)((gb + 1.0) / (double)FB_W);
+    const uint32_t klo = key_of_f32(hlo), khi = key_of_f32(hhi) - 1u;
+    // each chunk's whole bins above the window's row bin, one wave per chunk
+    for (int g = wave_id(); g < G; g += NWAVE) {
+        const int off = offg[g];
+        double w = 0.0;
+        if (off >= 0) {
+            const int nb = rbstar - off <= 0 ? 0 : (rbstar - off >= FB_N ? FB_N : rbstar - off);
+            const double *fm = c.fbm + (size_t)g * FB_N;
+            double t[FB_N / 64];
+#pragma unroll
+            for (int q = 0; q < FB_N / 64; ++q) {
+                const int cb = q * 64 + lane_id();
+                t[q] = cb < nb ? fm[cb] : 0.0;
+            }
+#pragma unroll
+            for (int q = 0; q < FB_N / 64; ++q) w += t[q];
+        }
+        w = wave_sum(w);
+        if (lane_id() == 0) sm.cw[g] = w * sm.chs[g];
+    }
+    uint32_t wklo = klo, wkhi = khi;  // the window; (wkhi, khi] adds to the chunks' weights
+    if (wcnt > (uint32_t)WCAP) {
+        // crowded bin: 256 sub-bins of [hlo, hhi) by a re-read (index 255 = top)
+        __syncthreads();
+        for (int i = tid; i < 256; i += NT) { sm.v.l1.cnt[i] = 0u; sm.v.l1.mass[i] = 0.0; }
+        uint32_t xlo, xhi;
+        x_interval<DT>(sm, klo, khi, c.T, &xlo, &xhi);
+        const float inv = 256.0f / (hhi - hlo);
+        rescan<DT>(c, xlo, xhi, [&](int64_t, float y, uint32_t k) {
+            if (k < klo || k > khi) return;
+            const int sb = min(255, (int)((hhi - y) * inv));
+            atomicAdd(&sm.v.l1.cnt[255 - sb], 1u);
+            atomicAdd(&sm.v.l1.mass[255 - sb], exp((double)y - md));
+        });
+        __syncthreads();
+        if (wave_id() == 0) {
+            double ab;
+            const int d = wave_find_desc<double>(sm.v.l1.mass, 256, A - A_above, &ab);
+            if (lane_id() == 0) { sm.bi[3] = 255 - d; sm.bd[5] = ab; sm.bu[3] = sm.v.l1.cnt[d]; }
+        }
+        __syncthreads();
+        const int sstar = sm.bi[3];
+        A_above += sm.bd[5];
+        const uint32_t scnt = sm.bu[3];
+        __syncthreads();
+        // key range of sub-bin sstar inside [klo, khi]; the sub-bin index is
+        // non-increasing in the key
+        if (wave_id() == 0) {
+            auto sbk = [&](uint32_t k) -> int { return min(255, (int)((hhi - f32_of_key(k)) * inv)); };
+            uint64_t lo = klo, hi = khi;  // smallest key with sbk <= sstar
+            if (sbk(klo) <= sstar) hi = klo;
+            else {
+                while (hi - lo > 1) {
+                    uint64_t step = (hi - lo) / 64; if (step == 0) step = 1;
+                    const uint64_t p = lo + (uint64_t)(lane_id() + 1) * step;
+                    const bool pred = p >= hi ? true : (sbk((uint32_t)p) <= sstar);
+                    const uint64_t mk = __ballot(pred);
+                    if (mk == 0ull) { lo = lo + 64 * step; continue; }
+                    const int f = __builtin_ctzll(mk);
+                    const uint64_t nhi = lo + (uint64_t)(f + 1) * step;
+                    if (nhi < hi) hi = nhi;
+                    lo = lo + (uint64_t)f * step;
+                }
+            }
+            uint64_t lo2 = klo, hi2 = khi;  // largest key with sbk >= sstar
+            if (sbk(khi) >= sstar) lo2 = khi;
+            else {
+                while (hi2 - lo2 > 1) {
+                    uint64_t step = (hi2 - lo2) / 64; if (step == 0) step = 1;
+                    const uint64_t p = lo2 + (uint64_t)(lane_id() + 1) * step;
+                    const bool pred = p >= hi2 ? true : (sbk((uint32_t)p) < sstar);
+                    const uint64_t mk = __ballot(pred);
+                    if (mk == 0ull) { lo2 = lo2 + 64 * step; continue; }
+                    const int f = __builtin_ctzll(mk);
+                    const uint64_t nhi = lo2 + (uint64_t)(f + 1) * step;
+                    if (nhi < hi2) hi2 = nhi;
+                    lo2 = lo2 + (uint64_t)f * step;
+                }
+            }
+            if (lane_id() == 0) { sm.bu[4] = (uint32_t)hi; sm.bu[5] = (uint32_t)lo2; }
+        }
+        __syncthreads();
+        wklo = sm.bu[4];
+        wkhi = sm.bu[5];
+        __syncthreads();
+        if (scnt > (uint32_t)WCAP || wklo > wkhi) {
+            final_generic<DT>(sm, c, pl, ro, a);
+            return;
+        }
+    }
+    // collect [wklo, wkhi] into LDS; (wkhi, khi] is kept mass of its chunks
+    __syncthreads();
+    if (tid == 0) sm.bu[6] = 0u;
+    uint32_t xlo, xhi;
+    x_interval<DT>(sm, wklo, khi, c.T, &xlo, &xhi);
+    rescan<DT>(c, xlo, xhi, [&](int64_t j, float y, uint32_t k) {
+        if (k < wklo || k > khi) return;
+        const double e = exp((double)y - md);
+        if (k <= wkhi) {
+            const uint32_t p = atomicAdd(&sm.bu[6], 1u);
+            if (p < (uint32_t)SURV_CAP) { sm.u.s.key[p] = k; sm.u.s.idx[p] = (int32_t)j; sm.u.s.e[p] = e; }
+        } else {
+            atomicAdd(&sm.cw[j / c.CH], e);
+        }
+    });
+    __syncthreads();
+    const uint32_t nw0 = sm.bu[6];
+    __syncthreads();
+    if (nw0 > (uint32_t)SURV_CAP) {
+        final_generic<DT>(sm, c, pl, ro, a);
+        return;
+    }
+    const uint32_t nw = nw0;
     uint32_t cut_key;
     int32_t cut_i;
     window_cut(sm, sm.u.s.key, sm.u.s.idx, sm.u.s.e, nw, A - A_above, 0.0, &cut_key, &cut_i, DT);
-    // per-chunk kept weight: whole fine bins above the window (phase 1), kept
-    // mass above the collected range, kept collected elements
-    const double gm = floor(md * (double)FB_W);
-    const double *gmm = reinterpret_cast<const double *>(a.ws + L.fbm) + (size_t)row * L.G * FB_N;
-    const double *amass = reinterpret_cast<const double *>(a.ws + L.amass) + (size_t)row * G_MAX;
-    // the window's row bin, as published with round 1 (deriving it from the
-    // window's top key would be off by one for the bin just below zero,
-    // whose top key is that of -0.0)
-    const double rbw = (double)ld_dev(&rc->rbin);
-    for (int g = tid; g < L.G; g += NT) {
-        double w = 0.0;
-        if (ld_dev(&csr[g].ymax) != -INFINITY) {
-            const double off = gm - ld_dev(&csr[g].gmc);
-            for (int rb = 0; rb < (int)rbw && rb < FB_N; ++rb) {
-                const double cb = (double)rb - off;
-                if (cb >= 0.0) w += ld_dev(&gmm[(size_t)g * FB_N + (int)cb]);
-            }
-            w *= sm.chs[g];
-        }
-        sm.cw[g] = w + ld_dev(&amass[g]);
-    }
-    __syncthreads();
     for (uint32_t i = tid; i < nw; i += NT)
         if (kept_by_cut(sm.u.s.key[i], sm.u.s.idx[i], cut_key, cut_i))
             atomicAdd(&sm.cw[sm.u.s.idx[i] / c.CH], sm.u.s.e[i]);
     int gsel;
     double resid, SK;
-    pick_chunk(sm, L.G, pl.u, &gsel, &resid, &SK);
+    pick_chunk(sm, G, pl.u, &gsel, &resid, &SK);
     int64_t id = -1;
     if (gsel >= 0) {
         const float T = pl.T;
@@ -1120,170 +1280,7 @@ __device__ __noinline__ void final_topp_window(Smem &sm, RowCx &c, const RowPlan
             return (y != -INFINITY && kept_by_cut(row_key(y, DT), j, cut_key, cut_i)) ? exp((double)y - md) : 0.0;
         });
     }
-    write_row(ro, a, row, id, id >= 0 ? MIS_ROW_OK : MIS_ROW_INVALID, pl.mode, mrow, cut_key, cut_i, SK);
-}
-
-// fp32 top-p leader, after phase 1: merge the chunks' fine bins on the row
-// grid, find the bin holding the cut and publish round 1 (collect the bin, or
-// histogram it first when it is crowded).  Returns 0 when rounds follow,
-// 1 when the row is invalid, 2 when the cut lies below the bins (re-read path).
-template <int DT>
-__device__ __forceinline__ int topp_plan(Smem &sm, RowCx &c, const RowPlan &pl, const ChunkSum *csr, RowCtl *rc)
-{
-    // the caller's Args are reached through the chunk summaries' owner layout
-    const int tid = threadIdx.x;
-    uint32_t anyflag = 0;
-    float m = -INFINITY;
-    for (int g = tid; g < c.G; g += NT) { anyflag |= ld_dev(&csr[g].flags); m = fmaxf(m, ld_dev(&csr[g].ymax)); }
-    anyflag = block_sum<uint32_t>(anyflag ? 1u : 0u, sm.red);
-    m = block_max<float>(m, sm.red);
-    int state = 0;
-    if (anyflag != 0u || m == -INFINITY) state = 1;
-    c.m = m;
-    const double md = (double)m;
-    double S = 0.0, A = 0.0, A_above = 0.0;
-    if (state == 0) {
-        const double gm = floor(md * (double)FB_W);
-        for (int g = tid; g < c.G; g += NT) sm.chs[g] = exp((double)ld_dev(&csr[g].ymax) - md);
-        __syncthreads();
-        double s = 0.0;
-        for (int g = tid; g < c.G; g += NT) if (ld_dev(&csr[g].ymax) != -INFINITY) s += ld_dev(&csr[g].S) * sm.chs[g];
-        S = block_sum<double>(s, sm.red);
-        for (int rb = tid; rb < FB_N; rb += NT) {
-            double mm = 0.0;
-            uint32_t cc = 0;
-            for (int g = 0; g < c.G; ++g) {
-                if (ld_dev(&csr[g].ymax) == -INFINITY) continue;
-                const double cb = (double)rb - (gm - ld_dev(&csr[g].gmc));
-                if (cb >= 0.0 && cb < (double)FB_N) {
-                    mm += ld_dev(&c.fbm[(size_t)g * FB_N + (int)cb]) * sm.chs[g];
-                    cc += ld_dev(&c.fbc[(size_t)g * FB_N + (int)cb]);
-                }
-            }
-            sm.v.rb.m[FB_N - 1 - rb] = mm;
-            sm.v.rb.c[FB_N - 1 - rb] = cc;
-        }
-        __syncthreads();
-        A = (double)pl.top_p * S;
-        if (wave_id() == 0) {
-            double ab;
-            const int d = wave_find_desc<double>(sm.v.rb.m, FB_N, A, &ab);
-            double tot = 0.0;
-            for (int q = lane_id(); q < FB_N; q += 64) tot += sm.v.rb.m[q];
-            tot = wave_sum(tot);
-            if (lane_id() == 0) {
-                sm.bi[2] = (tot >= A) ? (FB_N - 1 - d) : -1;  // -1: the cut lies below the bins
-                sm.bd[4] = ab;
-                sm.bu[2] = sm.v.rb.c[d];
-            }
-        }
-        __syncthreads();
-        const int rbstar = sm.bi[2];
-        A_above = sm.bd[4];
-        const uint32_t wcnt = sm.bu[2];
-        __syncthreads();
-        if (rbstar < 0) {
-            state = 2;
-        } else {
-            const double g = gm - (double)rbstar;  // the bin is [g/FB_W, (g+1)/FB_W)
-            const float lo = (float)(g / (double)FB_W);
-            const float hi = (float)((g + 1.0) / (double)FB_W);
-            const uint32_t klo = key_of_f32(lo);
-            const uint32_t khi = key_of_f32(hi) - 1u;
-            if (wcnt > (uint32_t)WCAP)
-                for (int i = tid; i < SUB_N; i += NT) { st_dev(&c.subc[i], 0u); st_dev(&c.subm[i], 0.0); }
-            if (tid == 0) {
-                st_dev(&rc->hlo, lo); st_dev(&rc->hhi, hi); st_dev(&rc->klo, klo); st_dev(&rc->khi, khi);
-                st_dev(&rc->kahi, khi); st_dev(&rc->rbin, rbstar);
-                st_dev(&rc->wcount, 0u);
-                st_dev(&rc->rtype, wcnt > (uint32_t)WCAP ? R_HIST : R_COLLECT);
-            }
-        }
-    }
-    if (tid == 0) {
-        st_dev(&rc->m, m);
-        if (state != 0) st_dev(&rc->rtype, R_DONE);
-        sm.bd[5] = S; sm.bd[6] = A; sm.bd[7] = A_above;
-    }
-    (void)block_release_add(sm, &rc->round, 1u);  // publish round 1
-    return state;
-}
-
-// fp32 top-p leader after a histogram round: find the sub-bin holding the cut,
-// publish a collect round for it.  Returns 0 (round published) or 2 (give up:
-// the re-read path takes over; the followers were released).
-template <int DT>
-__device__ __forceinline__ int topp_after_hist(Smem &sm, const RowCx &c, RowCtl *rc)
-{
-    const int tid = threadIdx.x;
-    const uint32_t klo = ld_dev(&rc->klo), khi = ld_dev(&rc->khi);
-    const float hlo = ld_dev(&rc->hlo), hhi = ld_dev(&rc->hhi);
-    const double A = sm.bd[6];
-    double A_above = sm.bd[7];
-    for (int i = tid; i < SUB_N; i += NT) { sm.sub_m[SUB_N - 1 - i] = ld_dev(&c.subm[i]); sm.sub_c[SUB_N - 1 - i] = ld_dev(&c.subc[i]); }
-    __syncthreads();
-    if (wave_id() == 0) {
-        double ab;
-        const int d = wave_find_desc<double>(sm.sub_m, SUB_N, A - A_above, &ab);
-        if (lane_id() == 0) { sm.bi[3] = SUB_N - 1 - d; sm.bd[4] = ab; sm.bu[2] = sm.sub_c[d]; }
-    }
-    __syncthreads();
-    const int sstar = sm.bi[3];
-    A_above += sm.bd[4];
-    const uint32_t scnt = sm.bu[2];
-    __syncthreads();
-    if (tid == 0) sm.bd[7] = A_above;
-    // key range of sub-bin sstar inside [klo, khi]; the sub-bin index is
-    // non-increasing in the key
-    if (wave_id() == 0) {
-        const float inv = (float)SUB_N / (hhi - hlo);
-        auto sbk = [&](uint32_t k) -> int { return min(SUB_N - 1, (int)((hhi - f32_of_key(k)) * inv)); };
-        uint64_t lo = klo, hi = khi;  // smallest key with sbk <= sstar
-        if (sbk(klo) <= sstar) hi = klo;
-        else {
-            while (hi - lo > 1) {
-                uint64_t step = (hi - lo) / 64; if (step == 0) step = 1;
-                const uint64_t p = lo + (uint64_t)(lane_id() + 1) * step;
-                const bool pred = p >= hi ? true : (sbk((uint32_t)p) <= sstar);
-                const uint64_t mk = __ballot(pred);
-                if (mk == 0ull) { lo = lo + 64 * step; continue; }
-                const int f = __builtin_ctzll(mk);
-                const uint64_t nhi = lo + (uint64_t)(f + 1) * step;
-                if (nhi < hi) hi = nhi;
-                lo = lo + (uint64_t)f * step;
-            }
-        }
-        const uint32_t skl = (uint32_t)hi;
-        uint64_t lo2 = klo, hi2 = khi;  // largest key with sbk >= sstar
-        if (sbk(khi) >= sstar) lo2 = khi;
-        else {
-            while (hi2 - lo2 > 1) {
-                uint64_t step = (hi2 - lo2) / 64; if (step == 0) step = 1;
-                const uint64_t p = lo2 + (uint64_t)(lane_id() + 1) * step;
-                const bool pred = p >= hi2 ? true : (sbk((uint32_t)p) < sstar);
-                const uint64_t mk = __ballot(pred);
-                if (mk == 0ull) { lo2 = lo2 + 64 * step; continue; }
-                const int f = __builtin_ctzll(mk);
-                const uint64_t nhi = lo2 + (uint64_t)(f + 1) * step;
-                if (nhi < hi2) hi2 = nhi;
-                lo2 = lo2 + (uint64_t)f * step;
-            }
-        }
-        if (lane_id() == 0) { sm.bu[4] = skl; sm.bu[5] = (uint32_t)lo2; }
-    }
-    __syncthreads();
-    const uint32_t skl = sm.bu[4], skh = sm.bu[5];
-    const bool give_up = (scnt > (uint32_t)WCAP || skl > skh);
-    __syncthreads();
-    if (tid == 0) {
-        if (give_up) st_dev(&rc->rtype, R_DONE);
-        else {
-            st_dev(&rc->rtype, R_COLLECT); st_dev(&rc->klo, skl); st_dev(&rc->khi, skh); st_dev(&rc->kahi, khi);
-            st_dev(&rc->wcount, 0u);
-        }
-    }
-    (void)block_release_add(sm, &rc->round, 1u);
-    return give_up ? 2 : 0;
+    write_row(ro, a, c.row, id, id >= 0 ? MIS_ROW_OK : MIS_ROW_INVALID, pl.mode, m, cut_key, cut_i, SK);
 }
 
 // Leader of a row that needs no refinement rounds: greedy, temperature only,
@@ -1363,26 +1360,19 @@ __device__ __noinline__ void final_row(Smem &sm, RowCx &c, const RowPlan &pl, co
     }
 }
 
-// ------------------------------------------------------------------ the kernel
+// ------------------------------------------------------------------ the chunk pass
 
+// One workgroup per (row, chunk): one coalesced read of the chunk into
+// registers -- the only HBM read of the logits -- reduced to the chunk
+// summary the row pass needs for the row's mode.
 template <int DT, int EPT>
-__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(3))) void k_sample(Args a)
+__global__ __launch_bounds__(NT) void k_chunk(Args a)
 {
     constexpr int VEC = Traits<DT>::VEC, NV = EPT / VEC, CH = NT * EPT;
-    __shared__ Smem sm;
+    __shared__ ChunkSmem sm;
     const Layout &L = a.L;
     const int tid = threadIdx.x;
-    Ctl *ctl = reinterpret_cast<Ctl *>(a.ws + L.ctl);
-
-    // ---- ticket -> (row, chunk)
-    if (tid == 0) {
-        const unsigned long long t = atomicAdd(&ctl->ticket, 1ull);
-        sm.bq[1] = t % (unsigned long long)(L.B * L.G);
-        sm.args = a;
-    }
-    __syncthreads();
-    const uint32_t task = uni((uint32_t)sm.bq[1]);
-    __syncthreads();
+    const uint32_t task = blockIdx.x;
     const uint32_t G = (uint32_t)L.G;
     const int row = uni((int32_t)(task / G)), chunk = uni((int32_t)(task % G));
     const int64_t V = a.V;
@@ -1391,8 +1381,6 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(3))) void k_
     mis_row_params P = a.params[row];
     P.temperature = uni(P.temperature); P.top_k = uni(P.top_k); P.top_p = uni(P.top_p); P.uniform = uni(P.uniform);
     const RowPlan pl = plan_row(P, V);
-    RowCtl *rc = reinterpret_cast<RowCtl *>(a.ws + L.rowctl) + row;
-    RowOut *ro = reinterpret_cast<RowOut *>(a.ws + L.rowout) + row;
     ChunkSum *csr = reinterpret_cast<ChunkSum *>(a.ws + L.chunks) + (size_t)row * L.G;
     ChunkSum *cs = csr + chunk;
 
@@ -1630,148 +1618,34 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(3))) void k_
         st_dev(&cs->ncand, ncand); st_dev(&cs->xmax, xmax); st_dev(&cs->S, Sc); st_dev(&cs->gmc, gmc);
         st_dev(&cs->below, below);
     }
+}
 
-    // ---- arrive; the last arrival leads the row
-    const uint32_t old = block_release_add(sm, &rc->arrive, 1u);
-    const bool leader = (old == G - 1u);
-    __syncthreads();
+// ------------------------------------------------------------------ the row pass
 
-    // the row context in LDS is filled in the leader only: code that every
-    // workgroup runs takes what it needs from the launch arguments
-    RowCx &c = sm.cx;
-    RowPlan &spl = sm.pl;
-    uint32_t *const subc_row = reinterpret_cast<uint32_t *>(a.ws + L.subc) + (size_t)row * SUB_N;
-    double *const subm_row = reinterpret_cast<double *>(a.ws + L.subm) + (size_t)row * SUB_N;
-    if (leader && tid == 0) {
-        c.rowp = rowp; c.V = V; c.vec_ok = a.vec_ok; c.T = pl.T; c.m = 0.0f; c.G = L.G; c.CH = CH; c.row = row;
+// One workgroup per row: merges the row's chunk summaries and finishes the
+// row (the functions above), re-reading parts of the row where needed.
+template <int DT>
+__global__ __launch_bounds__(NT) void k_final(Args a)
+{
+    __shared__ Smem sm;
+    const Layout &L = a.L;
+    const int row = blockIdx.x;
+    if (threadIdx.x == 0) {
+        sm.args = a;
+        RowCx &c = sm.cx;
+        c.rowp = a.logits + (int64_t)row * a.stride_bytes;
+        c.V = a.V; c.vec_ok = a.vec_ok; c.m = 0.0f; c.G = L.G; c.CH = (int64_t)NT * L.ept; c.row = row;
         c.fbc = reinterpret_cast<const uint32_t *>(a.ws + L.fbc) + (size_t)row * L.G * FB_N;
         c.fbm = reinterpret_cast<const double *>(a.ws + L.fbm) + (size_t)row * L.G * FB_N;
-        c.subc = reinterpret_cast<uint32_t *>(a.ws + L.subc) + (size_t)row * SUB_N;
-        c.subm = reinterpret_cast<double *>(a.ws + L.subm) + (size_t)row * SUB_N;
-        spl = pl;
+        c.subc = nullptr; c.subm = nullptr;
+        sm.pl = plan_row(a.params[row], a.V);
+        c.T = sm.pl.T;
     }
     __syncthreads();
-    const Args &sa = sm.args;
-
-    if (topp32) {
-        // ============================================ fp32 top-p: refinement rounds
-        int state = 0;  // leader: 0 rounds pending, 1 invalid, 2 fallback, 3 collected
-        if (leader) state = topp_plan<DT>(sm, c, spl, csr, rc);
-        uint32_t seen = 0;
-        bool ok = true;
-        for (;;) {
-            if (!block_wait_ge(sm, &rc->round, seen + 1u, ctl)) { ok = false; break; }
-            seen += 1u;
-            const uint32_t rtype = ld_dev(&rc->rtype);
-            if (rtype == R_DONE) break;
-            const uint32_t klo = ld_dev(&rc->klo), khi = ld_dev(&rc->khi), kahi = ld_dev(&rc->kahi);
-            const float hlo = ld_dev(&rc->hlo), hhi = ld_dev(&rc->hhi);
-            const double md = (double)ld_dev(&rc->m);
-            uint32_t xlo, xhi;
-            x_interval<DT>(sm, klo, kahi, pl.T, &xlo, &xhi);
-            // stage the few elements whose raw key can map into the round's
-            // range; the register-resident chunk is only compared here
-            if (tid == 0) sm.bu[3] = 0u;
-            __syncthreads();
-#pragma unroll
-            for (int i = 0; i < EPT; ++i) {
-                if (ok_(i)) {
-                    const uint32_t xk = key_of_f32(x[i]);
-                    if (xk >= xlo && xk <= xhi) {
-                        const uint32_t p = atomicAdd(&sm.bu[3], 1u);
-                        if (p < (uint32_t)STAGE_CAP) { sm.u.st.x[p] = x[i]; sm.u.st.j[p] = lofs(i); }
-                    }
-                }
-            }
-            __syncthreads();
-            const uint32_t nst0 = sm.bu[3];
-            const uint32_t nst = nst0 < (uint32_t)STAGE_CAP ? nst0 : (uint32_t)STAGE_CAP;
-            if (nst0 > (uint32_t)STAGE_CAP && tid == 0) atomicOr(&rc->ovf, 1u);
-            if (rtype == R_HIST) {
-                for (int i = tid; i < SUB_N; i += NT) { sm.sub_c[i] = 0u; sm.sub_m[i] = 0.0; }
-                __syncthreads();
-                const float inv = (float)SUB_N / (hhi - hlo);
-                for (uint32_t q = tid; q < nst; q += NT) {
-                    const float y = scale_y<DT>(sm.u.st.x[q], pl.T);
-                    const uint32_t k = row_key(y, DT);
-                    if (k >= klo && k <= khi) {
-                        const int sb = min(SUB_N - 1, (int)((hhi - y) * inv));
-                        atomicAdd(&sm.sub_c[sb], 1u);
-                        atomicAdd(&sm.sub_m[sb], exp((double)y - md));
-                    }
-                }
-                __syncthreads();
-                for (int i = tid; i < SUB_N; i += NT)
-                    if (sm.sub_c[i]) { atomicAdd(&subc_row[i], sm.sub_c[i]); atomicAdd(&subm_row[i], sm.sub_m[i]); }
-            } else {  // R_COLLECT
-                uint32_t mine = 0;
-                double am = 0.0;
-                for (uint32_t q = tid; q < nst; q += NT) {
-                    const float y = scale_y<DT>(sm.u.st.x[q], pl.T);
-                    const uint32_t k = row_key(y, DT);
-                    if (k >= klo && k <= khi) mine++;
-                    else if (k > khi && k <= kahi) am += exp((double)y - md);
-                }
-                uint32_t total;
-                const uint32_t off = block_excl_scan<uint32_t>(mine, sm.red, &total);
-                if (tid == 0) sm.bu[2] = total ? atomicAdd(&rc->wcount, total) : 0u;
-                __syncthreads();
-                uint32_t pos = sm.bu[2] + off;
-                __syncthreads();
-                Elem *win = reinterpret_cast<Elem *>(a.ws + L.win) + (size_t)row * WCAP;
-                for (uint32_t q = tid; q < nst; q += NT) {
-                    const uint32_t k = row_key(scale_y<DT>(sm.u.st.x[q], pl.T), DT);
-                    if (k >= klo && k <= khi) {
-                        if (pos < (uint32_t)WCAP) {
-                            st_dev_elem(&win[pos], k, (int32_t)(base + (int64_t)sm.u.st.j[q]));
-                        }
-                        pos++;
-                    }
-                }
-                am = block_sum<double>(am, sm.red);
-                if (tid == 0) st_dev(reinterpret_cast<double *>(a.ws + L.amass) + (size_t)row * G_MAX + chunk, am);
-            }
-            (void)block_release_add(sm, &rc->rarrive, 1u);
-            if (!leader) {
-                if (rtype == R_COLLECT) break;  // no round follows a collect round
-                continue;
-            }
-            // ---- leader: wait for every workgroup's part, then decide
-            if (!block_wait_ge(sm, &rc->rarrive, G * seen, ctl)) { ok = false; break; }
-            if (ld_dev(&rc->ovf) != 0u || (rtype == R_COLLECT && ld_dev(&rc->wcount) > (uint32_t)WCAP)) {
-                // a buffer overflowed: release the followers, take the re-read path
-                if (tid == 0) st_dev(&rc->rtype, R_DONE);
-                (void)block_release_add(sm, &rc->round, 1u);
-                state = 2;
-                break;
-            }
-            if (rtype == R_COLLECT) { state = 3; break; }
-            state = topp_after_hist<DT>(sm, c, rc);  // publishes the next round
-            if (state != 0) break;
-        }
-        if (leader) {
-            if (!ok) write_row(ro, a, row, -1, ROW_INTERNAL, pl.mode, 0.0f, 0u, 0, 0.0);
-            else if (state == 1) write_row(ro, a, row, -1, MIS_ROW_INVALID, pl.mode, 0.0f, 0u, 0, 0.0);
-            else if (state == 2) {
-                const float m = ld_dev(&rc->m);
-                __syncthreads();
-                if (tid == 0) c.m = m;
-                __syncthreads();
-                final_generic<DT>(sm, c, spl, ro, sa);
-            } else if (state == 3) {
-                final_topp_window<DT>(sm, c, spl, csr, rc, ro, sa);
-            }
-        }
-    } else if (leader) {
-        final_row<DT>(sm, c, spl, csr, ro, sa);
-    }
-
-    // ---- leave the row; the last workgroup out resets its control words
-    const uint32_t ex = block_release_add(sm, &rc->exited, 1u);
-    if (ex == G - 1u && tid == 0) {
-        st_dev(&rc->arrive, 0u); st_dev(&rc->round, 0u); st_dev(&rc->rarrive, 0u); st_dev(&rc->wcount, 0u);
-        st_dev(&rc->rtype, 0u); st_dev(&rc->ovf, 0u); st_dev(&rc->exited, 0u);
-    }
+    const ChunkSum *csr = reinterpret_cast<const ChunkSum *>(a.ws + L.chunks) + (size_t)row * L.G;
+    RowOut *ro = reinterpret_cast<RowOut *>(a.ws + L.rowout) + row;
+    if (DT == F32 && sm.pl.mode == M_TOPP) final_topp32<DT>(sm, sm.cx, sm.pl, csr, ro, sm.args);
+    else final_row<DT>(sm, sm.cx, sm.pl, csr, ro, sm.args);
 }
 
 // ------------------------------------------------------------------ debug emit
@@ -1819,37 +1693,37 @@ __global__ __launch_bounds__(NT) void k_emit(const char *__restrict__ logits, in
 static thread_local int g_last_hip = 0;
 
 template <int DT, int EPT>
-static hipError_t launch_main(const Args &a, hipStream_t st, void *const *events)
+static hipError_t launch_chunk(const Args &a, hipStream_t st)
 {
-    hipError_t e;
-    if (events && (e = hipEventRecord((hipEvent_t)events[0], st)) != hipSuccess) return e;
     const unsigned grid = (unsigned)(a.L.B * a.L.G);
-    hipLaunchKernelGGL((k_sample<DT, EPT>), dim3(grid), dim3(NT), 0, st, a);
-    e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    if (events) e = hipEventRecord((hipEvent_t)events[1], st);
-    return e;
+    hipLaunchKernelGGL((k_chunk<DT, EPT>), dim3(grid), dim3(NT), 0, st, a);
+    return hipGetLastError();
 }
 
+// events (optional): [0] before the chunk pass, [1] between the chunk pass
+// and the row pass, [2] after the row pass
 template <int DT>
 static hipError_t launch_dt(const Args &a, float *probs, uint32_t *keep, hipStream_t st, void *const *ev)
 {
     hipError_t e;
+    if (ev && (e = hipEventRecord((hipEvent_t)ev[0], st)) != hipSuccess) return e;
     switch (a.L.ept) {
-    case 64: e = launch_main<DT, 64>(a, st, ev); break;
-    case 32: e = launch_main<DT, 32>(a, st, ev); break;
-    case 16: e = launch_main<DT, 16>(a, st, ev); break;
-    default: e = launch_main<DT, 8>(a, st, ev); break;
+    case 64: e = launch_chunk<DT, 64>(a, st); break;
+    case 32: e = launch_chunk<DT, 32>(a, st); break;
+    case 16: e = launch_chunk<DT, 16>(a, st); break;
+    default: e = launch_chunk<DT, 8>(a, st); break;
     }
     if (e != hipSuccess) return e;
+    if (ev && (e = hipEventRecord((hipEvent_t)ev[1], st)) != hipSuccess) return e;
+    hipLaunchKernelGGL((k_final<DT>), dim3((unsigned)a.L.B), dim3(NT), 0, st, a);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    if (ev && (e = hipEventRecord((hipEvent_t)ev[2], st)) != hipSuccess) return e;
     if (probs || keep) {
         const unsigned gx = (unsigned)((a.V + (int64_t)NT * 8 - 1) / ((int64_t)NT * 8));
         hipLaunchKernelGGL((k_emit<DT>), dim3(gx, (unsigned)a.L.B), dim3(NT), 0, st, a.logits, a.V, a.stride_bytes,
                            a.params, a.L, (const char *)a.ws, probs, keep);
         e = hipGetLastError();
-        if (e != hipSuccess) return e;
     }
-    if (ev) e = hipEventRecord((hipEvent_t)ev[2], st);
     return e;
 }
 
