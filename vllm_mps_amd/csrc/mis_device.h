@@ -59,6 +59,49 @@ template <int DT> __device__ __forceinline__ float scale_y(float x, float T)
     return DT == F32 ? q : rn_dtype(q, DT);
 }
 
+// The same quotient through the row's reciprocal r = RN(1/T): q0 = RN(x*r)
+// lies within 1.5 ulp of x/T, every residual x - q*T is then exact in one
+// FMA, and two Newton corrections q + (x - q*T)*r give RN(x/T) (Markstein's
+// theorem: the second correction starts from a faithful quotient).  Quotients
+// near overflow, tiny x or quotients (whose residuals would underflow) and
+// infinite x take the generic division.  Checked bit for bit against x / T over every float x for a set
+// of temperatures (tests/test_host_logic.py samples the same property).
+__device__ __forceinline__ float div_rcp(float x, float T, float r)
+{
+    const float q0 = x * r;
+    const float aq = fabsf(q0);
+    if (!(aq < 0x1p127f) || aq < 0x1p-100f || fabsf(x) < 0x1p-100f) return x / T;
+    const float e0 = fmaf(-q0, T, x);
+    const float q1 = fmaf(e0, r, q0);
+    const float e1 = fmaf(-q1, T, x);
+    return fmaf(e1, r, q1);
+}
+template <int DT> __device__ __forceinline__ float scale_r(float x, float T, float r)
+{
+    const float q = div_rcp(x, T, r);
+    return DT == F32 ? q : rn_dtype(q, DT);
+}
+
+// exp(y - ym) for y <= ym in binary32 with a bounded relative error: the
+// difference and its base-2 scaling are formed in binary64 (exact difference,
+// one rounding of 2^-53), split into n + f with |f| <= 1/2, and 2^f comes from
+// the hardware exp2 (1 ulp) on the f32-rounded f (2^-26 absolute).  Relative
+// error <= 1.3e-7 while the result is normal; WEXP_REL_ERR bounds it with
+// margin.  Results below 2^-126 lose relative precision (absolute error
+// <= 2^-149), which the callers' bounds cover through an absolute term.
+constexpr double WEXP_REL_ERR = 4.8e-7;   // 2^-21
+constexpr double WEXP_ABS_ERR = 1.5e-45;  // one subnormal ulp per element
+__device__ __forceinline__ float wexp(float y, float ym)
+{
+    const double t = ((double)y - (double)ym) * 1.4426950408889634;
+    if (!(t > -1000.0)) return 0.0f;  // y = -inf (or below every subnormal)
+    const double n = rint(t);
+    const float f = (float)(t - n);
+    const float p = __builtin_amdgcn_exp2f(f);
+    const int ni = n < -300.0 ? -300 : (int)n;
+    return ldexpf(p, ni);
+}
+
 // ------------------------------------------------------------------ wave / block
 
 // Workgroup-uniform values read back from LDS: moving them to scalar
@@ -222,6 +265,83 @@ __device__ int wave_find_desc(const T *h, int nbins, T target, T *above)
     abv = __shfl(abv, first, 64);
     *above = abv;
     return bsel;
+}
+
+// Ascending search over n <= 64*per values in LDS, run by one whole wave:
+// the first index i whose inclusive prefix sum exceeds `target` (indices with
+// zero value never qualify); *before = sum of the values before i.  When
+// rounding leaves the target out of reach, the last index with a nonzero
+// value.  Returns -1 when every value is zero.
+__device__ int wave_find_asc(const double *v, int n, double target, double *before)
+{
+    const int l = lane_id();
+    const int per = (n + 63) / 64;
+    const int b0 = l * per, b1 = b0 + per < n ? b0 + per : n;
+    double s = 0.0;
+    for (int i = b0; i < b1; ++i) s += v[i];
+    const double inc = wave_incl_scan(s);
+    const uint64_t mask = __ballot(inc > target);
+    int sel = -1;
+    double bef = 0.0;
+    int owner;
+    if (mask != 0ull) {
+        owner = __builtin_ctzll(mask);
+        if (l == owner) {
+            double run = inc - s;
+            int last = -1;
+            double lastbef = 0.0;
+            for (int i = b0; i < b1; ++i) {
+                if (v[i] > 0.0) {
+                    if (run + v[i] > target) { sel = i; bef = run; break; }
+                    last = i; lastbef = run;
+                }
+                run += v[i];
+            }
+            if (sel < 0) { sel = last; bef = lastbef; }
+        }
+    } else {
+        const uint64_t ne = __ballot(s > 0.0);
+        if (ne == 0ull) { *before = 0.0; return -1; }
+        owner = 63 - __builtin_clzll(ne);
+        if (l == owner) {
+            double run = inc - s;
+            for (int i = b0; i < b1; ++i) {
+                if (v[i] > 0.0) { sel = i; bef = run; }
+                run += v[i];
+            }
+        }
+    }
+    sel = __shfl(sel, owner, 64);
+    bef = __shfl(bef, owner, 64);
+    *before = bef;
+    return sel;
+}
+
+// Bitonic sort, descending, of n <= cap (u64 key, f64 value) pairs in LDS by
+// all threads of the block; entries n .. pow2(n)-1 are padded with key 0, so
+// the arrays must hold pow2(n) entries.
+__device__ void block_sort_desc(uint64_t *k, double *e, int n)
+{
+    int npow = 1;
+    while (npow < n) npow <<= 1;
+    for (int i = n + (int)threadIdx.x; i < npow; i += NT) { k[i] = 0ull; e[i] = 0.0; }
+    __syncthreads();
+    for (int kk = 2; kk <= npow; kk <<= 1) {
+        for (int j = kk >> 1; j > 0; j >>= 1) {
+            for (int i = threadIdx.x; i < npow; i += NT) {
+                const int ixj = i ^ j;
+                if (ixj > i) {
+                    const bool desc = (i & kk) == 0;
+                    const uint64_t a = k[i], b = k[ixj];
+                    if (desc ? (a < b) : (a > b)) {
+                        k[i] = b; k[ixj] = a;
+                        const double t = e[i]; e[i] = e[ixj]; e[ixj] = t;
+                    }
+                }
+            }
+            __syncthreads();
+        }
+    }
 }
 
 // ------------------------------------------------------------------ raw-key intervals

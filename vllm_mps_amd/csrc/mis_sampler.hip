@@ -5,27 +5,35 @@
 // debug probabilities / keep bitmask).
 //
 // k_sample: B*G workgroups of 256 threads.  Each workgroup takes a ticket
-// (atomic counter) naming one chunk of one row, loads that chunk into
-// registers with coalesced 16-byte vector reads -- the only HBM read of the
-// logits -- and reduces it to a chunk summary.  The last workgroup of a row
-// to arrive becomes the row's leader and finishes the row:
+// (atomic counter) naming one chunk of one row -- tickets run row-major, so a
+// row's chunks start together -- and loads that chunk into registers with
+// coalesced 16-byte vector reads: the only HBM read of the logits.  The
+// per-element work is register arithmetic only (no LDS atomics on dense
+// data, which serialise on bin conflicts): a max, a divide by the row's
+// temperature through its reciprocal, an f32 exponential with a bounded
+// error.  Each chunk publishes a summary; the last workgroup of a row to
+// arrive finishes the row:
 //   greedy       argmax merge;
-//   small top-k  per chunk: every element >= a threshold that keeps the
-//                chunk's top k'; leader: exact k'-th value -> survivors ->
-//                top-p over the survivors -> draw;
-//   temperature  per-chunk weights -> the chunk holding the draw -> that chunk
-//                is re-read for the index;
-//   fp32 top-p   float64 mass histograms on a fixed value grid (16 bins per
-//                unit below each chunk's max) locate the bin holding the cut;
-//                the row's workgroups, still holding their chunks in
-//                registers, refine that bin (sub-histogram) and collect its
-//                elements when the leader asks; the leader resolves the exact
-//                cut and draws;
-//   otherwise    (large k', fp16/bf16 top-p, overflows) the leader re-reads the
-//                row: radix descent by mass or count, and the 16-bit rounding
-//                chain walked over runs of equal keys.
-// Tickets are handed out in start order, so a workgroup only ever waits for
-// row mates that have already started; every wait is bounded.
+//   temperature  per-chunk weights -> the chunk holding the draw -> that
+//                chunk is re-read for the index;
+//   small top-k  every chunk emits its elements above a threshold chosen from
+//                its per-thread maxima (closed under the ties the scaling
+//                creates); the leader takes the exact k'-th value over the
+//                candidates, checks that no truncated chunk could hide an
+//                element at or above it, then top-p over the survivors and
+//                the draw;
+//   fp32 top-p   the row's workgroups keep their chunks in registers and run
+//                a few rounds with the leader: coarse lane-private mass bins
+//                (conflict-free), then 256-way refinements of the band that
+//                holds the cut, then a collection of the cut's window; masses
+//                carry a proven f32 error bound, and when the decision margin
+//                is inside that bound one more round recomputes them in f64;
+//   otherwise    (k' > 1024, fp16/bf16 top-p, overflows, cuts outside the
+//                coarse range) the leader re-reads the row: radix descent by
+//                mass or count, and the 16-bit rounding chain walked over runs
+//                of equal keys.
+// Every cross-workgroup wait is for row mates that already hold a ticket, so
+// it ends; each is also bounded by a spin limit.
 //
 // Semantics follow model/sampler.py:18-60 per row: greedy argmax (ties ->
 // lowest index) when T == 0; y = dtype(f32(x) / T); top-k keeps y >= k'-th
@@ -43,46 +51,56 @@ namespace mis {
 
 constexpr int K_SMALL = 1024;      // largest k' served by the candidate path
 constexpr int CAND_CAP = 2048;     // candidates one chunk may emit
-constexpr int SURV_CAP = 2048;     // top-k survivors held in LDS
+constexpr int SURV_CAP = 1024;     // top-k survivors / top-p window held in LDS
 constexpr int G_MAX = 256;         // chunks per row
-constexpr int FB_W = 16;           // fine bins per unit of y (top-p)
-constexpr int FB_N = 384;          // fine bins below each chunk max (24 units)
-constexpr int SUB_N = 256;         // sub-bins of a refined fine bin
-constexpr int WCAP = 2048;         // elements a collect round may gather
-constexpr int REGION_BINS = 8;     // L1 bins per 16-bit chain pass
+constexpr int CB_N = 16;           // coarse top-p bins (lane-private)
+constexpr float CB_SCALE = 0.5f;   // coarse bin = floor(y * CB_SCALE): 2 units of y
+constexpr int RB_N = 256;          // sub-bins of a refinement round
+constexpr int WCAP = 4096;         // window slots per row in the workspace
+constexpr int MAX_REFINE = 4;      // refinement rounds before the re-read path
+constexpr int REGION_BINS = 1;     // L1 bins per 16-bit chain pass (re-read path)
 constexpr int RUN_CAP = REGION_BINS * 256;
-constexpr int TIE_CAP = 2048;
-constexpr int STAGE_CAP = 4096;      // elements one workgroup stages per round
+constexpr int TIE_CAP = 1024;
 constexpr uint32_t NCAND_OVERFLOW = 0xffffffffu;
 constexpr int32_t IDX_ALL = 0x7fffffff;
+constexpr uint32_t SPIN_LIMIT = 1u << 22;  // bounded cross-workgroup waits
 
 enum : int { M_BAD = 0, M_GREEDY = 1, M_SMALLK = 2, M_LARGEK = 3, M_TOPP = 4, M_TEMP = 5 };
 enum : uint32_t { FLAG_NAN = 1u, FLAG_PINF = 2u };
-enum : uint32_t { R_COLLECT = 1u, R_HIST = 2u, R_DONE = 3u };
+// kinds of a published top-p round
+enum : uint32_t { R_REFINE = 1u, R_COLLECT = 2u, R_EXACT = 3u };
 
 // ------------------------------------------------------------------ workspace
 
 struct Ctl {                    // 256 B
-    unsigned long long ticket;  // monotonically increasing; task = ticket % (B*G)
+    uint32_t ticket;            // tickets drawn in the current launch
     uint32_t error;             // bit 0: a bounded wait expired
-    uint32_t pad[61];
+    uint32_t pad[62];
 };
 
 struct RowCtl {                 // 64 B per row, zero at rest
-    uint32_t arrive;            // phase-1 arrivals
-    uint32_t round;             // last published refinement round (1, 2, ...)
-    uint32_t rarrive;           // round arrivals, cumulative
-    uint32_t wcount;            // elements appended by the collect round
-    uint32_t exited;            // workgroups done with the row
-    uint32_t rtype;             // R_COLLECT / R_HIST / R_DONE
-    uint32_t klo, khi;          // scaled-key range of the round
-    uint32_t kahi;              // collect: (khi, kahi] is summed as kept mass
-    float hlo, hhi;             // hist: value range [hlo, hhi)
+    uint32_t arr;               // arrivals, cumulative over rounds
+    uint32_t round;             // last round published (round r + 1 runs after it); ROUND_DONE = finished
+    uint32_t exited;            // workgroups that left the row
+    uint32_t wcount;            // window elements appended by the collect round
+    uint32_t rtype;             // R_REFINE / R_COLLECT / R_EXACT of the published round
+    uint32_t klo, khi;          // scaled-key band of the round (inclusive)
+    uint32_t nref;              // refinement rounds so far
+    float lo, sc;               // refine: sub-bin = floor((y - lo) * sc)
     float m;                    // row max of y
-    uint32_t ovf;               // a round overflowed a staging or window buffer
-    int32_t rbin;               // row fine bin (below the row max's bin) holding the cut
-    uint32_t pad[2];
+    uint32_t pad;
+    double S;                   // row sum of weights exp(y - m) (f32-weight estimate)
+    double A;                   // top_p * S
 };
+constexpr uint32_t ROUND_DONE = 0xffffffffu;
+
+// row-wide refine histogram, filled by the chunks' global atomics; the leader
+// reads and clears it between rounds
+struct RowHist {                // 3 KB per row
+    uint32_t cnt[RB_N];
+    unsigned long long mass[RB_N];  // weights relative to the row max, 2^-40 units
+};
+constexpr double HIST_SCALE = 1099511627776.0;  // 2^40
 static_assert(sizeof(RowCtl) == 64, "RowCtl is 64 bytes");
 
 // The control prefix of the workspace (Ctl, then one RowCtl for every row the
@@ -97,13 +115,24 @@ struct ChunkSum {               // 64 B per (row, chunk)
     float ymax;                 // max scaled logit of the chunk
     uint32_t flags;
     uint32_t ncand;             // small-k candidates written, or NCAND_OVERFLOW
-    float xmax;                 // max raw logit of the chunk
-    uint32_t pad0, pad1;
+    uint32_t nfin;              // finite elements of the chunk
+    uint32_t kc;                // small-k: non-candidates have scaled keys < kc
+    uint32_t trunc;             // small-k: some finite element was not emitted
     double S;                   // sum of weights relative to the chunk max
-    double gmc;                 // top-p: floor(ymax * FB_W), the chunk's bin anchor
-    double below;               // top-p: mass below the fine-bin range
-    double pad2;
+    double pad[3];
 };
+
+// per-(row, chunk) data of one top-p round; rewritten every round
+struct RoundBuf {               // 3328 B
+    double coarse[CB_N];        // round 1: mass per coarse bin (relative to the chunk max)
+    double S;                   // round 1 / exact round: sum of weights
+    double above;               // mass of keys above the band
+    double kept;                // final: kept weight of the chunk (relative to the row max)
+    uint32_t cnt[RB_N];         // refine: count per sub-bin
+    uint64_t mass[RB_N];        // refine: mass per sub-bin, fixed point (2^-32 units)
+    double pad[13];
+};
+static_assert(sizeof(RoundBuf) == 3328, "RoundBuf size");
 
 struct RowOut {                 // 64 B per row, read by k_emit
     int64_t id;
@@ -112,10 +141,13 @@ struct RowOut {                 // 64 B per row, read by k_emit
     float m;                    // row max of y
     uint32_t cut_key;           // kept iff key > cut_key or (key == cut_key and j <= cut_i)
     int32_t cut_i;
-    int32_t pad;
+    int32_t topp;               // fp32 top-p rows: TP_* outcome of the rounds (cleared by the row pass)
     double S;                   // sum of kept weights exp(y - m)
     double pad2[3];
 };
+
+// outcome of an fp32 top-p row's rounds, for the row pass
+enum : int32_t { TP_NONE = 0, TP_CUT = 1, TP_REREAD = 2, TP_INVALID = 3 };
 
 struct Cand { float x; int32_t idx; };
 struct Elem { uint32_t key; int32_t idx; };
@@ -123,43 +155,55 @@ struct Elem { uint32_t key; int32_t idx; };
 struct Layout {
     int64_t B, V;
     int ept, G;
-    size_t ctl, rowctl, rowout, chunks, fbc, fbm, cand, subc, subm, win, amass, total;
+    size_t ctl, rowctl, rowout, chunks, rbuf, hist, cand, win, total;
 };
 
 static inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
+// Elements per thread: 16 for fp32 and 32 for 16-bit logits (16 KB chunks),
+// 16-bit down to 16 when the batch would launch too few workgroups to fill
+// the chip, 64 when the row needs more than G_MAX chunks.
 static Layout make_layout(int64_t B, int64_t V, int dtype)
 {
     Layout L;
     L.B = B; L.V = V;
-    (void)dtype;
-    static const int opts[4] = {64, 32, 16, 8};
-    L.ept = 8;
-    for (int i = 0; i < 4; ++i) {
-        const int64_t G = (V + (int64_t)NT * opts[i] - 1) / ((int64_t)NT * opts[i]);
-        if (B * G >= 1024 && G <= G_MAX) { L.ept = opts[i]; break; }
-    }
-    L.G = (int)((V + (int64_t)NT * L.ept - 1) / ((int64_t)NT * L.ept));
-    if (L.G > G_MAX) {
-        L.ept = 64;
-        L.G = (int)((V + (int64_t)NT * 64 - 1) / ((int64_t)NT * 64));
-    }
+    auto chunks = [&](int ept) { return (V + (int64_t)NT * ept - 1) / ((int64_t)NT * ept); };
+    L.ept = dtype == MIS_DTYPE_F32 ? 16 : 32;
+    if (dtype != MIS_DTYPE_F32 && B * chunks(32) < 1024) L.ept = 16;
+    if (chunks(L.ept) > G_MAX) L.ept = 64;
+    L.G = (int)chunks(L.ept);
     const size_t BG = (size_t)B * L.G;
     size_t off = 0;
     L.ctl = off;    off = align256(off + sizeof(Ctl));
     L.rowctl = off; off = CTL_PREFIX;
     L.rowout = off; off = align256(off + sizeof(RowOut) * (size_t)B);
     L.chunks = off; off = align256(off + sizeof(ChunkSum) * BG);
-    L.fbc = off;    off = align256(off + sizeof(uint32_t) * FB_N * BG);
-    L.fbm = off;    off = align256(off + sizeof(double) * FB_N * BG);
+    L.rbuf = off;   off = align256(off + sizeof(RoundBuf) * BG);
+    L.hist = off;   off = align256(off + sizeof(RowHist) * (size_t)B);
     L.cand = off;   off = align256(off + sizeof(Cand) * (size_t)CAND_CAP * BG);
-    L.subc = off;   off = align256(off + sizeof(uint32_t) * SUB_N * (size_t)B);
-    L.subm = off;   off = align256(off + sizeof(double) * SUB_N * (size_t)B);
-    L.win = off;    off = align256(off + sizeof(Elem) * WCAP * (size_t)B);
-    L.amass = off;  off = align256(off + sizeof(double) * G_MAX * (size_t)B);
+    L.win = off;    off = align256(off + sizeof(Elem) * (size_t)WCAP * (size_t)B);
     L.total = off;
     return L;
 }
+
+// ------------------------------------------------------------------ phase timestamps
+//
+// Built with -DMIS_TRACE, thread 0 of a workgroup records the 100 MHz real-time
+// counter at phase boundaries into a per-row table placed past the workspace
+// (the caller then sizes the workspace with mis_workspace_bytes() + the
+// table).  Off in the product build: the calls compile to nothing.
+[[maybe_unused]] constexpr int TR_SLOTS = 32;
+#ifdef MIS_TRACE
+__device__ __forceinline__ void trace(char *ws, const Layout &L, int row, int slot)
+{
+    if (threadIdx.x == 0 && slot < TR_SLOTS) {
+        uint64_t *t = reinterpret_cast<uint64_t *>(ws + L.total) + (size_t)row * TR_SLOTS + slot;
+        __hip_atomic_store(t, (uint64_t)__builtin_amdgcn_s_memrealtime(), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+#else
+__device__ __forceinline__ void trace(char *, const Layout &, int, int) {}
+#endif
 
 // ------------------------------------------------------------------ row plan
 
@@ -206,33 +250,33 @@ struct RowCx {                 // what the leader of a row works with
     int G;
     int64_t CH;
     int row;
-    const uint32_t *fbc;       // this row's chunk fine-bin counts [G][FB_N]
-    const double *fbm;         // this row's chunk fine-bin masses [G][FB_N]
-    uint32_t *subc;            // this row's sub-histogram [SUB_N]
-    double *subm;
 };
 
 // ------------------------------------------------------------------ shared memory
 
+// One LDS layout for every phase of the kernel (about 24 KB, so six
+// workgroups fit on a CU): the chunk phase's lane-private coarse bins and the
+// leader's survivor / window arrays share the big union.
 struct Smem {
     union {
-        struct { uint32_t cnt[FB_N]; double mass[FB_N]; } p1;                              // 4.5 KB
-        struct { uint32_t cnt[2048]; } h11;                                                // 8 KB
-        struct { uint32_t cnt[256]; double mass[256]; } h8;                                // 3 KB
-        struct { uint32_t key[SURV_CAP]; int32_t idx[SURV_CAP]; double e[SURV_CAP]; } s;   // 32 KB
-        struct { uint64_t k[SURV_CAP]; double e[SURV_CAP]; } so;                          // 32 KB
-        struct { uint32_t cnt[RUN_CAP]; uint32_t rkey[RUN_CAP]; uint32_t rcnt[RUN_CAP]; float rp[RUN_CAP]; } r;  // 32 KB
+        float lp[CB_N][NT];                                                                 // 16 KB lane-private coarse bins
+        struct { uint32_t cnt[RB_N]; unsigned long long mass[RB_N]; } rf;                  // refine sub-bins (shared, sparse)
+        struct { uint32_t cnt[2048]; } h11;                                                 // 8 KB
+        struct { uint32_t cnt[256]; double mass[256]; } h8;                                 // 3 KB
+        struct { uint32_t key[SURV_CAP]; int32_t idx[SURV_CAP]; double e[SURV_CAP]; } s;    // 16 KB
+        struct { uint64_t k[SURV_CAP]; double e[SURV_CAP]; } so;                           // 16 KB
+        struct { uint32_t cnt[RUN_CAP]; uint32_t rkey[RUN_CAP]; uint32_t rcnt[RUN_CAP]; float rp[RUN_CAP]; } r;
         struct { int32_t idx[TIE_CAP]; } t;
-        struct { float x[STAGE_CAP]; uint32_t j[STAGE_CAP]; } st;                          // 32 KB
+        struct { double m[RB_N]; uint32_t c[RB_N]; } mg;                                    // leader merge of sub-bins
     } u;
     union {
-        struct { double m[FB_N]; uint32_t c[FB_N]; } rb;    // row-merged fine bins, index FB_N-1 = top
         struct { uint32_t cnt[256]; double mass[256]; } l1;  // re-read path: level-1 histogram
+        double coarse[CB_N];                                 // leader merge of coarse bins
     } v;
     double cw[G_MAX];          // per-chunk kept weight
     double chs[G_MAX];         // per-chunk rescale to the row max
-    double sub_m[SUB_N];       // round-local histograms
-    uint32_t sub_c[SUB_N];
+    double sub_m[256];         // round-local histograms
+    uint32_t sub_c[256];
     Red red;
     uint32_t bu[8];
     int32_t bi[8];
@@ -242,18 +286,6 @@ struct Smem {
     Args args;                 // launch arguments, RowCx and RowPlan of the row for the
     RowCx cx;                  // leader's out-of-line functions (kept out of private
     RowPlan pl;                // memory, which would otherwise hold a copy per lane)
-};
-
-// LDS of the chunk pass: only what its per-mode reductions need, so that
-// several workgroups fit on a CU
-struct ChunkSmem {
-    union {
-        struct { uint32_t cnt[FB_N]; double mass[FB_N]; } p1;  // fine bins (fp32 top-p)
-        struct { uint32_t cnt[256]; double mass[256]; } h8;    // candidate threshold histogram
-    } u;
-    Red red;
-    uint32_t bu[8];
-    int32_t bi[8];
 };
 
 __device__ __forceinline__ bool kept_by_cut(uint32_t key, int64_t j, uint32_t cut_key, int32_t cut_i)
@@ -269,15 +301,23 @@ __device__ __forceinline__ float opaque(float v)
     return v;
 }
 
-// ------------------------------------------------------------------ chunk -> row hand-off
+// ------------------------------------------------------------------ cross-workgroup hand-off
 //
-// The chunk pass (k_chunk) writes per-chunk summaries, fine bins and
-// candidates; the row pass (k_final) reads them in the next launch on the
-// same stream, so the kernel boundary orders and publishes them.
+// Summaries, candidates and round data go through device-coherent (agent
+// scope) stores and loads, which bypass the XCD-private L2s, so a leader on
+// another XCD reads what its row mates wrote.  A workgroup publishes by
+// waiting for its own stores (s_waitcnt) before the barrier that precedes its
+// arrival atomic.
 
 template <class T> struct same_t { typedef T type; };
-template <class T> __device__ __forceinline__ void st_dev(T *p, typename same_t<T>::type v) { *p = v; }
-template <class T> __device__ __forceinline__ T ld_dev(const T *p) { return *p; }
+template <class T> __device__ __forceinline__ void st_dev(T *p, typename same_t<T>::type v)
+{
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <class T> __device__ __forceinline__ T ld_dev(const T *p)
+{
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 __device__ __forceinline__ void st_dev_cand(Cand *p, float x, int32_t idx)
 {
     st_dev(reinterpret_cast<uint64_t *>(p), ((uint64_t)(uint32_t)idx << 32) | f32_bits(x));
@@ -288,11 +328,70 @@ __device__ __forceinline__ Cand ld_dev_cand(const Cand *p)
     Cand c; c.x = bits_f32((uint32_t)v); c.idx = (int32_t)(uint32_t)(v >> 32);
     return c;
 }
+__device__ __forceinline__ void st_dev_elem(Elem *p, uint32_t key, int32_t idx)
+{
+    st_dev(reinterpret_cast<uint64_t *>(p), ((uint64_t)(uint32_t)idx << 32) | key);
+}
+__device__ __forceinline__ Elem ld_dev_elem(const Elem *p)
+{
+    const uint64_t v = ld_dev(reinterpret_cast<const uint64_t *>(p));
+    Elem e; e.key = (uint32_t)v; e.idx = (int32_t)(uint32_t)(v >> 32);
+    return e;
+}
+// The row pass runs after the chunk pass has completed, so it reads the
+// summaries with ordinary (cached, freely batched) loads.
+template <class T> __device__ __forceinline__ T ldp(const T *p) { return *p; }
+__device__ __forceinline__ Cand ldp_cand(const Cand *p)
+{
+    const uint64_t v = *reinterpret_cast<const uint64_t *>(p);
+    Cand c; c.x = bits_f32((uint32_t)v); c.idx = (int32_t)(uint32_t)(v >> 32);
+    return c;
+}
 // candidates a chunk wrote (its summary says so; never more than the buffer)
 __device__ __forceinline__ uint32_t ncand_of(const ChunkSum *cs)
 {
-    const uint32_t n = ld_dev(&cs->ncand);
+    const uint32_t n = ldp(&cs->ncand);
     return n < (uint32_t)CAND_CAP ? n : (uint32_t)CAND_CAP;
+}
+
+// Summaries only the row pass reads (after this kernel has completed) go
+// through ordinary stores; fp32 top-p rows, whose leader reads them during
+// the kernel, use the device-coherent ones.
+template <class T> __device__ __forceinline__ void st_sum(bool coherent, T *p, typename same_t<T>::type v)
+{
+    if (coherent) st_dev(p, v);
+    else *p = v;
+}
+
+// every thread's device-coherent stores are complete, then the workgroup
+// barrier: after it, thread 0 may signal arrival
+__device__ __forceinline__ void publish_barrier()
+{
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+}
+
+// Arrival of this workgroup at the row counter; returns the counter's old value.
+__device__ __forceinline__ uint32_t arrive(RowCtl *rc)
+{
+    return __hip_atomic_fetch_add(&rc->arr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Thread 0 waits until the row publishes a round beyond `r` or finishes
+// (one polled word).  Returns false when the spin limit expired (the row is
+// then abandoned).
+__device__ bool wait_round(RowCtl *rc, uint32_t r, uint32_t *err)
+{
+    uint32_t nap = 1;
+    for (uint32_t it = 0; it < SPIN_LIMIT; ++it) {
+        if (ld_dev(&rc->round) > r) return true;  // round r + 1 published, or ROUND_DONE
+        // back off: thousands of waiting workgroups must not flood the
+        // memory system with polls
+        if (nap < 8) { __builtin_amdgcn_s_sleep(4); ++nap; }
+        else __builtin_amdgcn_s_sleep(16);
+    }
+    __hip_atomic_fetch_or(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return false;
 }
 
 // raw-key interval for a scaled-key interval, computed by wave 0
@@ -395,26 +494,20 @@ __device__ int64_t draw_in_chunk(Smem &sm, const RowCx &c, int g, double resid, 
 __device__ void pick_chunk(Smem &sm, int G, float u, int *g_out, double *resid_out, double *S_out)
 {
     __syncthreads();
-    if (threadIdx.x == 0) {
+    if (wave_id() == 0) {
         double S = 0.0;
-        for (int g = 0; g < G; ++g) S += sm.cw[g];
-        double target = (double)u * S, cum = 0.0;
-        int gsel = -1;
-        for (int g = 0; g < G; ++g) {
-            if (sm.cw[g] > 0.0) {
-                if (cum + sm.cw[g] > target) { gsel = g; break; }
-                cum += sm.cw[g];
-            }
+        for (int g = lane_id(); g < G; g += 64) S += sm.cw[g];
+        S = wave_sum(S);
+        double bef;
+        const int gsel = wave_find_asc(sm.cw, G, (double)u * S, &bef);
+        if (lane_id() == 0) {
+            sm.bd[0] = S;
+            // target - sum before the chunk; the rounding fallback keeps it inside
+            double r = (double)u * S - bef;
+            if (gsel >= 0 && !(r < sm.cw[gsel])) r = sm.cw[gsel];
+            sm.bd[1] = r < 0.0 ? 0.0 : r;
+            sm.bi[0] = gsel;
         }
-        if (gsel < 0) {  // rounding: the last chunk with weight, its last kept element
-            for (int g = G - 1; g >= 0; --g) if (sm.cw[g] > 0.0) { gsel = g; break; }
-            cum = 0.0;
-            for (int g = 0; g < gsel; ++g) cum += sm.cw[g];
-            target = cum + (gsel >= 0 ? sm.cw[gsel] : 0.0);
-        }
-        sm.bd[0] = S;
-        sm.bd[1] = target - cum;
-        sm.bi[0] = gsel;
     }
     __syncthreads();
     *S_out = sm.bd[0];
@@ -439,24 +532,17 @@ __device__ int64_t draw_in_list(Smem &sm, const int32_t *idx, const double *e, i
             if (j >= lo && j < hi && e[i] > 0.0) atomicAdd(&sm.sub_m[(j - lo) / width], e[i]);
         }
         __syncthreads();
-        if (threadIdx.x == 0) {
-            double cum = acc;
-            int bsel = -1;
-            for (int b = 0; b < 256; ++b) {
-                if (sm.sub_m[b] > 0.0) {
-                    if (cum + sm.sub_m[b] > target) { bsel = b; break; }
-                    cum += sm.sub_m[b];
-                }
+        if (wave_id() == 0) {
+            double bef;
+            int bsel = wave_find_asc(sm.sub_m, 256, target - acc, &bef);
+            if (lane_id() == 0) {
+                double tg = target;
+                // rounding fallback (the last element with weight): aim past the end
+                if (bsel >= 0 && !(acc + bef + sm.sub_m[bsel] > target)) tg = 1e300;
+                sm.bi[1] = bsel;
+                sm.bd[2] = acc + bef;
+                sm.bd[3] = tg;
             }
-            if (bsel < 0) {  // rounding: the last element with weight
-                for (int b = 255; b >= 0; --b) if (sm.sub_m[b] > 0.0) { bsel = b; break; }
-                cum = acc;
-                for (int b = 0; b < bsel; ++b) cum += sm.sub_m[b];
-                target = 1e300;
-            }
-            sm.bi[1] = bsel;
-            sm.bd[2] = cum;
-            sm.bd[3] = target;
         }
         __syncthreads();
         const int b = sm.bi[1];
@@ -468,71 +554,6 @@ __device__ int64_t draw_in_list(Smem &sm, const int32_t *idx, const double *e, i
         hi = lo + width < hi ? lo + width : hi;
     }
     return lo;
-}
-
-// Cut inside a candidate window held in LDS (key, idx, e): mass descent over
-// the keys to the running mass Aw (descending order, ties by index).
-__device__ void window_cut(Smem &sm, const uint32_t *key, const int32_t *idx, const double *e, uint32_t n,
-                           double Aw, double e_of_key_dummy, uint32_t *cut_key, int32_t *cut_i, int dt)
-{
-    (void)e_of_key_dummy;
-    uint32_t prefix = 0u;
-    double acc = 0.0;
-    uint32_t kc = 0;
-    double ekey = 0.0;
-    for (int lev = 0; lev < 4; ++lev) {
-        const int sh = 24 - 8 * lev;
-        const uint32_t hmask = lev == 0 ? 0u : ~((1u << (sh + 8)) - 1u);
-        __syncthreads();
-        for (int i = threadIdx.x; i < 256; i += NT) { sm.sub_m[i] = 0.0; sm.sub_c[i] = 0u; }
-        __syncthreads();
-        for (uint32_t i = threadIdx.x; i < n; i += NT) {
-            const uint32_t k = key[i];
-            if ((k & hmask) == (prefix & hmask)) {
-                atomicAdd(&sm.sub_m[(k >> sh) & 255u], e[i]);
-                atomicAdd(&sm.sub_c[(k >> sh) & 255u], 1u);
-            }
-        }
-        __syncthreads();
-        if (wave_id() == 0) {
-            double ab;
-            const int d = wave_find_desc<double>(sm.sub_m, 256, Aw - acc, &ab);
-            if (lane_id() == 0) { sm.bu[0] = (uint32_t)d; sm.bd[0] = ab; sm.bu[1] = sm.sub_c[d]; }
-        }
-        __syncthreads();
-        prefix |= sm.bu[0] << sh;
-        acc += sm.bd[0];
-        kc = sm.bu[1];
-        __syncthreads();
-    }
-    // the weight of one element holding the resolved key
-    if (threadIdx.x == 0) sm.bd[1] = 0.0;
-    __syncthreads();
-    for (uint32_t i = threadIdx.x; i < n; i += NT) if (key[i] == prefix) sm.bd[1] = e[i];
-    __syncthreads();
-    ekey = sm.bd[1];
-    __syncthreads();
-    double tt = ekey > 0.0 ? ceil((Aw - acc) / ekey) : 1.0;
-    if (!(tt >= 1.0)) tt = 1.0;
-    if (tt > (double)kc) tt = (double)kc;
-    uint32_t t = (uint32_t)tt;
-    while (t > 1 && acc + (double)(t - 1) * ekey >= Aw) --t;
-    while (t < kc && acc + (double)t * ekey < Aw) ++t;
-    *cut_key = prefix;
-    *cut_i = IDX_ALL;
-    if (t < kc) {  // the t-th smallest index among the elements holding the key
-        for (uint32_t i = threadIdx.x; i < n; i += NT) {
-            if (key[i] != prefix) continue;
-            const int32_t v = idx[i];
-            uint32_t r = 0;
-            for (uint32_t q = 0; q < n; ++q) r += (key[q] == prefix && idx[q] < v) ? 1u : 0u;
-            if (r == t - 1u) sm.bi[0] = v;
-        }
-        __syncthreads();
-        *cut_i = sm.bi[0];
-        __syncthreads();
-    }
-    (void)dt;
 }
 
 // ------------------------------------------------------------------ re-read path
@@ -846,12 +867,74 @@ __device__ __noinline__ void final_generic(Smem &sm, const RowCx &c, const RowPl
     write_row(ro, a, c.row, id, id >= 0 ? MIS_ROW_OK : MIS_ROW_INVALID, pl.mode, c.m, cut_key, cut_i, SK);
 }
 
+// The window's cut.  Input: n <= SURV_CAP elements in sm.u.s (key, idx, e),
+// `above` = mass of everything ranked before the window, A = the target
+// (an element is kept iff the mass before it is < A).  The window is sorted
+// into the stable descending order in sm.u.so (composite key
+// key << 32 | ~idx, mass); the last kept element is found by a block scan.
+// Returns its sorted position, or -1 when the cut is not inside the window.
+// *q_last = mass before the last kept element, *w_last = its weight.
+__device__ int window_resolve(Smem &sm, uint32_t n, double above, double A, uint32_t *cut_key, int32_t *cut_i,
+                              double *q_last, double *w_last)
+{
+    constexpr int PT = SURV_CAP / NT;
+    const int tid = threadIdx.x;
+    uint64_t kt[PT];
+    double et[PT];
+#pragma unroll
+    for (int q = 0; q < PT; ++q) {
+        const int i = q * NT + tid;
+        const bool in = i < (int)n;
+        kt[q] = in ? (((uint64_t)sm.u.s.key[i] << 32) | (uint64_t)(0xffffffffu - (uint32_t)sm.u.s.idx[i])) : 0ull;
+        et[q] = in ? sm.u.s.e[i] : 0.0;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < PT; ++q) { sm.u.so.k[q * NT + tid] = kt[q]; sm.u.so.e[q * NT + tid] = et[q]; }
+    __syncthreads();
+    block_sort_desc(sm.u.so.k, sm.u.so.e, (int)n);
+    // thread t scans the sorted positions [t*PT, t*PT + PT)
+    double local = 0.0;
+#pragma unroll
+    for (int q = 0; q < PT; ++q) { const int r = tid * PT + q; local += r < (int)n ? sm.u.so.e[r] : 0.0; }
+    double tot;
+    const double off = block_excl_scan<double>(local, sm.red, &tot);
+    if (tid == 0) { sm.bi[4] = -1; }
+    __syncthreads();
+    double run = above + off;
+    int cand = -1;
+    double qc = 0.0;
+#pragma unroll
+    for (int q = 0; q < PT; ++q) {
+        const int r = tid * PT + q;
+        if (r < (int)n) {
+            if (run < A) { cand = r; qc = run; }
+            run += sm.u.so.e[r];
+        }
+    }
+    atomicMax(&sm.bi[4], cand);
+    __syncthreads();
+    const int rl = sm.bi[4];
+    if (rl >= 0 && cand == rl) sm.bd[5] = qc;
+    __syncthreads();
+    if (rl < 0) return -1;                                     // the first window element is removed
+    if (rl == (int)n - 1 && !(above + tot >= A)) return -1;    // every window element is kept
+    const uint64_t ck = sm.u.so.k[rl];
+    *cut_key = (uint32_t)(ck >> 32);
+    *cut_i = (int32_t)(0xffffffffu - (uint32_t)ck);
+    *q_last = sm.bd[5];
+    *w_last = sm.u.so.e[rl];
+    return rl;
+}
+
 // ------------------------------------------------------------------ small top-k leader
 
 // Exact k'-th value over the per-chunk candidates, survivors, optional top-p,
-// draw.  Returns false when the survivors overflow LDS.
+// draw.  Returns false (the caller then re-reads the row) when a chunk
+// overflowed its candidate buffer, when a truncated chunk may hide an element
+// at or above the k'-th value, or when the survivors overflow LDS.
 template <int DT>
-__device__ __noinline__ bool final_smallk(Smem &sm, const RowCx &c, const RowPlan &pl, const ChunkSum *cs,
+__device__ __noinline__ bool leader_smallk(Smem &sm, const RowCx &c, const RowPlan &pl, const ChunkSum *cs,
                                           const Cand *cand, RowOut *ro, const Args &a)
 {
     const double md = (double)c.m;
@@ -868,6 +951,22 @@ __device__ __noinline__ bool final_smallk(Smem &sm, const RowCx &c, const RowPla
     __syncthreads();
     const uint32_t ntot = pre[c.G];
     const int G = c.G;
+    // chunk facts: overflow, truncation, finite counts
+    uint32_t ovf = 0, ntr = 0, nfin = 0;
+    for (int g = threadIdx.x; g < G; g += NT) {
+        ovf |= ldp(&cs[g].ncand) == NCAND_OVERFLOW ? 1u : 0u;
+        ntr |= ldp(&cs[g].trunc) != 0u ? 1u : 0u;
+        nfin += ldp(&cs[g].nfin);
+    }
+    ovf = block_sum<uint32_t>(ovf, sm.red);
+    ntr = block_sum<uint32_t>(ntr, sm.red);
+    nfin = block_sum<uint32_t>(nfin, sm.red);
+    trace(a.ws, a.L, c.row, 17);
+    if (ovf != 0u) return false;
+    // fewer finite elements than k': the k'-th value is -inf and every finite
+    // element survives, which the candidates hold only if no chunk truncated
+    const bool all_fin = nfin <= (uint32_t)pl.kk;
+    if ((all_fin && ntr != 0u) || (!all_fin && ntot < (uint32_t)pl.kk)) return false;
     auto cand_ptr = [&](uint32_t f) -> const Cand * {
         int lo = 0, hi = G - 1;  // last g with pre[g] <= f
         while (lo < hi) {
@@ -880,7 +979,7 @@ __device__ __noinline__ bool final_smallk(Smem &sm, const RowCx &c, const RowPla
     // k'-th largest raw key over the candidates: 11 / 11 / 10-bit digits.  Fewer
     // candidates than k' means fewer finite elements than k' in the row.
     uint32_t xk_thr = 0u;
-    if (ntot >= (uint32_t)pl.kk) {
+    if (!all_fin) {
         uint32_t prefix = 0u, rem = (uint32_t)pl.kk;
         for (int lev = 0; lev < 3; ++lev) {
             const int sh = lev == 0 ? 21 : (lev == 1 ? 10 : 0);
@@ -900,7 +999,7 @@ __device__ __noinline__ bool final_smallk(Smem &sm, const RowCx &c, const RowPla
                 }
                 uint32_t kv[BATCH];
 #pragma unroll
-                for (int u = 0; u < BATCH; ++u) kv[u] = key_of_f32(ld_dev_cand(cp[u]).x);
+                for (int u = 0; u < BATCH; ++u) kv[u] = key_of_f32(ldp_cand(cp[u]).x);
 #pragma unroll
                 for (int u = 0; u < BATCH; ++u) {
                     const uint32_t f = f0 + (uint32_t)(u * NT) + threadIdx.x;
@@ -924,6 +1023,16 @@ __device__ __noinline__ bool final_smallk(Smem &sm, const RowCx &c, const RowPla
     // survivors: scaled value >= scale(k'-th raw value); the ties the scaling
     // creates are kept, as the reference keeps them
     const uint32_t thr_key = xk_thr ? row_key(scale_y<DT>(f32_of_key(xk_thr), c.T), DT) : 0u;
+    trace(a.ws, a.L, c.row, 18);
+    // exactness: a truncated chunk left out only elements with scaled keys
+    // below its kc; they cannot reach the threshold if kc <= thr_key
+    if (ntr != 0u) {
+        uint32_t hide = 0;
+        for (int g = threadIdx.x; g < G; g += NT)
+            hide |= (ldp(&cs[g].trunc) != 0u && ldp(&cs[g].kc) > thr_key) ? 1u : 0u;
+        hide = block_sum<uint32_t>(hide, sm.red);
+        if (hide != 0u) return false;
+    }
     if (threadIdx.x == 0) sm.bu[3] = 0u;
     __syncthreads();
     for (uint32_t f0 = 0; f0 < ntot; f0 += NT * BATCH) {
@@ -935,7 +1044,7 @@ __device__ __noinline__ bool final_smallk(Smem &sm, const RowCx &c, const RowPla
         }
         Cand cv[BATCH];
 #pragma unroll
-        for (int u = 0; u < BATCH; ++u) cv[u] = ld_dev_cand(cp[u]);
+        for (int u = 0; u < BATCH; ++u) cv[u] = ldp_cand(cp[u]);
 #pragma unroll
         for (int u = 0; u < BATCH; ++u) {
             const uint32_t f = f0 + (uint32_t)(u * NT) + threadIdx.x;
@@ -952,6 +1061,7 @@ __device__ __noinline__ bool final_smallk(Smem &sm, const RowCx &c, const RowPla
     __syncthreads();
     const uint32_t ns = sm.bu[3];
     __syncthreads();
+    trace(a.ws, a.L, c.row, 19);
     if (ns > (uint32_t)SURV_CAP || ns == 0) return false;
 
     uint32_t cut_key = thr_key;
@@ -962,7 +1072,28 @@ __device__ __noinline__ bool final_smallk(Smem &sm, const RowCx &c, const RowPla
         for (uint32_t i = threadIdx.x; i < ns; i += NT) S += sm.u.s.e[i];
         S = block_sum<double>(S, sm.red);
         if (DT == F32) {
-            window_cut(sm, sm.u.s.key, sm.u.s.idx, sm.u.s.e, ns, (double)pl.top_p * S, 0.0, &cut_key, &cut_i, DT);
+            // exact masses over the survivors: sorted cut, then back to the
+            // (key, idx, e) view the draw reads
+            double ql, wl;
+            const int rl = window_resolve(sm, ns, 0.0, (double)pl.top_p * S, &cut_key, &cut_i, &ql, &wl);
+            if (rl < 0) {  // every survivor kept (A at or beyond the total)
+                cut_key = thr_key;
+                cut_i = IDX_ALL;
+            }
+            constexpr int PT = SURV_CAP / NT;
+            uint64_t kt[PT];
+            double et[PT];
+            for (int q = 0; q < PT; ++q) { kt[q] = sm.u.so.k[threadIdx.x + q * NT]; et[q] = sm.u.so.e[threadIdx.x + q * NT]; }
+            __syncthreads();
+            for (int q = 0; q < PT; ++q) {
+                const int i = threadIdx.x + q * NT;
+                if (i < (int)ns) {
+                    sm.u.s.key[i] = (uint32_t)(kt[q] >> 32);
+                    sm.u.s.idx[i] = (int32_t)(0xffffffffu - (uint32_t)kt[q]);
+                    sm.u.s.e[i] = et[q];
+                }
+            }
+            __syncthreads();
         } else {
             // 16-bit rounding chain over the survivors in stable descending order
             int npow = 1;
@@ -1056,6 +1187,7 @@ __device__ __noinline__ bool final_smallk(Smem &sm, const RowCx &c, const RowPla
         write_row(ro, a, c.row, -1, status, pl.mode, c.m, 0u, 0, 0.0);
         return true;
     }
+    trace(a.ws, a.L, c.row, 20);
     double SK = 0.0;
     for (uint32_t i = threadIdx.x; i < ns; i += NT) {
         if (!kept_by_cut(sm.u.s.key[i], sm.u.s.idx[i], cut_key, cut_i)) sm.u.s.e[i] = 0.0;
@@ -1067,227 +1199,37 @@ __device__ __noinline__ bool final_smallk(Smem &sm, const RowCx &c, const RowPla
     return true;
 }
 
-// fp32 top-p.  Merge the chunks' fine bins (16 per unit of y below each
-// chunk max, float64 masses) on the row grid and find the bin holding the
-// cut.  Re-read the row -- it has just been read, so it comes from the
-// Infinity Cache -- to collect that bin's elements into LDS, histogramming
-// the bin first (256 sub-bins) when it is crowded.  The exact cut is then a
-// mass descent over at most SURV_CAP elements.  Per-chunk kept weights: the
-// chunk's whole bins above the window plus its part of the window.
-template <int DT>
-__device__ __noinline__ void final_topp32(Smem &sm, RowCx &c, const RowPlan &pl, const ChunkSum *csr, RowOut *ro,
-                                          const Args &a)
+
+// Smallest key in [lo, hi] where the monotone predicate (false ... true) holds,
+// hi + 1 when it holds nowhere.  Run by one whole wave (64-ary search).
+template <class P> __device__ uint32_t key_search(uint32_t lo, uint32_t hi, P &&pred)
 {
-    const int tid = threadIdx.x, G = c.G;
-    uint32_t anyflag = 0;
-    float m = -INFINITY;
-    for (int g = tid; g < G; g += NT) { anyflag |= csr[g].flags; m = fmaxf(m, csr[g].ymax); }
-    anyflag = block_sum<uint32_t>(anyflag ? 1u : 0u, sm.red);
-    m = block_max<float>(m, sm.red);
-    c.m = m;
-    if (anyflag != 0u || m == -INFINITY) {
-        write_row(ro, a, c.row, -1, MIS_ROW_INVALID, pl.mode, m, 0u, 0, 0.0);
-        return;
+    if (lo > hi) return hi + 1u;
+    if (pred(lo)) return lo;
+    if (!pred(hi)) return hi + 1u;
+    uint64_t a = lo, b = hi;  // pred(a) false, pred(b) true
+    while (b - a > 1) {
+        uint64_t step = (b - a) / 64;
+        if (step == 0) step = 1;
+        const uint64_t p = a + (uint64_t)(lane_id() + 1) * step;
+        const bool t = p >= b ? true : pred((uint32_t)p);
+        const uint64_t mk = __ballot(t);
+        if (mk == 0ull) { a = a + 64 * step; continue; }
+        const int f = __builtin_ctzll(mk);
+        const uint64_t nb = a + (uint64_t)(f + 1) * step;
+        if (nb < b) b = nb;
+        a = a + (uint64_t)f * step;
     }
-    const double md = (double)m;
-    const double gm = floor(md * (double)FB_W);
-    // chunk g's bin 0 sits offg[g] row bins below the row's bin 0 (-1: empty chunk)
-    int *offg = reinterpret_cast<int *>(sm.sub_c);
-    for (int g = tid; g < G; g += NT) {
-        const float yg = csr[g].ymax;
-        sm.chs[g] = yg == -INFINITY ? 0.0 : exp((double)yg - md);
-        offg[g] = yg == -INFINITY ? -1 : (int)(gm - csr[g].gmc);
-    }
-    __syncthreads();
-    double s = 0.0;
-    for (int g = tid; g < G; g += NT) if (offg[g] >= 0) s += csr[g].S * sm.chs[g];
-    const double S = block_sum<double>(s, sm.red);
-    const double A = (double)pl.top_p * S;
-    for (int rb = tid; rb < FB_N; rb += NT) {
-        double mm = 0.0;
-        uint32_t cc = 0;
-        for (int g0 = 0; g0 < G; g0 += 8) {
-            int off[8];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) off[u] = g0 + u < G ? offg[g0 + u] : -1;
-            double mv[8];
-            uint32_t cv[8];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                const int cb = rb - off[u];
-                const bool in = off[u] >= 0 && cb >= 0 && cb < FB_N;
-                const size_t at = (size_t)(g0 + u < G ? g0 + u : 0) * FB_N + (in ? cb : 0);
-                mv[u] = in ? c.fbm[at] : 0.0;
-                cv[u] = in ? c.fbc[at] : 0u;
-            }
-#pragma unroll
-            for (int u = 0; u < 8; ++u) { mm += mv[u] * (g0 + u < G ? sm.chs[g0 + u] : 0.0); cc += cv[u]; }
-        }
-        sm.v.rb.m[FB_N - 1 - rb] = mm;
-        sm.v.rb.c[FB_N - 1 - rb] = cc;
-    }
-    __syncthreads();
-    if (wave_id() == 0) {
-        double ab;
-        const int d = wave_find_desc<double>(sm.v.rb.m, FB_N, A, &ab);
-        double tot = 0.0;
-        for (int q = lane_id(); q < FB_N; q += 64) tot += sm.v.rb.m[q];
-        tot = wave_sum(tot);
-        if (lane_id() == 0) {
-            sm.bi[2] = (tot >= A) ? (FB_N - 1 - d) : -1;  // -1: the cut lies below the bins
-            sm.bd[4] = ab;
-            sm.bu[2] = sm.v.rb.c[d];
-        }
-    }
-    __syncthreads();
-    const int rbstar = sm.bi[2];
-    double A_above = sm.bd[4];
-    const uint32_t wcnt = sm.bu[2];
-    __syncthreads();
-    if (rbstar < 0) {
-        final_generic<DT>(sm, c, pl, ro, a);
-        return;
-    }
-    const double gb = gm - (double)rbstar;  // the bin is [gb/FB_W, (gb+1)/FB_W)
-    const float hlo = (float)(gb / (double)FB_W), hhi = (float)((gb + 1.0) / (double)FB_W);
-    const uint32_t klo = key_of_f32(hlo), khi = key_of_f32(hhi) - 1u;
-    // each chunk's whole bins above the window's row bin, one wave per chunk
-    for (int g = wave_id(); g < G; g += NWAVE) {
-        const int off = offg[g];
-        double w = 0.0;
-        if (off >= 0) {
-            const int nb = rbstar - off <= 0 ? 0 : (rbstar - off >= FB_N ? FB_N : rbstar - off);
-            const double *fm = c.fbm + (size_t)g * FB_N;
-            double t[FB_N / 64];
-#pragma unroll
-            for (int q = 0; q < FB_N / 64; ++q) {
-                const int cb = q * 64 + lane_id();
-                t[q] = cb < nb ? fm[cb] : 0.0;
-            }
-#pragma unroll
-            for (int q = 0; q < FB_N / 64; ++q) w += t[q];
-        }
-        w = wave_sum(w);
-        if (lane_id() == 0) sm.cw[g] = w * sm.chs[g];
-    }
-    uint32_t wklo = klo, wkhi = khi;  // the window; (wkhi, khi] adds to the chunks' weights
-    if (wcnt > (uint32_t)WCAP) {
-        // crowded bin: 256 sub-bins of [hlo, hhi) by a re-read (index 255 = top)
-        __syncthreads();
-        for (int i = tid; i < 256; i += NT) { sm.v.l1.cnt[i] = 0u; sm.v.l1.mass[i] = 0.0; }
-        uint32_t xlo, xhi;
-        x_interval<DT>(sm, klo, khi, c.T, &xlo, &xhi);
-        const float inv = 256.0f / (hhi - hlo);
-        rescan<DT>(c, xlo, xhi, [&](int64_t, float y, uint32_t k) {
-            if (k < klo || k > khi) return;
-            const int sb = min(255, (int)((hhi - y) * inv));
-            atomicAdd(&sm.v.l1.cnt[255 - sb], 1u);
-            atomicAdd(&sm.v.l1.mass[255 - sb], exp((double)y - md));
-        });
-        __syncthreads();
-        if (wave_id() == 0) {
-            double ab;
-            const int d = wave_find_desc<double>(sm.v.l1.mass, 256, A - A_above, &ab);
-            if (lane_id() == 0) { sm.bi[3] = 255 - d; sm.bd[5] = ab; sm.bu[3] = sm.v.l1.cnt[d]; }
-        }
-        __syncthreads();
-        const int sstar = sm.bi[3];
-        A_above += sm.bd[5];
-        const uint32_t scnt = sm.bu[3];
-        __syncthreads();
-        // key range of sub-bin sstar inside [klo, khi]; the sub-bin index is
-        // non-increasing in the key
-        if (wave_id() == 0) {
-            auto sbk = [&](uint32_t k) -> int { return min(255, (int)((hhi - f32_of_key(k)) * inv)); };
-            uint64_t lo = klo, hi = khi;  // smallest key with sbk <= sstar
-            if (sbk(klo) <= sstar) hi = klo;
-            else {
-                while (hi - lo > 1) {
-                    uint64_t step = (hi - lo) / 64; if (step == 0) step = 1;
-                    const uint64_t p = lo + (uint64_t)(lane_id() + 1) * step;
-                    const bool pred = p >= hi ? true : (sbk((uint32_t)p) <= sstar);
-                    const uint64_t mk = __ballot(pred);
-                    if (mk == 0ull) { lo = lo + 64 * step; continue; }
-                    const int f = __builtin_ctzll(mk);
-                    const uint64_t nhi = lo + (uint64_t)(f + 1) * step;
-                    if (nhi < hi) hi = nhi;
-                    lo = lo + (uint64_t)f * step;
-                }
-            }
-            uint64_t lo2 = klo, hi2 = khi;  // largest key with sbk >= sstar
-            if (sbk(khi) >= sstar) lo2 = khi;
-            else {
-                while (hi2 - lo2 > 1) {
-                    uint64_t step = (hi2 - lo2) / 64; if (step == 0) step = 1;
-                    const uint64_t p = lo2 + (uint64_t)(lane_id() + 1) * step;
-                    const bool pred = p >= hi2 ? true : (sbk((uint32_t)p) < sstar);
-                    const uint64_t mk = __ballot(pred);
-                    if (mk == 0ull) { lo2 = lo2 + 64 * step; continue; }
-                    const int f = __builtin_ctzll(mk);
-                    const uint64_t nhi = lo2 + (uint64_t)(f + 1) * step;
-                    if (nhi < hi2) hi2 = nhi;
-                    lo2 = lo2 + (uint64_t)f * step;
-                }
-            }
-            if (lane_id() == 0) { sm.bu[4] = (uint32_t)hi; sm.bu[5] = (uint32_t)lo2; }
-        }
-        __syncthreads();
-        wklo = sm.bu[4];
-        wkhi = sm.bu[5];
-        __syncthreads();
-        if (scnt > (uint32_t)WCAP || wklo > wkhi) {
-            final_generic<DT>(sm, c, pl, ro, a);
-            return;
-        }
-    }
-    // collect [wklo, wkhi] into LDS; (wkhi, khi] is kept mass of its chunks
-    __syncthreads();
-    if (tid == 0) sm.bu[6] = 0u;
-    uint32_t xlo, xhi;
-    x_interval<DT>(sm, wklo, khi, c.T, &xlo, &xhi);
-    rescan<DT>(c, xlo, xhi, [&](int64_t j, float y, uint32_t k) {
-        if (k < wklo || k > khi) return;
-        const double e = exp((double)y - md);
-        if (k <= wkhi) {
-            const uint32_t p = atomicAdd(&sm.bu[6], 1u);
-            if (p < (uint32_t)SURV_CAP) { sm.u.s.key[p] = k; sm.u.s.idx[p] = (int32_t)j; sm.u.s.e[p] = e; }
-        } else {
-            atomicAdd(&sm.cw[j / c.CH], e);
-        }
-    });
-    __syncthreads();
-    const uint32_t nw0 = sm.bu[6];
-    __syncthreads();
-    if (nw0 > (uint32_t)SURV_CAP) {
-        final_generic<DT>(sm, c, pl, ro, a);
-        return;
-    }
-    const uint32_t nw = nw0;
-    uint32_t cut_key;
-    int32_t cut_i;
-    window_cut(sm, sm.u.s.key, sm.u.s.idx, sm.u.s.e, nw, A - A_above, 0.0, &cut_key, &cut_i, DT);
-    for (uint32_t i = tid; i < nw; i += NT)
-        if (kept_by_cut(sm.u.s.key[i], sm.u.s.idx[i], cut_key, cut_i))
-            atomicAdd(&sm.cw[sm.u.s.idx[i] / c.CH], sm.u.s.e[i]);
-    int gsel;
-    double resid, SK;
-    pick_chunk(sm, G, pl.u, &gsel, &resid, &SK);
-    int64_t id = -1;
-    if (gsel >= 0) {
-        const float T = pl.T;
-        id = draw_in_chunk<DT>(sm, c, gsel, resid, [&](float xv, int64_t j) -> double {
-            const float y = scale_y<DT>(xv, T);
-            return (y != -INFINITY && kept_by_cut(row_key(y, DT), j, cut_key, cut_i)) ? exp((double)y - md) : 0.0;
-        });
-    }
-    write_row(ro, a, c.row, id, id >= 0 ? MIS_ROW_OK : MIS_ROW_INVALID, pl.mode, m, cut_key, cut_i, SK);
+    return (uint32_t)b;
 }
+
+// ------------------------------------------------------------------ row leaders
 
 // Leader of a row that needs no refinement rounds: greedy, temperature only,
 // small top-k, and the re-read path for everything else.
 template <int DT>
-__device__ __noinline__ void final_row(Smem &sm, RowCx &c, const RowPlan &pl, const ChunkSum *csr, RowOut *ro,
-                                       const Args &a)
+__device__ __noinline__ void leader_row(Smem &sm, RowCx &c, const RowPlan &pl, const ChunkSum *csr, RowOut *ro,
+                                        const Args &a)
 {
     const int tid = threadIdx.x, row = c.row;
     const Layout &L = a.L;
@@ -1300,93 +1242,398 @@ __device__ __noinline__ void final_row(Smem &sm, RowCx &c, const RowPlan &pl, co
     uint32_t anyflag = 0u;
     float m = -INFINITY;
     for (int g = tid; g < L.G; g += NT) {
-        ChunkSum s;
-        s.xkey = ld_dev(&csr[g].xkey); s.xarg = ld_dev(&csr[g].xarg);
-        s.flags = ld_dev(&csr[g].flags); s.ymax = ld_dev(&csr[g].ymax);
-        if (s.xkey > k2 || (s.xkey == k2 && s.xarg < i2)) { k2 = s.xkey; i2 = s.xarg; }
-        anyflag |= s.flags;
-        m = fmaxf(m, s.ymax);
+        const uint32_t xk = ldp(&csr[g].xkey);
+        const int32_t xa = ldp(&csr[g].xarg);
+        if (xk > k2 || (xk == k2 && xa < i2)) { k2 = xk; i2 = xa; }
+        anyflag |= ldp(&csr[g].flags);
+        m = fmaxf(m, ldp(&csr[g].ymax));
     }
-    wave_argmax(k2, i2);
-    if (lane_id() == 0) { sm.red.u[wave_id()] = k2; sm.red.l[wave_id()] = i2; }
-    __syncthreads();
-    if (tid == 0) {
-        for (int w = 1; w < NWAVE; ++w) {
-            const uint32_t kk = sm.red.u[w];
-            const int32_t ii = (int32_t)sm.red.l[w];
-            if (kk > k2 || (kk == k2 && ii < i2)) { k2 = kk; i2 = ii; }
+    if (pl.mode == M_GREEDY) {
+        wave_argmax(k2, i2);
+        if (lane_id() == 0) { sm.red.u[wave_id()] = k2; sm.red.l[wave_id()] = i2; }
+        __syncthreads();
+        if (tid == 0) {
+            for (int w = 1; w < NWAVE; ++w) {
+                const uint32_t kk = sm.red.u[w];
+                const int32_t ii = (int32_t)sm.red.l[w];
+                if (kk > k2 || (kk == k2 && ii < i2)) { k2 = kk; i2 = ii; }
+            }
+            write_row(ro, a, row, i2, MIS_ROW_OK, pl.mode, 0.0f, 0u, i2, 1.0);
         }
-        sm.bi[0] = i2;
+        return;
     }
-    __syncthreads();
-    i2 = sm.bi[0];
-    __syncthreads();
     anyflag = block_sum<uint32_t>(anyflag ? 1u : 0u, sm.red);
     m = block_max<float>(m, sm.red);
     c.m = m;
     const double md = (double)m;
-    if (pl.mode == M_GREEDY) {
-        write_row(ro, a, row, i2, MIS_ROW_OK, pl.mode, 0.0f, 0u, i2, 1.0);
-    } else if (anyflag != 0u || m == -INFINITY) {
+    if (anyflag != 0u || m == -INFINITY) {
         write_row(ro, a, row, -1, MIS_ROW_INVALID, pl.mode, m, 0u, 0, 0.0);
     } else if (pl.mode == M_TEMP) {
         // chunk weights are exp(y - ymax_c): rescale to the row max m
         for (int g = tid; g < L.G; g += NT) {
-            const float yg = ld_dev(&csr[g].ymax);
+            const float yg = ldp(&csr[g].ymax);
             sm.chs[g] = yg == -INFINITY ? 0.0 : exp((double)yg - md);
-            sm.cw[g] = ld_dev(&csr[g].S) * sm.chs[g];
+            sm.cw[g] = ldp(&csr[g].S) * sm.chs[g];
         }
         int gsel;
         double resid, SK;
         pick_chunk(sm, L.G, pl.u, &gsel, &resid, &SK);
         int64_t id = -1;
         if (gsel >= 0) {
-            constexpr float L2E = 1.44269504088896341f;
-            const float yc = ld_dev(&csr[gsel].ymax), T = pl.T;
+            // the chunk pass's weights, recomputed the same way
+            const float yc = ldp(&csr[gsel].ymax), T = pl.T;
             id = draw_in_chunk<DT>(sm, c, gsel, resid / sm.chs[gsel], [&](float xv, int64_t) -> double {
-                return (double)exp2f((scale_y<DT>(xv, T) - yc) * L2E);
+                return (double)wexp(scale_y<DT>(xv, T), yc);
             });
         }
         write_row(ro, a, row, id, id >= 0 ? MIS_ROW_OK : MIS_ROW_INVALID, pl.mode, m, row_key(-INFINITY, DT), -1, SK);
     } else if (pl.mode == M_SMALLK) {
-        bool ovf = false;
-        for (int g = 0; g < L.G; ++g) ovf |= (ld_dev(&csr[g].ncand) == NCAND_OVERFLOW);
         const Cand *cand = reinterpret_cast<const Cand *>(a.ws + L.cand) + (size_t)row * L.G * CAND_CAP;
-        bool done = false;
-        if (!ovf) done = final_smallk<DT>(sm, c, pl, csr, cand, ro, a);
-        if (!done) final_generic<DT>(sm, c, pl, ro, a);
+        if (!leader_smallk<DT>(sm, c, pl, csr, cand, ro, a)) final_generic<DT>(sm, c, pl, ro, a);
     } else {
         final_generic<DT>(sm, c, pl, ro, a);
     }
 }
 
-// ------------------------------------------------------------------ the chunk pass
+// Per-chunk scale factors exp(ymax_c - m) into sm.chs; returns the row max m
+// and whether any chunk flagged NaN / +inf.  One load pair per chunk and
+// thread, issued together.
+__device__ float row_scales(Smem &sm, const ChunkSum *csr, int G, uint32_t *bad)
+{
+    uint32_t anyflag = 0u;
+    float m = -INFINITY;
+    for (int g = threadIdx.x; g < G; g += NT) {
+        const uint32_t f = ld_dev(&csr[g].flags);
+        const float yg = ld_dev(&csr[g].ymax);
+        anyflag |= f;
+        m = fmaxf(m, yg);
+        sm.chs[g] = (double)yg;
+    }
+    anyflag = block_sum<uint32_t>(anyflag ? 1u : 0u, sm.red);
+    m = block_max<float>(m, sm.red);
+    const double md = (double)m;
+    for (int g = threadIdx.x; g < G; g += NT) {
+        const double yg = sm.chs[g];
+        sm.chs[g] = (yg == -INFINITY || m == -INFINITY) ? 0.0 : exp(yg - md);
+    }
+    __syncthreads();
+    *bad = anyflag;
+    return m;
+}
 
-// One workgroup per (row, chunk): one coalesced read of the chunk into
-// registers -- the only HBM read of the logits -- reduced to the chunk
-// summary the row pass needs for the row's mode.
+__device__ __forceinline__ float coarse_bin(float y) { return floorf(y * CB_SCALE); }
+__device__ __forceinline__ int sub_bin(float y, float lo, float sc)
+{
+    return (int)fminf(fmaxf(floorf((y - lo) * sc), 0.0f), (float)(RB_N - 1));
+}
+
+// Publishes the next round of an fp32 top-p row (thread 0 writes RowCtl).
+__device__ void publish_round(RowCtl *rc, uint32_t r_next, uint32_t rtype, uint32_t klo, uint32_t khi, uint32_t nref)
+{
+    if (threadIdx.x == 0) {
+        const float lo = f32_of_key(klo), hi = f32_of_key(khi);
+        const float sc = hi > lo ? (float)RB_N / (hi - lo) : 0.0f;
+        st_dev(&rc->rtype, rtype);
+        st_dev(&rc->klo, klo);
+        st_dev(&rc->khi, khi);
+        st_dev(&rc->lo, lo);
+        st_dev(&rc->sc, sc);
+        st_dev(&rc->nref, nref);
+        if (rtype == R_COLLECT) st_dev(&rc->wcount, 0u);
+        __builtin_amdgcn_s_waitcnt(0);
+        st_dev(&rc->round, r_next);
+    }
+}
+
+// Final outcome of an fp32 top-p row's rounds: recorded for the row pass
+// (which draws, or re-reads the row), then the row mates are released.
+__device__ void topp_outcome(RowCtl *rc, RowOut *ro, int32_t outcome, float m, uint32_t cut_key, int32_t cut_i,
+                             double S)
+{
+    if (threadIdx.x == 0) {
+        ro->m = m;
+        ro->cut_key = cut_key;
+        ro->cut_i = cut_i;
+        ro->S = S;
+        ro->topp = outcome;
+        __builtin_amdgcn_s_waitcnt(0);
+        st_dev(&rc->round, ROUND_DONE);
+    }
+}
+
+// Leader of an fp32 top-p row once all its chunks have finished round r
+// (1 = coarse bins, else the kind in rc->rtype).  Publishes round r + 1, or
+// finishes the row: the cut and the per-chunk kept weights (TP_CUT), or a
+// hand-over to the row pass's re-read path (TP_REREAD), or TP_INVALID.
+// Reads of the row mates' data are issued in batches: each dependent
+// device-coherent load costs a full memory round trip.
+template <int DT>
+__device__ __noinline__ void leader_topp(Smem &sm, RowCx &c, const RowPlan &pl, const ChunkSum *csr, RoundBuf *rbf,
+                                         RowCtl *rc, RowHist *hist, const Elem *win, RowOut *ro, uint32_t r)
+{
+    const int tid = threadIdx.x, G = c.G;
+    if (tid == 0) {  // the row's control words, loaded together
+        const uint32_t rt = ld_dev(&rc->rtype), k0 = ld_dev(&rc->klo), k1 = ld_dev(&rc->khi);
+        const uint32_t nr = ld_dev(&rc->nref), nw = ld_dev(&rc->wcount);
+        const float lo = ld_dev(&rc->lo), sc = ld_dev(&rc->sc);
+        const double S = ld_dev(&rc->S), A = ld_dev(&rc->A);
+        sm.bu[0] = rt; sm.bu[1] = k0; sm.bu[2] = k1; sm.bu[3] = nr; sm.bu[4] = nw;
+        sm.bf[1] = lo; sm.bf[2] = sc; sm.bd[6] = S; sm.bd[7] = A;
+    }
+    uint32_t bad;
+    const float m = row_scales(sm, csr, G, &bad);  // its barriers publish the words above
+    c.m = m;
+    const double md = (double)m;
+    const uint32_t rtype = r == 1 ? 0u : sm.bu[0];
+    const uint32_t klo = sm.bu[1], khi = sm.bu[2], nref = sm.bu[3], nw0 = sm.bu[4];
+    const float blo = sm.bf[1], bsc = sm.bf[2];
+    const double S0 = sm.bd[6], A0 = sm.bd[7];
+    __syncthreads();
+    // the f32 weights of the chunk pass carry relative error <= WEXP_REL_ERR;
+    // band choices keep a wider margin, for the f32 and fixed-point bin sums
+    if (r == 1) {
+        if (bad != 0u || m == -INFINITY) {
+            topp_outcome(rc, ro, TP_INVALID, m, 0u, 0, 0.0);
+            return;
+        }
+        // S, and the coarse bins on the row grid: row bin b <-> coarse index Ar - b
+        const float Ar = coarse_bin(m);
+        double s = 0.0;
+        for (int g = tid; g < G; g += NT) s += ld_dev(&rbf[g].S) * sm.chs[g];
+        const double S = block_sum<double>(s, sm.red);
+        const double A = (double)pl.top_p * S;
+        if (tid < CB_N) sm.v.coarse[tid] = 0.0;
+        constexpr int GP = NT / CB_N;  // chunks per pass, one value per thread
+        for (int g0 = 0; g0 < G; g0 += GP) {
+            const int gl = tid / CB_N, lb = tid % CB_N, g = g0 + gl;
+            double v = 0.0;
+            int off = CB_N;  // row bin of chunk bin 0; CB_N = none
+            if (g < G) {
+                const double cv = ld_dev(&rbf[g].coarse[lb]);
+                const float yg = ld_dev(&csr[g].ymax);
+                if (yg != -INFINITY) { v = cv * sm.chs[g]; off = (int)(Ar - coarse_bin(yg)); }
+            }
+            sm.u.mg.m[tid] = v;             // [gl][lb]
+            if (lb == 0) sm.u.mg.c[gl] = (uint32_t)off;
+            __syncthreads();
+            if (tid < CB_N) {               // row bin tid <- chunk bin tid - off of each chunk
+                double acc = 0.0;
+                for (int q = 0; q < GP; ++q) {
+                    const int l2 = tid - (int)sm.u.mg.c[q];
+                    if (l2 >= 0 && l2 < CB_N) acc += sm.u.mg.m[q * CB_N + l2];
+                }
+                sm.v.coarse[tid] += acc;
+            }
+            __syncthreads();
+        }
+        if (tid == 0) {
+            const double delta = 1e-5 * S;
+            double cum = 0.0;
+            int ba = -1, bb = -1;
+            for (int b = 0; b < CB_N; ++b) {
+                const double nx = cum + sm.v.coarse[b];
+                if (nx >= A - delta && cum <= A + delta) { if (ba < 0) ba = b; bb = b; }
+                cum = nx;
+            }
+            sm.bi[0] = ba; sm.bi[1] = bb;
+            st_dev(&rc->m, m); st_dev(&rc->S, S); st_dev(&rc->A, A);
+        }
+        // the row histogram starts clear for the refine round
+        for (int j = tid; j < RB_N; j += NT) { st_dev(&hist->cnt[j], 0u); st_dev(&hist->mass[j], 0ull); }
+        __syncthreads();
+        const int ba = sm.bi[0], bb = sm.bi[1];
+        if (ba < 0) {  // the cut lies below the coarse range
+            topp_outcome(rc, ro, TP_REREAD, m, 0u, 0, 0.0);
+            return;
+        }
+        // key interval of coarse indices [Ar - bb, Ar - ba]
+        const float cb_lo = Ar - (float)bb, cb_hi = Ar - (float)ba;
+        if (wave_id() == 0) {
+            const uint32_t kfin = row_key(-INFINITY, DT) + 1u, ktop = 0xff7fffffu;  // finite keys
+            const uint32_t k0 = key_search(kfin, ktop, [&](uint32_t k) { return coarse_bin(f32_of_key(k)) >= cb_lo; });
+            const uint32_t k1 = key_search(kfin, ktop, [&](uint32_t k) { return coarse_bin(f32_of_key(k)) > cb_hi; }) - 1u;
+            if (lane_id() == 0) { sm.bu[5] = k0; sm.bu[6] = k1; }
+        }
+        __syncthreads();
+        publish_round(rc, 2u, R_REFINE, sm.bu[5], sm.bu[6], 0u);
+        return;
+    }
+    double above = 0.0;
+    for (int g = tid; g < G; g += NT) above += ld_dev(&rbf[g].above) * sm.chs[g];
+    above = block_sum<double>(above, sm.red);
+    if (rtype == R_REFINE) {
+        // the row histogram: one entry per thread, cleared behind the read
+        const uint32_t cn = ld_dev(&hist->cnt[tid]);
+        const unsigned long long ms = ld_dev(&hist->mass[tid]);
+        sm.u.mg.m[tid] = (double)ms * (1.0 / HIST_SCALE);
+        sm.u.mg.c[tid] = cn;
+        st_dev(&hist->cnt[tid], 0u);
+        st_dev(&hist->mass[tid], 0ull);
+        __syncthreads();
+        if (wave_id() == 0) {
+            // band: sub-bins (descending y) whose cumulative mass interval meets
+            // [A - delta, A + delta]; jb = first to reach A - delta, ja = first
+            // to pass A + delta (or the lowest non-empty one)
+            const double delta = 1e-5 * S0;
+            double ab;
+            const int jb = wave_find_desc<double>(sm.u.mg.m, RB_N, A0 - delta - above, &ab);
+            const int ja = wave_find_desc<double>(sm.u.mg.m, RB_N, A0 + delta - above, &ab);
+            uint32_t cnt = 0;
+            for (int j = lane_id(); j < RB_N; j += 64) cnt += (j >= ja && j <= jb) ? sm.u.mg.c[j] : 0u;
+            cnt = wave_sum(cnt);
+            double tot = 0.0;
+            for (int j = lane_id(); j < RB_N; j += 64) tot += sm.u.mg.m[j];
+            tot = wave_sum(tot);
+            if (lane_id() == 0) {
+                // the band must reach the target from above and below
+                const bool ok = above <= A0 + delta && above + tot >= A0 - delta && cnt > 0u && ja <= jb;
+                sm.bi[0] = ok ? ja : -1; sm.bi[1] = jb; sm.bu[7] = cnt;
+            }
+        }
+        __syncthreads();
+        const int ja = sm.bi[0], jb = sm.bi[1];
+        const uint32_t cnt = sm.bu[7];
+        if (ja < 0) {
+            topp_outcome(rc, ro, TP_REREAD, m, 0u, 0, 0.0);
+            return;
+        }
+        if (wave_id() == 0) {
+            const uint32_t k0 = key_search(klo, khi, [&](uint32_t k) { return sub_bin(f32_of_key(k), blo, bsc) >= ja; });
+            const uint32_t k1 = key_search(klo, khi, [&](uint32_t k) { return sub_bin(f32_of_key(k), blo, bsc) > jb; }) - 1u;
+            if (lane_id() == 0) { sm.bu[5] = k0; sm.bu[6] = k1; }
+        }
+        __syncthreads();
+        const uint32_t k0 = sm.bu[5], k1 = sm.bu[6];
+        __syncthreads();
+        if (cnt <= (uint32_t)SURV_CAP) publish_round(rc, r + 1u, R_COLLECT, k0, k1, nref);
+        else if (k0 >= k1 || nref + 1u >= (uint32_t)MAX_REFINE) topp_outcome(rc, ro, TP_REREAD, m, 0u, 0, 0.0);
+        else publish_round(rc, r + 1u, R_REFINE, k0, k1, nref + 1u);
+        return;
+    }
+    // collect or exact round: the window is in the workspace
+    const bool exact = rtype == R_EXACT;
+    double S = S0, A = A0;
+    if (exact) {
+        double s = 0.0;
+        for (int g = tid; g < G; g += NT) s += ld_dev(&rbf[g].S) * sm.chs[g];
+        S = block_sum<double>(s, sm.red);
+        A = (double)pl.top_p * S;
+    }
+    const uint32_t nw = nw0;
+    if (nw > (uint32_t)SURV_CAP) {
+        topp_outcome(rc, ro, TP_REREAD, m, 0u, 0, 0.0);
+        return;
+    }
+    {
+        constexpr int PER = SURV_CAP / NT;  // window loads, issued together
+        Elem el[PER];
+#pragma unroll
+        for (int q = 0; q < PER; ++q) {
+            const uint32_t i = (uint32_t)(q * NT + tid);
+            el[q] = i < nw ? ld_dev_elem(&win[i]) : Elem{0u, 0};
+        }
+#pragma unroll
+        for (int q = 0; q < PER; ++q) {
+            const uint32_t i = (uint32_t)(q * NT + tid);
+            if (i < nw) {
+                sm.u.s.key[i] = el[q].key;
+                sm.u.s.idx[i] = el[q].idx;
+                sm.u.s.e[i] = exp((double)f32_of_key(el[q].key) - md);
+            }
+        }
+    }
+    __syncthreads();
+    uint32_t cut_key = 0u;
+    int32_t cut_i = 0;
+    double ql = 0.0, wl = 0.0;
+    const int rl = window_resolve(sm, nw, above, A, &cut_key, &cut_i, &ql, &wl);
+    const bool inside = rl >= 0;
+    // the decision is proven when both margins exceed the error of the f32
+    // weights summed into `above` and S
+    const double err = exact ? 0.0 : (WEXP_REL_ERR + 1e-12) * (above + A) + 1e-300;
+    const bool robust = inside && (A - ql) > err && (ql + wl - A) > err;
+    if (!exact && !robust) {
+        publish_round(rc, r + 1u, R_EXACT, klo, khi, nref);
+        return;
+    }
+    if (!inside) {
+        topp_outcome(rc, ro, TP_REREAD, m, 0u, 0, 0.0);
+        return;
+    }
+    // per-chunk kept weight: everything above the window, plus the window's
+    // kept prefix (sorted positions 0 .. rl); the row pass draws from them
+    for (int g = tid; g < G; g += NT) sm.cw[g] = ld_dev(&rbf[g].above) * sm.chs[g];
+    __syncthreads();
+    for (int q = tid; q <= rl; q += NT) {
+        const int32_t j = (int32_t)(0xffffffffu - (uint32_t)sm.u.so.k[q]);
+        atomicAdd(&sm.cw[(int)(j / c.CH)], sm.u.so.e[q]);
+    }
+    __syncthreads();
+    double SK = 0.0;
+    for (int g = tid; g < G; g += NT) { SK += sm.cw[g]; rbf[g].kept = sm.cw[g]; }
+    SK = block_sum<double>(SK, sm.red);
+    topp_outcome(rc, ro, TP_CUT, m, cut_key, cut_i, SK);
+}
+
+// ------------------------------------------------------------------ the kernel
+
+// ascending bitonic sort of one value per lane across a wave
+__device__ __forceinline__ uint32_t wave_sort_asc(uint32_t v)
+{
+    const int l = lane_id();
+#pragma unroll
+    for (int k = 2; k <= 64; k <<= 1) {
+#pragma unroll
+        for (int j = k >> 1; j > 0; j >>= 1) {
+            const uint32_t o = (uint32_t)__shfl_xor((int)v, j, 64);
+            const bool up = (l & k) == 0, lower = (l & j) == 0;
+            v = (up == lower) ? (o < v ? o : v) : (o > v ? o : v);
+        }
+    }
+    return v;
+}
+
+// The chunk pass: one workgroup per (row, chunk).  Loads the chunk into
+// registers and reduces it for the row's mode to the summary the row pass
+// reads.  fp32 top-p rows stay for the refinement rounds, led by the last
+// workgroup of the row to arrive in each round.
 template <int DT, int EPT>
-__global__ __launch_bounds__(NT) void k_chunk(Args a)
+__global__ __launch_bounds__(NT, 5) void k_sample(Args a)
 {
     constexpr int VEC = Traits<DT>::VEC, NV = EPT / VEC, CH = NT * EPT;
-    __shared__ ChunkSmem sm;
+    __shared__ Smem sm;
     const Layout &L = a.L;
     const int tid = threadIdx.x;
+    const int G = L.G;
+    Ctl *ctl = reinterpret_cast<Ctl *>(a.ws + L.ctl);
+    // workgroups are dispatched in blockIdx order on every XCD, and a row's
+    // chunks have consecutive indices: a workgroup that waits for row mates
+    // waits only for ones dispatched no later than the row's last chunk
     const uint32_t task = blockIdx.x;
-    const uint32_t G = (uint32_t)L.G;
-    const int row = uni((int32_t)(task / G)), chunk = uni((int32_t)(task % G));
+    const int row = (int)(task / (uint32_t)G), chunk = (int)(task % (uint32_t)G);
     const int64_t V = a.V;
     const int64_t base = (int64_t)chunk * CH;
     const char *rowp = a.logits + (int64_t)row * a.stride_bytes;
     mis_row_params P = a.params[row];
     P.temperature = uni(P.temperature); P.top_k = uni(P.top_k); P.top_p = uni(P.top_p); P.uniform = uni(P.uniform);
     const RowPlan pl = plan_row(P, V);
-    ChunkSum *csr = reinterpret_cast<ChunkSum *>(a.ws + L.chunks) + (size_t)row * L.G;
+    ChunkSum *csr = reinterpret_cast<ChunkSum *>(a.ws + L.chunks) + (size_t)row * G;
     ChunkSum *cs = csr + chunk;
+    RowCtl *rc = reinterpret_cast<RowCtl *>(a.ws + L.rowctl) + row;
+    RowOut *ro = reinterpret_cast<RowOut *>(a.ws + L.rowout) + row;
+    RoundBuf *rbr = reinterpret_cast<RoundBuf *>(a.ws + L.rbuf) + (size_t)row * G;
+    RoundBuf *rb = rbr + chunk;
+    if (tid == 0) {
+        sm.args = a;
+        RowCx &c = sm.cx;
+        c.rowp = rowp; c.V = V; c.vec_ok = a.vec_ok; c.m = 0.0f; c.G = G; c.CH = CH; c.row = row; c.T = pl.T;
+        sm.pl = pl;
+    }
 
-    // ---- one coalesced read of the chunk into registers
+    if (chunk == 0) trace(a.ws, L, row, 0);
+    // ---- one coalesced read of the chunk into registers; -inf past the row
     float x[EPT];
-    if (a.vec_ok && base + CH <= V) {  // whole chunk inside the row: all loads issued back to back
+    if (a.vec_ok && base + CH <= V) {
 #pragma unroll
         for (int v = 0; v < NV; ++v) loadvec<DT>(rowp, base + ((int64_t)v * NT + tid) * VEC, &x[v * VEC]);
     } else {
@@ -1397,255 +1644,357 @@ __global__ __launch_bounds__(NT) void k_chunk(Args a)
                 loadvec<DT>(rowp, j0, &x[v * VEC]);
             } else {
 #pragma unroll
-                for (int e = 0; e < VEC; ++e) x[v * VEC + e] = (j0 + e < V) ? load1<DT>(rowp, j0 + e) : 0.0f;
+                for (int e = 0; e < VEC; ++e) x[v * VEC + e] = (j0 + e < V) ? load1<DT>(rowp, j0 + e) : -INFINITY;
             }
         }
     }
-    // element i of this thread sits at base + lofs(i); `valid` has bit i set
-    // when that index is inside the row
-    auto lofs = [&](int i) -> uint32_t { return (uint32_t)(((i / VEC) * NT + tid) * VEC + (i % VEC)); };
     const int32_t base32 = (int32_t)base;  // V < 2^31
-    auto idx_of = [&](int i) -> int32_t { return base32 + (int32_t)lofs(i); };
-    uint64_t valid = ~0ull;
-    {
-        const int64_t lim = V - base;  // elements of this chunk inside the row
-        if (lim < (int64_t)CH) {
-            valid = 0ull;
-            const uint32_t lim32 = (uint32_t)lim;
-#pragma unroll
-            for (int i = 0; i < EPT; ++i) valid |= (lofs(i) < lim32 ? 1ull : 0ull) << i;
-        }
-    }
-    auto ok_ = [&](int i) -> bool { return (valid >> i) & 1ull; };
+    auto idx_of = [&](int i) -> int32_t { return base32 + (int32_t)((((i / VEC) * NT + tid) * VEC) + (i % VEC)); };
 
-    // ---- argmax of the raw logits (NaN ranks first)
-    uint32_t bk = 0u;
-    int32_t bi = IDX_ALL;
+    const bool topp32 = DT == F32 && pl.mode == M_TOPP;
+    float ymax = -INFINITY;
+    if (pl.mode == M_GREEDY) {
+        // ---- argmax of the raw logits (NaN ranks first, ties -> lowest index)
+        uint32_t bk = 0u;
+        int32_t bi = IDX_ALL;
 #pragma unroll
-    for (int i = 0; i < EPT; ++i) {
-        if (ok_(i)) {
+        for (int i = 0; i < EPT; ++i) {
             const uint32_t k = argmax_key(x[i]);
             if (k > bk) { bk = k; bi = idx_of(i); }
         }
-    }
-    wave_argmax(bk, bi);
-    if (lane_id() == 0) { sm.red.u[wave_id()] = bk; sm.red.l[wave_id()] = bi; }
-    __syncthreads();
-    if (tid == 0) {
-        for (int w = 1; w < NWAVE; ++w) {
-            const uint32_t k2 = sm.red.u[w];
-            const int32_t i2 = (int32_t)sm.red.l[w];
-            if (k2 > bk || (k2 == bk && i2 < bi)) { bk = k2; bi = i2; }
+        wave_argmax(bk, bi);
+        if (lane_id() == 0) { sm.red.u[wave_id()] = bk; sm.red.l[wave_id()] = bi; }
+        __syncthreads();
+        if (tid == 0) {
+            for (int w = 1; w < NWAVE; ++w) {
+                const uint32_t k2 = sm.red.u[w];
+                const int32_t i2 = (int32_t)sm.red.l[w];
+                if (k2 > bk || (k2 == bk && i2 < bi)) { bk = k2; bi = i2; }
+            }
+            cs->xkey = bk; cs->xarg = bi;
         }
-        sm.bu[0] = bk;
-        sm.bi[0] = bi;
-    }
-    __syncthreads();
-    bk = sm.bu[0];
-    bi = sm.bi[0];
-    __syncthreads();
-
-    uint32_t flags = 0u;
-    float xmax = -INFINITY, ymax = -INFINITY;
-    if (pl.mode != M_BAD && pl.mode != M_GREEDY) {
-        if (bk == 0xffffffffu) flags |= FLAG_NAN;
-        else {
-            xmax = f32_of_key(bk);
+    } else if (pl.mode != M_BAD) {
+        // ---- chunk max and flags
+        float tmax = -INFINITY;
+        uint32_t nan = 0u, nf = 0u;
+#pragma unroll
+        for (int i = 0; i < EPT; ++i) {
+            tmax = fmaxf(tmax, x[i]);
+            nan |= x[i] != x[i] ? 1u : 0u;
+            nf += x[i] != -INFINITY ? 1u : 0u;
+        }
+        const float xmax = block_max<float>(tmax, sm.red);
+        const uint32_t anynan = block_sum<uint32_t>(nan, sm.red);
+        const uint32_t nfin = block_sum<uint32_t>(nf, sm.red);
+        uint32_t flags = anynan ? FLAG_NAN : 0u;
+        if (xmax != -INFINITY) {
             ymax = scale_y<DT>(xmax, pl.T);  // scaling is monotone
             if (ymax == INFINITY) flags |= FLAG_PINF;
         }
-    }
-    const bool live = (pl.mode != M_BAD && pl.mode != M_GREEDY && flags == 0u);
-    const bool topp32 = (DT == F32 && pl.mode == M_TOPP);
-
-    // ---- phase 1 per mode
-    uint32_t ncand = 0;
-    double Sc = 0.0, below = 0.0, gmc = 0.0;
-    if (live && pl.mode == M_SMALLK) {
-        uint32_t nfin = 0;
-        float xminf = INFINITY;
+        const bool live = flags == 0u && ymax != -INFINITY;
+        const float T = pl.T, rT = 1.0f / pl.T;
+        double Sc = 0.0;
+        uint32_t ncand = 0u, kc = 0u, trunc = 0u;
+        if (live && pl.mode == M_TEMP) {
+            double s = 0.0;
 #pragma unroll
-        for (int i = 0; i < EPT; ++i)
-            if (ok_(i) && x[i] != -INFINITY) { nfin++; xminf = fminf(xminf, x[i]); }
-        nfin = block_sum<uint32_t>(nfin, sm.red);
-        xminf = block_min<float>(xminf, sm.red);
-        // candidates: finite x >= xlo_c, where xlo_c keeps the chunk's top k'.
-        // Bins are linear in the raw value over [xminf, xmax] (index 255 = top).
-        float xlo_c = -INFINITY;
-        if (nfin > (uint32_t)pl.kk && xmax > xminf) {
-            const float inv = 256.0f / (xmax - xminf);
-            sm.u.h8.cnt[tid] = 0u;
+            for (int i = 0; i < EPT; ++i) s += (double)wexp(scale_r<DT>(x[i], T, rT), ymax);
+            Sc = block_sum<double>(s, sm.red);
+        } else if (live && topp32) {
+            // round 1: weights and lane-private coarse bins on the global grid
+            // floor(y / 2); bins more than CB_N below the chunk's are not kept.
+            // Each lane owns one column of the bins, so plain read-modify-write
+            // suffices (LDS float atomics serialise)
+            const float Ac = coarse_bin(ymax);
+#pragma unroll
+            for (int b = 0; b < CB_N; ++b) sm.u.lp[b][tid] = 0.0f;
+            double s = 0.0;
+#pragma unroll
+            for (int i = 0; i < EPT; ++i) {
+                const float y = scale_r<DT>(opaque(x[i]), T, rT);
+                const float w = wexp(y, ymax);
+                s += (double)w;
+                const float cb = Ac - coarse_bin(y);
+                if (cb < (float)CB_N) { const int cbi = (int)cb; sm.u.lp[cbi][tid] += w; }  // lane-private: no atomic
+            }
+            Sc = block_sum<double>(s, sm.red);  // its barriers also order the bins
+            {
+                const int b = tid >> 4, q = tid & 15;
+                double t = 0.0;
+#pragma unroll
+                for (int l = 0; l < 16; ++l) t += (double)sm.u.lp[b][q * 16 + l];
+#pragma unroll
+                for (int o = 8; o > 0; o >>= 1) t += __shfl_xor(t, o, 64);
+                if (q == 0) st_dev(&rb->coarse[b], t);
+            }
+            if (tid == 0) st_dev(&rb->S, Sc);
+        } else if (live && pl.mode == M_SMALLK) {
+            // ---- candidates: every finite x whose scaled key reaches a threshold
+            // taken from the per-thread maxima, enough for n_c candidates
+            const uint32_t kk = (uint32_t)pl.kk;
+            uint32_t nc = G == 1 ? kk : 2u * ((kk + (uint32_t)G - 1u) / (uint32_t)G) + 32u;
+            if (nc > kk) nc = kk;
+            uint32_t xlo = 0u;  // raw-key floor of the candidates
+            if (nfin > nc) {
+                uint32_t tkey;
+                if (nc <= 256u) {
+                    // each wave's ceil(nc/4)-th largest thread maximum: every
+                    // wave then holds that many elements at or above the least
+                    // of the four, so at least nc in all
+                    const int q = (int)((nc + 3u) / 4u);
+                    const uint32_t srt = wave_sort_asc(key_of_f32(tmax));
+                    const uint32_t tw = (uint32_t)__shfl((int)srt, 64 - q, 64);
+                    tkey = block_min<uint32_t>(tw, sm.red);
+                } else {
+                    // larger nc (few chunks per row): bisect the raw key for
+                    // a threshold with nc <= count <= CAND_CAP
+                    uint32_t lo = 0u, hi = key_of_f32(xmax) + 1u, clo = nfin;
+                    while (clo > (uint32_t)CAND_CAP && hi - lo > 1u) {
+                        const uint32_t mid = lo + (hi - lo) / 2u;
+                        uint32_t c = 0u;
+#pragma unroll
+                        for (int i = 0; i < EPT; ++i) c += (x[i] != -INFINITY && key_of_f32(x[i]) >= mid) ? 1u : 0u;
+                        c = block_sum<uint32_t>(c, sm.red);
+                        if (c >= nc) { lo = mid; clo = c; } else { hi = mid; }
+                    }
+                    tkey = lo;
+                }
+                // close under the ties the scaling creates
+                const uint32_t sk = row_key(scale_y<DT>(f32_of_key(tkey), T), DT);
+                kc = sk;
+                if (wave_id() == 0) {
+                    const uint32_t xl = x_lower<DT>(sk, T);
+                    if (lane_id() == 0) sm.bu[3] = xl;
+                }
+                __syncthreads();
+                xlo = sm.bu[3];
+                __syncthreads();
+            }
+            uint32_t mine = 0u;
+#pragma unroll
+            for (int i = 0; i < EPT; ++i) mine += (x[i] != -INFINITY && key_of_f32(x[i]) >= xlo) ? 1u : 0u;
+            uint32_t total;
+            uint32_t off = block_excl_scan<uint32_t>(mine, sm.red, &total);
+            if (total <= (uint32_t)CAND_CAP) {
+                Cand *cand = reinterpret_cast<Cand *>(a.ws + L.cand) + ((size_t)row * G + chunk) * CAND_CAP;
+#pragma unroll
+                for (int i = 0; i < EPT; ++i)
+                    if (x[i] != -INFINITY && key_of_f32(x[i]) >= xlo) {
+                        cand[off].x = x[i];
+                        cand[off].idx = idx_of(i);
+                        ++off;
+                    }
+                ncand = total;
+            } else {
+                ncand = NCAND_OVERFLOW;
+            }
+            trunc = total < nfin ? 1u : 0u;
+        }
+        if (tid == 0) {
+            const bool co = topp32;
+            st_sum(co, &cs->xkey, 0u); st_sum(co, &cs->xarg, IDX_ALL);
+            st_sum(co, &cs->ymax, ymax); st_sum(co, &cs->flags, flags); st_sum(co, &cs->S, Sc);
+            st_sum(co, &cs->ncand, ncand); st_sum(co, &cs->nfin, nfin); st_sum(co, &cs->kc, kc); st_sum(co, &cs->trunc, trunc);
+        }
+    }
+    if (topp32) publish_barrier();
+    if (chunk == 0) trace(a.ws, L, row, 1);
+
+    if (!topp32) return;  // the row pass finishes the row from the summaries
+
+    // ---- fp32 top-p: refinement rounds with the chunk held in registers
+    const Elem *winr = reinterpret_cast<const Elem *>(a.ws + L.win) + (size_t)row * WCAP;
+    RowHist *hist = reinterpret_cast<RowHist *>(a.ws + L.hist) + row;
+    Elem *winw = reinterpret_cast<Elem *>(a.ws + L.win) + (size_t)row * WCAP;
+    const float T = pl.T, rT = 1.0f / pl.T;
+    uint32_t r = 1;
+    bool timed_out = false;
+    for (;;) {
+        if (tid == 0) sm.bu[6] = arrive(rc) + 1u == r * (uint32_t)G ? 1u : 0u;
+        __syncthreads();
+        const bool lead = sm.bu[6] != 0u;
+        __syncthreads();
+        if (lead) {
+            trace(a.ws, L, row, 2 * (int)r);
+            leader_topp<DT>(sm, sm.cx, sm.pl, csr, rbr, rc, hist, winr, ro, r);
+            trace(a.ws, L, row, 2 * (int)r + 1);
+        }
+        if (tid == 0) {
+            const bool ok = wait_round(rc, r, &ctl->error);
+            const uint32_t rd = ld_dev(&rc->round);
+            uint32_t st = 0u;
+            if (!ok) st = 2u;
+            else if (rd == ROUND_DONE) st = 1u;
+            sm.bu[5] = st;
+            if (st == 0u) {  // the round's parameters, loaded together
+                const uint32_t rt = ld_dev(&rc->rtype), k0 = ld_dev(&rc->klo), k1 = ld_dev(&rc->khi);
+                const float lo = ld_dev(&rc->lo), sc = ld_dev(&rc->sc), mr = ld_dev(&rc->m);
+                sm.bu[0] = rt; sm.bu[1] = k0; sm.bu[2] = k1;
+                sm.bf[0] = lo; sm.bf[1] = sc; sm.bf[2] = mr;
+            }
+        }
+        __syncthreads();
+        const uint32_t st = sm.bu[5];
+        if (st != 0u) { timed_out = st == 2u; break; }
+        const uint32_t rtype = uni(sm.bu[0]), klo = uni(sm.bu[1]), khi = uni(sm.bu[2]);
+        const float lo = uni(sm.bf[0]), scb = uni(sm.bf[1]), mrow = uni(sm.bf[2]);
+        __syncthreads();
+        ++r;
+        double above = 0.0;
+        if (rtype == R_REFINE) {
+            sm.u.rf.cnt[tid] = 0u;
+            sm.u.rf.mass[tid] = 0ull;
             __syncthreads();
 #pragma unroll
             for (int i = 0; i < EPT; ++i) {
-                if (ok_(i) && x[i] != -INFINITY) {
-                    const int b = min(255, (int)((xmax - opaque(x[i])) * inv));
-                    atomicAdd(&sm.u.h8.cnt[255 - b], 1u);
+                const float y = scale_r<DT>(opaque(x[i]), T, rT);
+                const uint32_t k = row_key(y, DT);
+                if (k > khi) above += (double)wexp(y, ymax);
+                else if (k >= klo) {
+                    const int j = sub_bin(y, lo, scb);
+                    // integer LDS atomics: float ones run far slower
+                    atomicAdd(&sm.u.rf.cnt[j], 1u);
+                    atomicAdd(&sm.u.rf.mass[j], (unsigned long long)__float2uint_rn(wexp(y, ymax) * 4294967296.0f));
                 }
             }
-            __syncthreads();
-            if (wave_id() == 0) {
-                uint32_t above;
-                const int d = wave_find_desc<uint32_t>(sm.u.h8.cnt, 256, (uint32_t)pl.kk, &above);
-                if (lane_id() == 0) { sm.bu[0] = (uint32_t)(255 - d); sm.bu[1] = above; sm.bu[2] = sm.u.h8.cnt[d]; }
+            above = block_sum<double>(above, sm.red);  // its barriers also order the bins
+            {
+                // into the row histogram, relative to the row max (2^-40 units)
+                const uint32_t cn = sm.u.rf.cnt[tid];
+                if (cn) {
+                    const double f = exp((double)ymax - (double)mrow) * (HIST_SCALE / 4294967296.0);
+                    __hip_atomic_fetch_add(&hist->cnt[tid], cn, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    __hip_atomic_fetch_add(&hist->mass[tid], (unsigned long long)((double)sm.u.rf.mass[tid] * f),
+                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
             }
+            if (tid == 0) st_dev(&rb->above, above);
+        } else if (rtype == R_COLLECT) {
+            uint32_t mine = 0u;
+#pragma unroll
+            for (int i = 0; i < EPT; ++i) {
+                const float y = scale_r<DT>(opaque(x[i]), T, rT);
+                const uint32_t k = row_key(y, DT);
+                if (k > khi) above += (double)wexp(y, ymax);
+                else if (k >= klo) mine++;
+            }
+            uint32_t total;
+            uint32_t off = block_excl_scan<uint32_t>(mine, sm.red, &total);
+            if (tid == 0) sm.bu[4] = total ? __hip_atomic_fetch_add(&rc->wcount, total, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0u;
             __syncthreads();
-            const int bstar = (int)sm.bu[0];
-            const uint32_t above_b = sm.bu[1], in_b = sm.bu[2];
-            __syncthreads();
-            int sstar = 255;
-            if (above_b + in_b > (uint32_t)CAND_CAP) {
-                // refine the boundary bin into 256 sub-bins
-                sm.u.h8.cnt[tid] = 0u;
-                __syncthreads();
+            const uint32_t wbase = sm.bu[4];
+            if (mine) {
 #pragma unroll
                 for (int i = 0; i < EPT; ++i) {
-                    if (ok_(i) && x[i] != -INFINITY) {
-                        const float t = (xmax - opaque(x[i])) * inv;
-                        const int b = min(255, (int)t);
-                        if (b == bstar) atomicAdd(&sm.u.h8.cnt[255 - min(255, (int)((t - (float)b) * 256.0f))], 1u);
-                    }
-                }
-                __syncthreads();
-                if (wave_id() == 0) {
-                    uint32_t above;
-                    const int d = wave_find_desc<uint32_t>(sm.u.h8.cnt, 256, (uint32_t)pl.kk - above_b, &above);
-                    if (lane_id() == 0) sm.bu[0] = (uint32_t)(255 - d);
-                }
-                __syncthreads();
-                sstar = (int)sm.bu[0];
-                __syncthreads();
-            }
-            // smallest raw value inside the selected bins
-            float xb = INFINITY;
-#pragma unroll
-            for (int i = 0; i < EPT; ++i) {
-                if (ok_(i) && x[i] != -INFINITY) {
-                    const float t = (xmax - opaque(x[i])) * inv;
-                    const int b = min(255, (int)t);
-                    if (b < bstar || (b == bstar && min(255, (int)((t - (float)b) * 256.0f)) <= sstar))
-                        xb = fminf(xb, opaque(x[i]));
-                }
-            }
-            xb = block_min<float>(xb, sm.red);
-            // close the set under the ties the scaling creates: every x whose
-            // scaled key equals that of xb is a candidate too
-            uint32_t xlo, xhi;
-            const uint32_t kb = row_key(scale_y<DT>(xb, pl.T), DT);
-            x_interval<DT>(sm, kb, kb, pl.T, &xlo, &xhi);
-            xlo_c = f32_of_key(xlo);
-        }
-        uint32_t mine = 0;
-#pragma unroll
-        for (int i = 0; i < EPT; ++i)
-            if (ok_(i) && x[i] != -INFINITY && x[i] >= xlo_c) mine++;
-        uint32_t total;
-        uint32_t off = block_excl_scan<uint32_t>(mine, sm.red, &total);
-        if (total <= (uint32_t)CAND_CAP) {
-            Cand *cand = reinterpret_cast<Cand *>(a.ws + L.cand) + ((size_t)row * L.G + chunk) * CAND_CAP;
-#pragma unroll
-            for (int i = 0; i < EPT; ++i) {
-                if (ok_(i) && x[i] != -INFINITY && x[i] >= xlo_c) {
-                    st_dev_cand(&cand[off++], x[i], idx_of(i));
-                }
-            }
-            ncand = total;
-        } else {
-            ncand = NCAND_OVERFLOW;
-        }
-    } else if (live && pl.mode == M_TEMP) {
-        // draw weights exp(y - ymax_c) in f32 on the scaled values y =
-        // dtype(x / T) (within the draw's tolerance), float64 sums.  Weights
-        // taken on x / T before its rounding would be off by |y| ulps.
-        double s = 0.0;
-        if (ymax != -INFINITY) {
-            constexpr float L2E = 1.44269504088896341f;
-#pragma unroll
-            for (int i = 0; i < EPT; ++i)
-                if (ok_(i)) s += (double)exp2f((scale_y<DT>(x[i], pl.T) - ymax) * L2E);
-        }
-        Sc = block_sum<double>(s, sm.red);
-    } else if (live && topp32) {
-        // exact y, float64 weights relative to the chunk max, fine bins on the
-        // global grid floor(y * FB_W)
-        for (int i = tid; i < FB_N; i += NT) { sm.u.p1.cnt[i] = 0u; sm.u.p1.mass[i] = 0.0; }
-        __syncthreads();
-        const double ym = (double)ymax;
-        gmc = ymax == -INFINITY ? 0.0 : floor(ym * (double)FB_W);
-        double s = 0.0, bl = 0.0;
-        if (ymax != -INFINITY) {
-#pragma unroll
-            for (int i = 0; i < EPT; ++i) {
-                if (ok_(i)) {
-                    const float y = scale_y<DT>(x[i], pl.T);
-                    if (y != -INFINITY) {
-                        const double e = exp((double)y - ym);
-                        s += e;
-                        const double rb = gmc - floor((double)y * (double)FB_W);
-                        if (rb < (double)FB_N) {
-                            const int b = (int)rb;
-                            atomicAdd(&sm.u.p1.cnt[b], 1u);
-                            atomicAdd(&sm.u.p1.mass[b], e);
-                        } else {
-                            bl += e;
-                        }
+                    const float y = scale_r<DT>(opaque(x[i]), T, rT);
+                    const uint32_t k = row_key(y, DT);
+                    if (k <= khi && k >= klo) {
+                        const uint32_t pos = wbase + off++;
+                        if (pos < (uint32_t)WCAP) st_dev_elem(&winw[pos], k, idx_of(i));
                     }
                 }
             }
-        }
-        Sc = block_sum<double>(s, sm.red);
-        below = block_sum<double>(bl, sm.red);
-        uint32_t *gc = reinterpret_cast<uint32_t *>(a.ws + L.fbc) + ((size_t)row * L.G + chunk) * FB_N;
-        double *gm = reinterpret_cast<double *>(a.ws + L.fbm) + ((size_t)row * L.G + chunk) * FB_N;
-        for (int i = tid; i < FB_N; i += NT) { st_dev(&gc[i], sm.u.p1.cnt[i]); st_dev(&gm[i], sm.u.p1.mass[i]); }
-    } else if (live) {
-        // large k' and fp16/bf16 top-p: the leader re-reads the row
-        double s = 0.0;
-        if (ymax != -INFINITY) {
-            const double ym = (double)ymax;
-#pragma unroll
-            for (int i = 0; i < EPT; ++i) {
-                if (ok_(i)) {
-                    const float y = scale_y<DT>(x[i], pl.T);
-                    if (y != -INFINITY) s += exp((double)y - ym);
-                }
+            above = block_sum<double>(above, sm.red);
+            if (tid == 0) st_dev(&rb->above, above);
+        } else {  // R_EXACT: float64 weights, rare: the chunk is re-read in a rolled loop
+            double s = 0.0;
+            const double ymd = (double)ymax;
+            const int64_t cend = base + CH < V ? base + CH : V;
+            for (int64_t j = base + tid; j < cend; j += NT) {
+                const float y = scale_y<DT>(load1<DT>(rowp, j), T);
+                const double e = y == -INFINITY ? 0.0 : exp((double)y - ymd);
+                s += e;
+                if (row_key(y, DT) > khi) above += e;
             }
+            s = block_sum<double>(s, sm.red);
+            above = block_sum<double>(above, sm.red);
+            if (tid == 0) { st_dev(&rb->S, s); st_dev(&rb->above, above); }
         }
-        Sc = block_sum<double>(s, sm.red);
+        publish_barrier();
     }
     if (tid == 0) {
-        st_dev(&cs->xkey, bk); st_dev(&cs->xarg, bi); st_dev(&cs->ymax, ymax); st_dev(&cs->flags, flags);
-        st_dev(&cs->ncand, ncand); st_dev(&cs->xmax, xmax); st_dev(&cs->S, Sc); st_dev(&cs->gmc, gmc);
-        st_dev(&cs->below, below);
+        if (timed_out) {
+            a.out_ids[row] = -1;
+            if (a.out_status) a.out_status[row] = MIS_ROW_INTERNAL;
+        }
+        // the last workgroup to leave clears the row's control words
+        const uint32_t ex = __hip_atomic_fetch_add(&rc->exited, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (ex + 1u == (uint32_t)G) {
+            trace(a.ws, L, row, 14);
+            st_dev(&rc->arr, 0u); st_dev(&rc->round, 0u); st_dev(&rc->wcount, 0u);
+            st_dev(&rc->rtype, 0u); st_dev(&rc->nref, 0u); st_dev(&rc->exited, 0u);
+        }
     }
 }
 
 // ------------------------------------------------------------------ the row pass
 
-// One workgroup per row: merges the row's chunk summaries and finishes the
-// row (the functions above), re-reading parts of the row where needed.
+// fp32 top-p row after its rounds: draw from the per-chunk kept weights, or
+// re-read the row when the rounds handed it over.
+template <int DT>
+__device__ __noinline__ void finish_topp(Smem &sm, RowCx &c, const RowPlan &pl, const RoundBuf *rbf, RowOut *ro,
+                                         const Args &a, int32_t outcome)
+{
+    const float m = ro->m;
+    c.m = m;
+    const double md = (double)m;
+    if (outcome == TP_INVALID) {
+        write_row(ro, a, c.row, -1, MIS_ROW_INVALID, pl.mode, m, 0u, 0, 0.0);
+    } else if (outcome == TP_REREAD) {
+        final_generic<DT>(sm, c, pl, ro, a);
+    } else if (outcome == TP_CUT) {
+        const uint32_t cut_key = ro->cut_key;
+        const int32_t cut_i = ro->cut_i;
+        for (int g = threadIdx.x; g < c.G; g += NT) sm.cw[g] = rbf[g].kept;
+        int gsel;
+        double resid, SK;
+        pick_chunk(sm, c.G, pl.u, &gsel, &resid, &SK);
+        int64_t id = -1;
+        if (gsel >= 0) {
+            const float T = pl.T;
+            id = draw_in_chunk<DT>(sm, c, gsel, resid, [&](float xv, int64_t j) -> double {
+                const float y = scale_y<DT>(xv, T);
+                return (y != -INFINITY && kept_by_cut(row_key(y, DT), j, cut_key, cut_i)) ? exp((double)y - md) : 0.0;
+            });
+        }
+        write_row(ro, a, c.row, id, id >= 0 ? MIS_ROW_OK : MIS_ROW_INVALID, pl.mode, m, cut_key, cut_i, SK);
+    } else {  // the rounds did not finish (a bounded wait expired)
+        write_row(ro, a, c.row, -1, MIS_ROW_INTERNAL, pl.mode, m, 0u, 0, 0.0);
+    }
+}
+
+// One workgroup per row: merges the chunk summaries and finishes the row
+// (greedy, temperature, small top-k), draws for fp32 top-p rows whose cut the
+// rounds resolved, and re-reads the row for everything else.
 template <int DT>
 __global__ __launch_bounds__(NT) void k_final(Args a)
 {
     __shared__ Smem sm;
     const Layout &L = a.L;
     const int row = blockIdx.x;
+    RowOut *ro = reinterpret_cast<RowOut *>(a.ws + L.rowout) + row;
     if (threadIdx.x == 0) {
         sm.args = a;
         RowCx &c = sm.cx;
         c.rowp = a.logits + (int64_t)row * a.stride_bytes;
         c.V = a.V; c.vec_ok = a.vec_ok; c.m = 0.0f; c.G = L.G; c.CH = (int64_t)NT * L.ept; c.row = row;
-        c.fbc = reinterpret_cast<const uint32_t *>(a.ws + L.fbc) + (size_t)row * L.G * FB_N;
-        c.fbm = reinterpret_cast<const double *>(a.ws + L.fbm) + (size_t)row * L.G * FB_N;
-        c.subc = nullptr; c.subm = nullptr;
         sm.pl = plan_row(a.params[row], a.V);
         c.T = sm.pl.T;
+        sm.bi[6] = ro->topp;
     }
     __syncthreads();
+    const int32_t outcome = sm.bi[6];
+    trace(a.ws, L, row, 16);
+    __syncthreads();
     const ChunkSum *csr = reinterpret_cast<const ChunkSum *>(a.ws + L.chunks) + (size_t)row * L.G;
-    RowOut *ro = reinterpret_cast<RowOut *>(a.ws + L.rowout) + row;
-    if (DT == F32 && sm.pl.mode == M_TOPP) final_topp32<DT>(sm, sm.cx, sm.pl, csr, ro, sm.args);
-    else final_row<DT>(sm, sm.cx, sm.pl, csr, ro, sm.args);
+    const RoundBuf *rbf = reinterpret_cast<const RoundBuf *>(a.ws + L.rbuf) + (size_t)row * L.G;
+    if (DT == F32 && sm.pl.mode == M_TOPP) {
+        finish_topp<DT>(sm, sm.cx, sm.pl, rbf, ro, sm.args, outcome);
+        if (threadIdx.x == 0) ro->topp = TP_NONE;
+    } else {
+        leader_row<DT>(sm, sm.cx, sm.pl, csr, ro, sm.args);
+    }
+    trace(a.ws, L, row, 31);
 }
 
 // ------------------------------------------------------------------ debug emit
@@ -1693,25 +2042,24 @@ __global__ __launch_bounds__(NT) void k_emit(const char *__restrict__ logits, in
 static thread_local int g_last_hip = 0;
 
 template <int DT, int EPT>
-static hipError_t launch_chunk(const Args &a, hipStream_t st)
+static hipError_t launch_sample(const Args &a, hipStream_t st)
 {
     const unsigned grid = (unsigned)(a.L.B * a.L.G);
-    hipLaunchKernelGGL((k_chunk<DT, EPT>), dim3(grid), dim3(NT), 0, st, a);
+    hipLaunchKernelGGL((k_sample<DT, EPT>), dim3(grid), dim3(NT), 0, st, a);
     return hipGetLastError();
 }
 
 // events (optional): [0] before the chunk pass, [1] between the chunk pass
-// and the row pass, [2] after the row pass
+// and the row pass, [2] after the row pass (before the debug emit)
 template <int DT>
 static hipError_t launch_dt(const Args &a, float *probs, uint32_t *keep, hipStream_t st, void *const *ev)
 {
     hipError_t e;
     if (ev && (e = hipEventRecord((hipEvent_t)ev[0], st)) != hipSuccess) return e;
     switch (a.L.ept) {
-    case 64: e = launch_chunk<DT, 64>(a, st); break;
-    case 32: e = launch_chunk<DT, 32>(a, st); break;
-    case 16: e = launch_chunk<DT, 16>(a, st); break;
-    default: e = launch_chunk<DT, 8>(a, st); break;
+    case 64: e = launch_sample<DT, 64>(a, st); break;
+    case 32: e = launch_sample<DT, 32>(a, st); break;
+    default: e = launch_sample<DT, 16>(a, st); break;
     }
     if (e != hipSuccess) return e;
     if (ev && (e = hipEventRecord((hipEvent_t)ev[1], st)) != hipSuccess) return e;
@@ -1722,9 +2070,9 @@ static hipError_t launch_dt(const Args &a, float *probs, uint32_t *keep, hipStre
         const unsigned gx = (unsigned)((a.V + (int64_t)NT * 8 - 1) / ((int64_t)NT * 8));
         hipLaunchKernelGGL((k_emit<DT>), dim3(gx, (unsigned)a.L.B), dim3(NT), 0, st, a.logits, a.V, a.stride_bytes,
                            a.params, a.L, (const char *)a.ws, probs, keep);
-        e = hipGetLastError();
+        if ((e = hipGetLastError()) != hipSuccess) return e;
     }
-    return e;
+    return hipSuccess;
 }
 
 }  // namespace mis
