@@ -55,7 +55,25 @@ def parse():
     ap.add_argument("--rotate-gib", type=float, default=1.0, help="distinct input bytes cycled through")
     ap.add_argument("--cpu-rows", type=int, default=32, help="rows in the CPU-baseline sample (0 = skip)")
     ap.add_argument("--cpu-steps", type=int, default=5)
+    ap.add_argument("--copy-calib-mib", type=int, default=0,
+                    help="after the timed steps, run 5 plain device copies of this many MiB (calibrates "
+                         "rocprofv3 FETCH_SIZE / WRITE_SIZE against known bytes)")
     return ap.parse_args()
+
+
+def traffic_from_profile(config: str):
+    """HBM bytes per chunk-pass launch measured by rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE,
+    each scaled by the same counter's reading for a copy of known size), from the committed
+    summary profiles/k_sample_<config>_traffic.md; None when there is none."""
+    path = os.path.join(ROOT, "profiles", f"k_sample_{config}_traffic.md")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(float(line.split(":", 1)[1]))
+    except OSError:
+        pass
+    return None
 
 
 def cpu_baseline(w, nrows: int, steps: int) -> dict:
@@ -151,7 +169,7 @@ def main():
     k1_mean, k2_mean = statistics.mean(k1_us), statistics.mean(k2_us)
     bytes_k1 = B * V * esz + 16 * B  # logits + params: the chunk pass's HBM read
     if k1_mean >= k2_mean:
-        dom, dom_us, dom_bytes = "k_chunk", k1_mean, bytes_k1
+        dom, dom_us, dom_bytes = "k_sample", k1_mean, bytes_k1
     else:
         dom, dom_us, dom_bytes = "k_final", k2_mean, bytes_alg - bytes_k1
     q = statistics.quantiles(step_us, n=10)
@@ -177,11 +195,20 @@ def main():
         "hbm_gbs_step": round(gbs_step, 1),
         "hbm_frac_step": round(gbs_step / HBM_PEAK_GBS, 4),
         "algorithmic_bytes_per_step": bytes_alg,
-        "kernels_us": {"k_chunk": round(k1_mean, 2), "k_final": round(k2_mean, 2)},
+        "kernels_us": {"k_sample": round(k1_mean, 2), "k_final": round(k2_mean, 2)},
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": traffic_from_profile(args.config) if dom == "k_sample" else None,
                      "algorithmic_bytes_per_launch": dom_bytes, "mean_launch_us": round(dom_us, 2)},
     }
+    if args.copy_calib_mib > 0:
+        n = args.copy_calib_mib << 20
+        src = torch.empty(n, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     if args.cpu_rows > 0:
         res["cpu_baseline"] = cpu_baseline(w, args.cpu_rows, args.cpu_steps)
     else:

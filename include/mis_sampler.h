@@ -55,7 +55,7 @@ enum {
                                   full-row radix descent (1024 < k' < V, or more than 2048
                                   candidates tied at one chunk's k'-th value): not served
                                   by this build */
-    MIS_ROW_INTERNAL = 4       /* a bounded cross-workgroup wait expired (not expected) */
+    MIS_ROW_INTERNAL = 4       /* reserved: not produced by this build */
 };
 
 /*
@@ -79,14 +79,12 @@ typedef struct mis_row_params {
 size_t mis_workspace_bytes(int64_t B, int64_t V, int dtype);
 
 /*
- * Prepares a freshly allocated workspace: clears the control words at its
- * start (hipMemsetAsync on `stream`; not for use under graph capture).  Call
- * once per workspace before its first mis_sample(); every completed
- * mis_sample() leaves those words cleared again, for a call of any shape.
- * A workspace whose first bytes were zeroed by other means is equally ready.
- * After a call that failed on the device, initialise the workspace again.
- * No counterpart in the reference (its sampler keeps no device state; this
- * library's single-launch design keeps per-row arrival counters there).
+ * Prepares a freshly allocated workspace: clears its first 256 bytes
+ * (hipMemsetAsync on `stream`; not for use under graph capture).  The
+ * kernels of this build keep no state in the workspace between calls (every
+ * call writes what it later reads), so the call is optional; it stays in
+ * the ABI so that a later build may keep control words there again.
+ * No counterpart in the reference (its sampler keeps no device state).
  */
 int mis_workspace_init(void *workspace, size_t workspace_bytes, void *stream);
 
@@ -101,8 +99,7 @@ int mis_workspace_init(void *workspace, size_t workspace_bytes, void *stream);
  *   out_keep      device [B, ceil(V/32)] uint32 keep bitmask, bit j%32 of word
  *                 j/32 = token j survives every filter (nullable; debug)
  *   workspace     device scratch of at least mis_workspace_bytes(B, V, dtype)
- *                 bytes, 256-byte aligned, prepared once by mis_workspace_init();
- *                 not shared by concurrent calls
+ *                 bytes, 256-byte aligned; not shared by concurrent calls
  *   stream        hipStream_t the kernels are launched on
  * Returns MIS_OK or an error code; launches are asynchronous.
  */

@@ -13,6 +13,12 @@ void shim_rn_dtype_array(const float *x, float *y, int64_t n, int dt)
 {
     for (int64_t i = 0; i < n; ++i) y[i] = mis::rn_dtype(x[i], dt);
 }
+void shim_dexp_array(const double *d, double *out, int64_t n)
+{
+    double tab[mis::ETAB_N];
+    for (int t = 0; t < mis::ETAB_N; ++t) mis::exp_table(tab, t);
+    for (int64_t i = 0; i < n; ++i) out[i] = mis::dexp(d[i], tab);
+}
 // naive reference for chain_add_n: one float addition per step
 float shim_chain_naive(float F, float p, uint64_t n)
 {

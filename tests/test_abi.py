@@ -74,7 +74,8 @@ def test_argument_validation_without_gpu(lib):
     assert call(fake, 0, 4, 1000, 1000, fake, fake, None, None, None, fake, 16, None) == 2
     assert call(fake, 0, 4, 1000, 1000, fake, fake, None, None, None, vp(0x1008), 1 << 30, None) == 2
     # unsupported sizes
-    assert call(fake, 0, 70000, 10, 10, fake, fake, None, None, None, fake, 1 << 40, None) == 4
+    assert call(fake, 0, 1 << 31, 10, 10, fake, fake, None, None, None, fake, 1 << 60, None) == 4
+    assert call(fake, 0, 1, (1 << 30) + 1, (1 << 30) + 1, fake, fake, None, None, None, fake, 1 << 60, None) == 4
     # profiled entry needs three events
     ev = (vp * 3)(None, None, None)
     assert lib.mis_sample_profiled(fake, 0, 1, 10, 10, fake, fake, None, None, None, fake, 1 << 20, None, ev) == 1

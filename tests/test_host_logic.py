@@ -32,6 +32,7 @@ def shim(tmp_path_factory):
     L.shim_value_of_row_key.argtypes = [ctypes.c_uint32, i]; L.shim_value_of_row_key.restype = f
     L.shim_argmax_key.argtypes = [f]; L.shim_argmax_key.restype = ctypes.c_uint32
     L.shim_rn_dtype_array.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, i]
+    L.shim_dexp_array.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64]
     return L
 
 
@@ -123,3 +124,25 @@ def test_argmax_key_nan_first(shim):
     assert shim.shim_argmax_key(float("nan")) == 0xFFFFFFFF
     assert shim.shim_argmax_key(float("inf")) < 0xFFFFFFFF
     assert shim.shim_argmax_key(1.0) > shim.shim_argmax_key(-1.0)
+
+
+def test_dexp_relative_error(shim):
+    """The float64 exp of the fp32 top-p masses against x87 extended
+    precision (64-bit significand): relative error below DEXP_REL_ERR = 1e-15
+    wherever the result is normal, exact at 0, zero at -inf."""
+    rng = np.random.default_rng(7)
+    d = np.concatenate([
+        -rng.exponential(3.0, 200000), -rng.uniform(0, 708, 200000), -rng.uniform(0, 1e-3, 20000),
+        -np.arange(0, 700, 0.0078125),  # table boundaries j/64 and binade edges
+        np.array([0.0, -0.0, -1e-300, -708.0, -744.9, -745.0, -800.0, -np.inf]),
+    ]).astype(np.float64)
+    out = np.empty_like(d)
+    shim.shim_dexp_array(d.ctypes.data, out.ctypes.data, d.size)
+    ref = np.exp(d.astype(np.longdouble))
+    normal = ref >= np.longdouble(2.2250738585072014e-308)
+    rel = np.abs((out[normal].astype(np.longdouble) - ref[normal]) / ref[normal])
+    assert float(rel.max()) < 1e-15, float(rel.max())
+    sub = ~normal & (d > -745.0)
+    assert np.all(np.abs(out[sub].astype(np.longdouble) - ref[sub]) <= np.longdouble(2.0 ** -1074))
+    assert np.all(out[d == 0.0] == 1.0)
+    assert np.all(out[d <= -745.0] == 0.0)

@@ -5,6 +5,7 @@
 // exercise the exact code the kernels run.
 #pragma once
 
+#include <math.h>
 #include <stdint.h>
 #include <string.h>
 
@@ -207,6 +208,35 @@ MIS_HD float chain_E(float F, float p, int dt)
     float C = rn_dtype(F, dt);
     float d = C - p;
     return rn_dtype(d, dt);
+}
+
+// ---------------------------------------------------------------- float64 exp
+// e^d for d <= 0 in float64, relative error below DEXP_REL_ERR while the
+// result is normal (subnormal results: absolute error below 2^-1074).
+// Tang's table method: d * 64/ln2 rounds to n = 64q + j (0 <= j < 64),
+// r = d - n * ln2/64 (|r| <= ln2/128) in two FMA steps with ln2/64 split
+// into a head and a tail, e^r by its degree-5 Taylor polynomial (truncation
+// below 4e-17), then e^d = 2^q * 2^(j/64) * e^r with 2^(j/64) from a table
+// that exp_table() fills.
+constexpr double DEXP_REL_ERR = 1e-15;
+constexpr int ETAB_N = 64;
+MIS_HD void exp_table(double *tab, int tid)
+{
+    if (tid < ETAB_N) tab[tid] = exp2((double)tid * (1.0 / ETAB_N));
+}
+MIS_HD double dexp(double d, const double *tab)
+{
+    if (!(d > -745.0)) return 0.0;
+    const double n = rint(d * 92.33248261689366);  // 64 / ln2
+    double r = fma(n, -0x1.62e42fefa39efp-7, d);   // ln2/64, head
+    r = fma(n, -0x1.abc9e3b39803fp-62, r);         // ln2/64, tail
+    const int ni = (int)n;
+    double p = fma(r, 1.0 / 120.0, 1.0 / 24.0);
+    p = fma(r, p, 1.0 / 6.0);
+    p = fma(r, p, 0.5);
+    p = fma(r, p, 1.0);
+    p = fma(r, p, 1.0);
+    return ldexp(tab[ni & (ETAB_N - 1)] * p, ni >> 6);
 }
 
 }  // namespace mis

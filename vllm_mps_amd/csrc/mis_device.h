@@ -168,7 +168,7 @@ template <> __device__ __forceinline__ int64_t *red_of<int64_t>(Red &r) { return
 template <> __device__ __forceinline__ uint32_t *red_of<uint32_t>(Red &r) { return r.u; }
 template <> __device__ __forceinline__ float *red_of<float>(Red &r) { return r.f; }
 
-template <class T> __device__ T block_excl_scan(T v, Red &rr, T *total)
+template <class T> __device__ __forceinline__ T block_excl_scan(T v, Red &rr, T *total)
 {
     T *red = red_of<T>(rr);
     const T inc = wave_incl_scan(v);
@@ -185,7 +185,7 @@ template <class T> __device__ T block_excl_scan(T v, Red &rr, T *total)
     __syncthreads();
     return res;
 }
-template <class T> __device__ T block_sum(T v, Red &rr)
+template <class T> __device__ __forceinline__ T block_sum(T v, Red &rr)
 {
     T *red = red_of<T>(rr);
     v = wave_sum(v);
@@ -196,7 +196,7 @@ template <class T> __device__ T block_sum(T v, Red &rr)
     __syncthreads();
     return t;
 }
-template <class T> __device__ T block_max(T v, Red &rr)
+template <class T> __device__ __forceinline__ T block_max(T v, Red &rr)
 {
     T *red = red_of<T>(rr);
     v = wave_max(v);
@@ -207,7 +207,7 @@ template <class T> __device__ T block_max(T v, Red &rr)
     __syncthreads();
     return t;
 }
-template <class T> __device__ T block_min(T v, Red &rr)
+template <class T> __device__ __forceinline__ T block_min(T v, Red &rr)
 {
     T *red = red_of<T>(rr);
     v = wave_min(v);
@@ -225,7 +225,7 @@ template <class T> __device__ T block_min(T v, Red &rr)
 // If the target is never reached (rounding) it returns the lowest non-empty
 // bin.  nbins must be a multiple of 64.
 template <class T>
-__device__ int wave_find_desc(const T *h, int nbins, T target, T *above)
+__device__ __forceinline__ int wave_find_desc(const T *h, int nbins, T target, T *above)
 {
     const int l = lane_id();
     const int per = nbins / 64;
@@ -272,7 +272,7 @@ __device__ int wave_find_desc(const T *h, int nbins, T target, T *above)
 // zero value never qualify); *before = sum of the values before i.  When
 // rounding leaves the target out of reach, the last index with a nonzero
 // value.  Returns -1 when every value is zero.
-__device__ int wave_find_asc(const double *v, int n, double target, double *before)
+__device__ __forceinline__ int wave_find_asc(const double *v, int n, double target, double *before)
 {
     const int l = lane_id();
     const int per = (n + 63) / 64;
@@ -320,7 +320,7 @@ __device__ int wave_find_asc(const double *v, int n, double target, double *befo
 // Bitonic sort, descending, of n <= cap (u64 key, f64 value) pairs in LDS by
 // all threads of the block; entries n .. pow2(n)-1 are padded with key 0, so
 // the arrays must hold pow2(n) entries.
-__device__ void block_sort_desc(uint64_t *k, double *e, int n)
+__device__ __forceinline__ void block_sort_desc(uint64_t *k, double *e, int n)
 {
     int npow = 1;
     while (npow < n) npow <<= 1;
@@ -358,7 +358,7 @@ template <int DT> __device__ __forceinline__ uint32_t rk_of_xkey(uint32_t xk, fl
 
 // Smallest raw key (over all non-NaN floats) whose scaled key is >= target;
 // 0xff800001 when none.  Executed by one whole wave (64-ary search).
-template <int DT> __device__ uint32_t x_lower(uint32_t target, float T)
+template <int DT> __device__ __forceinline__ uint32_t x_lower(uint32_t target, float T)
 {
     const uint32_t XLO = 0x007fffffu, XHI = 0xff800000u;  // -inf .. +inf
     if (rk_of_xkey<DT>(XLO, T) >= target) return XLO;
@@ -381,7 +381,7 @@ template <int DT> __device__ uint32_t x_lower(uint32_t target, float T)
 }
 
 // Largest raw key whose scaled key is <= target (0x007ffffe when none).
-template <int DT> __device__ uint32_t x_upper(uint32_t target, float T)
+template <int DT> __device__ __forceinline__ uint32_t x_upper(uint32_t target, float T)
 {
     if (target == 0xffffffffu) return 0xff800000u;
     return x_lower<DT>(target + 1u, T) - 1u;

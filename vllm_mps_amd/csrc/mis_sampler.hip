@@ -55,59 +55,20 @@ constexpr int SURV_CAP = 1024;     // top-k survivors / top-p window held in LDS
 constexpr int G_MAX = 256;         // chunks per row
 constexpr int CB_N = 16;           // coarse top-p bins (lane-private)
 constexpr float CB_SCALE = 0.5f;   // coarse bin = floor(y * CB_SCALE): 2 units of y
-constexpr int RB_N = 256;          // sub-bins of a refinement round
-constexpr int WCAP = 4096;         // window slots per row in the workspace
-constexpr int MAX_REFINE = 4;      // refinement rounds before the re-read path
 constexpr int REGION_BINS = 1;     // L1 bins per 16-bit chain pass (re-read path)
 constexpr int RUN_CAP = REGION_BINS * 256;
 constexpr int TIE_CAP = 1024;
 constexpr uint32_t NCAND_OVERFLOW = 0xffffffffu;
 constexpr int32_t IDX_ALL = 0x7fffffff;
-constexpr uint32_t SPIN_LIMIT = 1u << 22;  // bounded cross-workgroup waits
 
 enum : int { M_BAD = 0, M_GREEDY = 1, M_SMALLK = 2, M_LARGEK = 3, M_TOPP = 4, M_TEMP = 5 };
 enum : uint32_t { FLAG_NAN = 1u, FLAG_PINF = 2u };
-// kinds of a published top-p round
-enum : uint32_t { R_REFINE = 1u, R_COLLECT = 2u, R_EXACT = 3u };
 
 // ------------------------------------------------------------------ workspace
 
-struct Ctl {                    // 256 B
-    uint32_t ticket;            // tickets drawn in the current launch
-    uint32_t error;             // bit 0: a bounded wait expired
-    uint32_t pad[62];
-};
-
-struct RowCtl {                 // 64 B per row, zero at rest
-    uint32_t arr;               // arrivals, cumulative over rounds
-    uint32_t round;             // last round published (round r + 1 runs after it); ROUND_DONE = finished
-    uint32_t exited;            // workgroups that left the row
-    uint32_t wcount;            // window elements appended by the collect round
-    uint32_t rtype;             // R_REFINE / R_COLLECT / R_EXACT of the published round
-    uint32_t klo, khi;          // scaled-key band of the round (inclusive)
-    uint32_t nref;              // refinement rounds so far
-    float lo, sc;               // refine: sub-bin = floor((y - lo) * sc)
-    float m;                    // row max of y
-    uint32_t pad;
-    double S;                   // row sum of weights exp(y - m) (f32-weight estimate)
-    double A;                   // top_p * S
-};
-constexpr uint32_t ROUND_DONE = 0xffffffffu;
-
-// row-wide refine histogram, filled by the chunks' global atomics; the leader
-// reads and clears it between rounds
-struct RowHist {                // 3 KB per row
-    uint32_t cnt[RB_N];
-    unsigned long long mass[RB_N];  // weights relative to the row max, 2^-40 units
-};
-constexpr double HIST_SCALE = 1099511627776.0;  // 2^40
-static_assert(sizeof(RowCtl) == 64, "RowCtl is 64 bytes");
-
-// The control prefix of the workspace (Ctl, then one RowCtl for every row the
-// ABI allows) sits at a fixed place whatever the shape, so control words that
-// each call leaves at zero stay zero for the next call of any shape.
-constexpr int64_t B_MAX = 65535;
-constexpr size_t CTL_PREFIX = 256 + sizeof(RowCtl) * (size_t)(B_MAX + 1);
+// The workspace keeps no state between calls: every word a call reads it has
+// written earlier in the same call.
+constexpr size_t CTL_PREFIX = 256;
 
 struct ChunkSum {               // 64 B per (row, chunk)
     uint32_t xkey;              // argmax key of the raw logits (NaN = 0xffffffff)
@@ -122,17 +83,13 @@ struct ChunkSum {               // 64 B per (row, chunk)
     double pad[3];
 };
 
-// per-(row, chunk) data of one top-p round; rewritten every round
-struct RoundBuf {               // 3328 B
-    double coarse[CB_N];        // round 1: mass per coarse bin (relative to the chunk max)
-    double S;                   // round 1 / exact round: sum of weights
-    double above;               // mass of keys above the band
-    double kept;                // final: kept weight of the chunk (relative to the row max)
-    uint32_t cnt[RB_N];         // refine: count per sub-bin
-    uint64_t mass[RB_N];        // refine: mass per sub-bin, fixed point (2^-32 units)
-    double pad[13];
+// per-(row, chunk) coarse mass bins of an fp32 top-p row
+struct RoundBuf {               // 256 B
+    double coarse[CB_N];        // mass per coarse bin (relative to the chunk max)
+    double S;                   // sum of weights relative to the chunk max
+    double pad[15];
 };
-static_assert(sizeof(RoundBuf) == 3328, "RoundBuf size");
+static_assert(sizeof(RoundBuf) == 256, "RoundBuf size");
 
 struct RowOut {                 // 64 B per row, read by k_emit
     int64_t id;
@@ -141,13 +98,10 @@ struct RowOut {                 // 64 B per row, read by k_emit
     float m;                    // row max of y
     uint32_t cut_key;           // kept iff key > cut_key or (key == cut_key and j <= cut_i)
     int32_t cut_i;
-    int32_t topp;               // fp32 top-p rows: TP_* outcome of the rounds (cleared by the row pass)
+    int32_t pad;
     double S;                   // sum of kept weights exp(y - m)
     double pad2[3];
 };
-
-// outcome of an fp32 top-p row's rounds, for the row pass
-enum : int32_t { TP_NONE = 0, TP_CUT = 1, TP_REREAD = 2, TP_INVALID = 3 };
 
 struct Cand { float x; int32_t idx; };
 struct Elem { uint32_t key; int32_t idx; };
@@ -155,33 +109,29 @@ struct Elem { uint32_t key; int32_t idx; };
 struct Layout {
     int64_t B, V;
     int ept, G;
-    size_t ctl, rowctl, rowout, chunks, rbuf, hist, cand, win, total;
+    size_t rowout, chunks, rbuf, cand, total;
 };
 
 static inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-// Elements per thread: 16 for fp32 and 32 for 16-bit logits (16 KB chunks),
-// 16-bit down to 16 when the batch would launch too few workgroups to fill
-// the chip, 64 when the row needs more than G_MAX chunks.
+// Elements per thread: 16 (chunks of 4096 elements; 16 vector registers of
+// logits per thread keep the chunk pass at six or more waves per SIMD), 64
+// when the row would need more than G_MAX chunks.
 static Layout make_layout(int64_t B, int64_t V, int dtype)
 {
     Layout L;
     L.B = B; L.V = V;
     auto chunks = [&](int ept) { return (V + (int64_t)NT * ept - 1) / ((int64_t)NT * ept); };
-    L.ept = dtype == MIS_DTYPE_F32 ? 16 : 32;
-    if (dtype != MIS_DTYPE_F32 && B * chunks(32) < 1024) L.ept = 16;
+    (void)dtype;
+    L.ept = 16;
     if (chunks(L.ept) > G_MAX) L.ept = 64;
     L.G = (int)chunks(L.ept);
     const size_t BG = (size_t)B * L.G;
-    size_t off = 0;
-    L.ctl = off;    off = align256(off + sizeof(Ctl));
-    L.rowctl = off; off = CTL_PREFIX;
+    size_t off = CTL_PREFIX;
     L.rowout = off; off = align256(off + sizeof(RowOut) * (size_t)B);
     L.chunks = off; off = align256(off + sizeof(ChunkSum) * BG);
     L.rbuf = off;   off = align256(off + sizeof(RoundBuf) * BG);
-    L.hist = off;   off = align256(off + sizeof(RowHist) * (size_t)B);
     L.cand = off;   off = align256(off + sizeof(Cand) * (size_t)CAND_CAP * BG);
-    L.win = off;    off = align256(off + sizeof(Elem) * (size_t)WCAP * (size_t)B);
     L.total = off;
     return L;
 }
@@ -254,26 +204,23 @@ struct RowCx {                 // what the leader of a row works with
 
 // ------------------------------------------------------------------ shared memory
 
-// One LDS layout for every phase of the kernel (about 24 KB, so six
-// workgroups fit on a CU): the chunk phase's lane-private coarse bins and the
-// leader's survivor / window arrays share the big union.
+// LDS of the row pass (one workgroup per row): the survivor / window arrays
+// and the re-read path's histograms share the big union.
 struct Smem {
     union {
-        float lp[CB_N][NT];                                                                 // 16 KB lane-private coarse bins
-        struct { uint32_t cnt[RB_N]; unsigned long long mass[RB_N]; } rf;                  // refine sub-bins (shared, sparse)
         struct { uint32_t cnt[2048]; } h11;                                                 // 8 KB
         struct { uint32_t cnt[256]; double mass[256]; } h8;                                 // 3 KB
         struct { uint32_t key[SURV_CAP]; int32_t idx[SURV_CAP]; double e[SURV_CAP]; } s;    // 16 KB
         struct { uint64_t k[SURV_CAP]; double e[SURV_CAP]; } so;                           // 16 KB
         struct { uint32_t cnt[RUN_CAP]; uint32_t rkey[RUN_CAP]; uint32_t rcnt[RUN_CAP]; float rp[RUN_CAP]; } r;
         struct { int32_t idx[TIE_CAP]; } t;
-        struct { double m[RB_N]; uint32_t c[RB_N]; } mg;                                    // leader merge of sub-bins
     } u;
     union {
         struct { uint32_t cnt[256]; double mass[256]; } l1;  // re-read path: level-1 histogram
         double coarse[CB_N];                                 // leader merge of coarse bins
     } v;
     double cw[G_MAX];          // per-chunk kept weight
+    double etab[ETAB_N];       // 2^(j/64) for dexp
     double chs[G_MAX];         // per-chunk rescale to the row max
     double sub_m[256];         // round-local histograms
     uint32_t sub_c[256];
@@ -286,6 +233,15 @@ struct Smem {
     Args args;                 // launch arguments, RowCx and RowPlan of the row for the
     RowCx cx;                  // leader's out-of-line functions (kept out of private
     RowPlan pl;                // memory, which would otherwise hold a copy per lane)
+};
+
+// LDS of the chunk pass: only what its per-mode reductions need (17 KB), so
+// that more of its workgroups fit on a CU
+struct ChunkSmem {
+    float lp[CB_N][NT];        // lane-private coarse bins (fp32 top-p)
+    double etab[ETAB_N];       // 2^(j/64) for dexp
+    Red red;
+    uint32_t bu[8];
 };
 
 __device__ __forceinline__ bool kept_by_cut(uint32_t key, int64_t j, uint32_t cut_key, int32_t cut_i)
@@ -301,43 +257,8 @@ __device__ __forceinline__ float opaque(float v)
     return v;
 }
 
-// ------------------------------------------------------------------ cross-workgroup hand-off
+// ------------------------------------------------------------------ loads of the row pass
 //
-// Summaries, candidates and round data go through device-coherent (agent
-// scope) stores and loads, which bypass the XCD-private L2s, so a leader on
-// another XCD reads what its row mates wrote.  A workgroup publishes by
-// waiting for its own stores (s_waitcnt) before the barrier that precedes its
-// arrival atomic.
-
-template <class T> struct same_t { typedef T type; };
-template <class T> __device__ __forceinline__ void st_dev(T *p, typename same_t<T>::type v)
-{
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-template <class T> __device__ __forceinline__ T ld_dev(const T *p)
-{
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void st_dev_cand(Cand *p, float x, int32_t idx)
-{
-    st_dev(reinterpret_cast<uint64_t *>(p), ((uint64_t)(uint32_t)idx << 32) | f32_bits(x));
-}
-__device__ __forceinline__ Cand ld_dev_cand(const Cand *p)
-{
-    const uint64_t v = ld_dev(reinterpret_cast<const uint64_t *>(p));
-    Cand c; c.x = bits_f32((uint32_t)v); c.idx = (int32_t)(uint32_t)(v >> 32);
-    return c;
-}
-__device__ __forceinline__ void st_dev_elem(Elem *p, uint32_t key, int32_t idx)
-{
-    st_dev(reinterpret_cast<uint64_t *>(p), ((uint64_t)(uint32_t)idx << 32) | key);
-}
-__device__ __forceinline__ Elem ld_dev_elem(const Elem *p)
-{
-    const uint64_t v = ld_dev(reinterpret_cast<const uint64_t *>(p));
-    Elem e; e.key = (uint32_t)v; e.idx = (int32_t)(uint32_t)(v >> 32);
-    return e;
-}
 // The row pass runs after the chunk pass has completed, so it reads the
 // summaries with ordinary (cached, freely batched) loads.
 template <class T> __device__ __forceinline__ T ldp(const T *p) { return *p; }
@@ -354,48 +275,10 @@ __device__ __forceinline__ uint32_t ncand_of(const ChunkSum *cs)
     return n < (uint32_t)CAND_CAP ? n : (uint32_t)CAND_CAP;
 }
 
-// Summaries only the row pass reads (after this kernel has completed) go
-// through ordinary stores; fp32 top-p rows, whose leader reads them during
-// the kernel, use the device-coherent ones.
-template <class T> __device__ __forceinline__ void st_sum(bool coherent, T *p, typename same_t<T>::type v)
-{
-    if (coherent) st_dev(p, v);
-    else *p = v;
-}
 
-// every thread's device-coherent stores are complete, then the workgroup
-// barrier: after it, thread 0 may signal arrival
-__device__ __forceinline__ void publish_barrier()
-{
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-}
-
-// Arrival of this workgroup at the row counter; returns the counter's old value.
-__device__ __forceinline__ uint32_t arrive(RowCtl *rc)
-{
-    return __hip_atomic_fetch_add(&rc->arr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Thread 0 waits until the row publishes a round beyond `r` or finishes
-// (one polled word).  Returns false when the spin limit expired (the row is
-// then abandoned).
-__device__ bool wait_round(RowCtl *rc, uint32_t r, uint32_t *err)
-{
-    uint32_t nap = 1;
-    for (uint32_t it = 0; it < SPIN_LIMIT; ++it) {
-        if (ld_dev(&rc->round) > r) return true;  // round r + 1 published, or ROUND_DONE
-        // back off: thousands of waiting workgroups must not flood the
-        // memory system with polls
-        if (nap < 8) { __builtin_amdgcn_s_sleep(4); ++nap; }
-        else __builtin_amdgcn_s_sleep(16);
-    }
-    __hip_atomic_fetch_or(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    return false;
-}
 
 // raw-key interval for a scaled-key interval, computed by wave 0
-template <int DT, class S> __device__ void x_interval(S &sm, uint32_t klo, uint32_t khi, float T, uint32_t *xlo, uint32_t *xhi)
+template <int DT, class S> __device__ __forceinline__ void x_interval(S &sm, uint32_t klo, uint32_t khi, float T, uint32_t *xlo, uint32_t *xhi)
 {
     __syncthreads();
     if (wave_id() == 0) {
@@ -409,7 +292,7 @@ template <int DT, class S> __device__ void x_interval(S &sm, uint32_t klo, uint3
     __syncthreads();
 }
 
-__device__ void write_row(RowOut *ro, const Args &a, int row, int64_t id, int status, int mode, float m,
+__device__ __forceinline__ void write_row(RowOut *ro, const Args &a, int row, int64_t id, int status, int mode, float m,
                           uint32_t cut_key, int32_t cut_i, double S)
 {
     if (threadIdx.x == 0) {
@@ -431,7 +314,7 @@ __device__ void write_row(RowOut *ro, const Args &a, int row, int64_t id, int st
 // order) exceeds `resid`; wfun(x, j) gives the weight (0 = not kept).  When
 // rounding leaves `resid` out of reach, the chunk's last kept index.
 template <int DT, class WF>
-__device__ int64_t draw_in_chunk(Smem &sm, const RowCx &c, int g, double resid, WF &&wfun)
+__device__ __forceinline__ int64_t draw_in_chunk(Smem &sm, const RowCx &c, int g, double resid, WF &&wfun)
 {
     // Thread t takes the contiguous elements [cbeg + t*per, cbeg + (t+1)*per)
     // of the chunk, loaded up front (16-byte vectors where aligned), so the
@@ -491,7 +374,7 @@ __device__ int64_t draw_in_chunk(Smem &sm, const RowCx &c, int g, double resid, 
 }
 
 // Chunk holding u * sum(sm.cw) and the residual weight inside it.
-__device__ void pick_chunk(Smem &sm, int G, float u, int *g_out, double *resid_out, double *S_out)
+__device__ __forceinline__ void pick_chunk(Smem &sm, int G, float u, int *g_out, double *resid_out, double *S_out)
 {
     __syncthreads();
     if (wave_id() == 0) {
@@ -518,7 +401,7 @@ __device__ void pick_chunk(Smem &sm, int G, float u, int *g_out, double *resid_o
 
 // First index (ascending) of an LDS element list at which the running weight
 // exceeds `target`: radix over index space, 256 buckets per level.
-__device__ int64_t draw_in_list(Smem &sm, const int32_t *idx, const double *e, int n, int64_t V, double target)
+__device__ __forceinline__ int64_t draw_in_list(Smem &sm, const int32_t *idx, const double *e, int n, int64_t V, double target)
 {
     int64_t lo = 0, hi = V;
     double acc = 0.0;
@@ -576,7 +459,7 @@ __device__ __forceinline__ void rescan(const RowCx &c, uint32_t xklo, uint32_t x
 // reaches target; else running count.  Returns the resolved key; *acc_out =
 // mass or count strictly above it; *kcnt = elements holding exactly it.
 template <int DT>
-__device__ __noinline__ uint32_t descend(Smem &sm, const RowCx &c, bool by_mass, double target, uint32_t floor_key,
+__device__ __forceinline__ uint32_t descend(Smem &sm, const RowCx &c, bool by_mass, double target, uint32_t floor_key,
                                          double *acc_out, uint32_t *kcnt)
 {
     __syncthreads();
@@ -627,7 +510,7 @@ __device__ __noinline__ uint32_t descend(Smem &sm, const RowCx &c, bool by_mass,
 
 // Index of the t-th (1-based) element in index order whose scaled key is `key`.
 template <int DT>
-__device__ __noinline__ int32_t tie_index(Smem &sm, const RowCx &c, uint32_t key, uint32_t t)
+__device__ __forceinline__ int32_t tie_index(Smem &sm, const RowCx &c, uint32_t key, uint32_t t)
 {
     uint32_t xlo, xhi;
     x_interval<DT>(sm, key, key, c.T, &xlo, &xhi);
@@ -666,7 +549,7 @@ __device__ __noinline__ int32_t tie_index(Smem &sm, const RowCx &c, uint32_t key
 // Sequential walk of the 16-bit top-p chain over runs (one thread).  Returns
 // true when some rank triggers removal; the cut then keeps *t_keep elements of
 // run *run_at (0 = the cut is the previous run).
-__device__ bool chain_walk(const uint32_t *rcnt, const float *rp, int nruns, float &F, float thr16, int dt,
+__device__ __forceinline__ bool chain_walk(const uint32_t *rcnt, const float *rp, int nruns, float &F, float thr16, int dt,
                            int *run_at, uint32_t *t_keep)
 {
     for (int r = 0; r < nruns; ++r) {
@@ -691,7 +574,7 @@ __device__ bool chain_walk(const uint32_t *rcnt, const float *rp, int nruns, flo
 // Top-p cut over elements with key >= floor_key; sm.v.l1 holds their 256-bin
 // histogram and S their total weight.
 template <int DT>
-__device__ __noinline__ void topp_cut_generic(Smem &sm, const RowCx &c, float top_p, uint32_t floor_key, double S,
+__device__ __forceinline__ void topp_cut_generic(Smem &sm, const RowCx &c, float top_p, uint32_t floor_key, double S,
                                               uint32_t *cut_key, int32_t *cut_i, int *status)
 {
     const double md = (double)c.m;
@@ -801,7 +684,7 @@ __device__ __noinline__ void topp_cut_generic(Smem &sm, const RowCx &c, float to
 // Full row by re-reads: top-k of any size by count descent, then top-p, then
 // the draw.  Serves large k', fp16/bf16 top-p and every overflow.
 template <int DT>
-__device__ __noinline__ void final_generic(Smem &sm, const RowCx &c, const RowPlan &pl, RowOut *ro, const Args &a)
+__device__ __forceinline__ void final_generic(Smem &sm, const RowCx &c, const RowPlan &pl, RowOut *ro, const Args &a)
 {
     if (DT != F32 && pl.kk > 0) {
         // the 16-bit top-k radix descent is switched off in this build
@@ -874,7 +757,7 @@ __device__ __noinline__ void final_generic(Smem &sm, const RowCx &c, const RowPl
 // key << 32 | ~idx, mass); the last kept element is found by a block scan.
 // Returns its sorted position, or -1 when the cut is not inside the window.
 // *q_last = mass before the last kept element, *w_last = its weight.
-__device__ int window_resolve(Smem &sm, uint32_t n, double above, double A, uint32_t *cut_key, int32_t *cut_i,
+__device__ __forceinline__ int window_resolve(Smem &sm, uint32_t n, double above, double A, uint32_t *cut_key, int32_t *cut_i,
                               double *q_last, double *w_last)
 {
     constexpr int PT = SURV_CAP / NT;
@@ -934,7 +817,7 @@ __device__ int window_resolve(Smem &sm, uint32_t n, double above, double A, uint
 // overflowed its candidate buffer, when a truncated chunk may hide an element
 // at or above the k'-th value, or when the survivors overflow LDS.
 template <int DT>
-__device__ __noinline__ bool leader_smallk(Smem &sm, const RowCx &c, const RowPlan &pl, const ChunkSum *cs,
+__device__ __forceinline__ bool leader_smallk(Smem &sm, const RowCx &c, const RowPlan &pl, const ChunkSum *cs,
                                           const Cand *cand, RowOut *ro, const Args &a)
 {
     const double md = (double)c.m;
@@ -976,49 +859,67 @@ __device__ __noinline__ bool leader_smallk(Smem &sm, const RowCx &c, const RowPl
         return cand + (size_t)lo * CAND_CAP + (f - pre[lo]);
     };
     constexpr int BATCH = 8;  // candidate loads in flight per thread
-    // k'-th largest raw key over the candidates: 11 / 11 / 10-bit digits.  Fewer
-    // candidates than k' means fewer finite elements than k' in the row.
+    // k'-th largest raw value over the candidates: linear bins between the
+    // smallest and largest candidate (values that differ spread over the bins,
+    // so the LDS counters see few conflicts), then the boundary bin's
+    // candidates sorted.  Fewer candidates than k' means fewer finite
+    // elements than k' in the row.
     uint32_t xk_thr = 0u;
     if (!all_fin) {
-        uint32_t prefix = 0u, rem = (uint32_t)pl.kk;
-        for (int lev = 0; lev < 3; ++lev) {
-            const int sh = lev == 0 ? 21 : (lev == 1 ? 10 : 0);
-            const int nbits = lev == 2 ? 10 : 11;
-            const int nb = 1 << nbits;
-            const uint32_t hmask = lev == 0 ? 0u : ~((1u << (sh + nbits)) - 1u);
-            __syncthreads();
-            for (int i = threadIdx.x; i < 2048; i += NT) sm.u.h11.cnt[i] = 0u;
-            __syncthreads();
+        auto for_cands = [&](auto &&fn) {
             for (uint32_t f0 = 0; f0 < ntot; f0 += NT * BATCH) {
-                // addresses first (LDS reads), then the loads back to back
                 const Cand *cp[BATCH];
 #pragma unroll
                 for (int u = 0; u < BATCH; ++u) {
                     const uint32_t f = f0 + (uint32_t)(u * NT) + threadIdx.x;
                     cp[u] = cand_ptr(f < ntot ? f : 0u);
                 }
-                uint32_t kv[BATCH];
+                float xv[BATCH];
 #pragma unroll
-                for (int u = 0; u < BATCH; ++u) kv[u] = key_of_f32(ldp_cand(cp[u]).x);
+                for (int u = 0; u < BATCH; ++u) xv[u] = ldp_cand(cp[u]).x;
 #pragma unroll
-                for (int u = 0; u < BATCH; ++u) {
-                    const uint32_t f = f0 + (uint32_t)(u * NT) + threadIdx.x;
-                    if (f < ntot && (kv[u] & hmask) == (prefix & hmask))
-                        atomicAdd(&sm.u.h11.cnt[(kv[u] >> sh) & (uint32_t)(nb - 1)], 1u);
-                }
+                for (int u = 0; u < BATCH; ++u)
+                    if (f0 + (uint32_t)(u * NT) + threadIdx.x < ntot) fn(xv[u]);
             }
+        };
+        float cmin = INFINITY, cmax = -INFINITY;
+        for_cands([&](float x) { cmin = fminf(cmin, x); cmax = fmaxf(cmax, x); });
+        cmin = block_min<float>(cmin, sm.red);
+        cmax = block_max<float>(cmax, sm.red);
+        if (!(cmax > cmin)) {
+            xk_thr = key_of_f32(cmax);  // every candidate holds the same value
+        } else {
+            const float inv = 2048.0f / (cmax - cmin);
+            auto bin_of = [&](float x) -> int { return min(2047, (int)((x - cmin) * inv)); };
+            for (int i = threadIdx.x; i < 2048; i += NT) sm.u.h11.cnt[i] = 0u;
+            __syncthreads();
+            for_cands([&](float x) { atomicAdd(&sm.u.h11.cnt[bin_of(x)], 1u); });
             __syncthreads();
             if (wave_id() == 0) {
                 uint32_t above;
-                const int d = wave_find_desc<uint32_t>(sm.u.h11.cnt, nb, rem, &above);
-                if (lane_id() == 0) { sm.bu[0] = (uint32_t)d; sm.bu[1] = above; }
+                const int d = wave_find_desc<uint32_t>(sm.u.h11.cnt, 2048, (uint32_t)pl.kk, &above);
+                if (lane_id() == 0) { sm.bu[0] = (uint32_t)d; sm.bu[1] = above; sm.bu[2] = sm.u.h11.cnt[d]; }
             }
             __syncthreads();
-            rem -= sm.bu[1];
-            prefix |= sm.bu[0] << sh;
+            const int bsel = (int)sm.bu[0];
+            const uint32_t above = sm.bu[1], nbin = sm.bu[2];
+            if (nbin > (uint32_t)SURV_CAP || (uint32_t)pl.kk <= above) return false;
+            __syncthreads();
+            if (threadIdx.x == 0) sm.bu[3] = 0u;
+            __syncthreads();
+            for_cands([&](float x) {
+                if (bin_of(x) == bsel) {
+                    const uint32_t q = atomicAdd(&sm.bu[3], 1u);
+                    if (q < (uint32_t)SURV_CAP) { sm.u.so.k[q] = key_of_f32(x); sm.u.so.e[q] = 0.0; }
+                }
+            });
+            __syncthreads();
+            const int nb = (int)min(sm.bu[3], (uint32_t)SURV_CAP);
+            __syncthreads();
+            block_sort_desc(sm.u.so.k, sm.u.so.e, nb);
+            xk_thr = (uint32_t)sm.u.so.k[(int)((uint32_t)pl.kk - above) - 1];
             __syncthreads();
         }
-        xk_thr = prefix;
     }
     // survivors: scaled value >= scale(k'-th raw value); the ties the scaling
     // creates are kept, as the reference keeps them
@@ -1202,7 +1103,7 @@ __device__ __noinline__ bool leader_smallk(Smem &sm, const RowCx &c, const RowPl
 
 // Smallest key in [lo, hi] where the monotone predicate (false ... true) holds,
 // hi + 1 when it holds nowhere.  Run by one whole wave (64-ary search).
-template <class P> __device__ uint32_t key_search(uint32_t lo, uint32_t hi, P &&pred)
+template <class P> __device__ __forceinline__ uint32_t key_search(uint32_t lo, uint32_t hi, P &&pred)
 {
     if (lo > hi) return hi + 1u;
     if (pred(lo)) return lo;
@@ -1228,7 +1129,7 @@ template <class P> __device__ uint32_t key_search(uint32_t lo, uint32_t hi, P &&
 // Leader of a row that needs no refinement rounds: greedy, temperature only,
 // small top-k, and the re-read path for everything else.
 template <int DT>
-__device__ __noinline__ void leader_row(Smem &sm, RowCx &c, const RowPlan &pl, const ChunkSum *csr, RowOut *ro,
+__device__ __forceinline__ void leader_row(Smem &sm, RowCx &c, const RowPlan &pl, const ChunkSum *csr, RowOut *ro,
                                         const Args &a)
 {
     const int tid = threadIdx.x, row = c.row;
@@ -1298,13 +1199,13 @@ __device__ __noinline__ void leader_row(Smem &sm, RowCx &c, const RowPlan &pl, c
 // Per-chunk scale factors exp(ymax_c - m) into sm.chs; returns the row max m
 // and whether any chunk flagged NaN / +inf.  One load pair per chunk and
 // thread, issued together.
-__device__ float row_scales(Smem &sm, const ChunkSum *csr, int G, uint32_t *bad)
+__device__ __forceinline__ float row_scales(Smem &sm, const ChunkSum *csr, int G, uint32_t *bad)
 {
     uint32_t anyflag = 0u;
     float m = -INFINITY;
     for (int g = threadIdx.x; g < G; g += NT) {
-        const uint32_t f = ld_dev(&csr[g].flags);
-        const float yg = ld_dev(&csr[g].ymax);
+        const uint32_t f = ldp(&csr[g].flags);
+        const float yg = ldp(&csr[g].ymax);
         anyflag |= f;
         m = fmaxf(m, yg);
         sm.chs[g] = (double)yg;
@@ -1322,257 +1223,29 @@ __device__ float row_scales(Smem &sm, const ChunkSum *csr, int G, uint32_t *bad)
 }
 
 __device__ __forceinline__ float coarse_bin(float y) { return floorf(y * CB_SCALE); }
-__device__ __forceinline__ int sub_bin(float y, float lo, float sc)
-{
-    return (int)fminf(fmaxf(floorf((y - lo) * sc), 0.0f), (float)(RB_N - 1));
-}
 
-// Publishes the next round of an fp32 top-p row (thread 0 writes RowCtl).
-__device__ void publish_round(RowCtl *rc, uint32_t r_next, uint32_t rtype, uint32_t klo, uint32_t khi, uint32_t nref)
+// One coalesced read of a chunk into registers (16-byte vectors where the row
+// allows); -inf past the end of the row.
+template <int DT, int EPT>
+__device__ __forceinline__ void load_chunk(const char *rowp, int64_t base, int64_t V, int vec_ok, float (&x)[EPT])
 {
-    if (threadIdx.x == 0) {
-        const float lo = f32_of_key(klo), hi = f32_of_key(khi);
-        const float sc = hi > lo ? (float)RB_N / (hi - lo) : 0.0f;
-        st_dev(&rc->rtype, rtype);
-        st_dev(&rc->klo, klo);
-        st_dev(&rc->khi, khi);
-        st_dev(&rc->lo, lo);
-        st_dev(&rc->sc, sc);
-        st_dev(&rc->nref, nref);
-        if (rtype == R_COLLECT) st_dev(&rc->wcount, 0u);
-        __builtin_amdgcn_s_waitcnt(0);
-        st_dev(&rc->round, r_next);
-    }
-}
-
-// Final outcome of an fp32 top-p row's rounds: recorded for the row pass
-// (which draws, or re-reads the row), then the row mates are released.
-__device__ void topp_outcome(RowCtl *rc, RowOut *ro, int32_t outcome, float m, uint32_t cut_key, int32_t cut_i,
-                             double S)
-{
-    if (threadIdx.x == 0) {
-        ro->m = m;
-        ro->cut_key = cut_key;
-        ro->cut_i = cut_i;
-        ro->S = S;
-        ro->topp = outcome;
-        __builtin_amdgcn_s_waitcnt(0);
-        st_dev(&rc->round, ROUND_DONE);
-    }
-}
-
-// Leader of an fp32 top-p row once all its chunks have finished round r
-// (1 = coarse bins, else the kind in rc->rtype).  Publishes round r + 1, or
-// finishes the row: the cut and the per-chunk kept weights (TP_CUT), or a
-// hand-over to the row pass's re-read path (TP_REREAD), or TP_INVALID.
-// Reads of the row mates' data are issued in batches: each dependent
-// device-coherent load costs a full memory round trip.
-template <int DT>
-__device__ __noinline__ void leader_topp(Smem &sm, RowCx &c, const RowPlan &pl, const ChunkSum *csr, RoundBuf *rbf,
-                                         RowCtl *rc, RowHist *hist, const Elem *win, RowOut *ro, uint32_t r)
-{
-    const int tid = threadIdx.x, G = c.G;
-    if (tid == 0) {  // the row's control words, loaded together
-        const uint32_t rt = ld_dev(&rc->rtype), k0 = ld_dev(&rc->klo), k1 = ld_dev(&rc->khi);
-        const uint32_t nr = ld_dev(&rc->nref), nw = ld_dev(&rc->wcount);
-        const float lo = ld_dev(&rc->lo), sc = ld_dev(&rc->sc);
-        const double S = ld_dev(&rc->S), A = ld_dev(&rc->A);
-        sm.bu[0] = rt; sm.bu[1] = k0; sm.bu[2] = k1; sm.bu[3] = nr; sm.bu[4] = nw;
-        sm.bf[1] = lo; sm.bf[2] = sc; sm.bd[6] = S; sm.bd[7] = A;
-    }
-    uint32_t bad;
-    const float m = row_scales(sm, csr, G, &bad);  // its barriers publish the words above
-    c.m = m;
-    const double md = (double)m;
-    const uint32_t rtype = r == 1 ? 0u : sm.bu[0];
-    const uint32_t klo = sm.bu[1], khi = sm.bu[2], nref = sm.bu[3], nw0 = sm.bu[4];
-    const float blo = sm.bf[1], bsc = sm.bf[2];
-    const double S0 = sm.bd[6], A0 = sm.bd[7];
-    __syncthreads();
-    // the f32 weights of the chunk pass carry relative error <= WEXP_REL_ERR;
-    // band choices keep a wider margin, for the f32 and fixed-point bin sums
-    if (r == 1) {
-        if (bad != 0u || m == -INFINITY) {
-            topp_outcome(rc, ro, TP_INVALID, m, 0u, 0, 0.0);
-            return;
-        }
-        // S, and the coarse bins on the row grid: row bin b <-> coarse index Ar - b
-        const float Ar = coarse_bin(m);
-        double s = 0.0;
-        for (int g = tid; g < G; g += NT) s += ld_dev(&rbf[g].S) * sm.chs[g];
-        const double S = block_sum<double>(s, sm.red);
-        const double A = (double)pl.top_p * S;
-        if (tid < CB_N) sm.v.coarse[tid] = 0.0;
-        constexpr int GP = NT / CB_N;  // chunks per pass, one value per thread
-        for (int g0 = 0; g0 < G; g0 += GP) {
-            const int gl = tid / CB_N, lb = tid % CB_N, g = g0 + gl;
-            double v = 0.0;
-            int off = CB_N;  // row bin of chunk bin 0; CB_N = none
-            if (g < G) {
-                const double cv = ld_dev(&rbf[g].coarse[lb]);
-                const float yg = ld_dev(&csr[g].ymax);
-                if (yg != -INFINITY) { v = cv * sm.chs[g]; off = (int)(Ar - coarse_bin(yg)); }
-            }
-            sm.u.mg.m[tid] = v;             // [gl][lb]
-            if (lb == 0) sm.u.mg.c[gl] = (uint32_t)off;
-            __syncthreads();
-            if (tid < CB_N) {               // row bin tid <- chunk bin tid - off of each chunk
-                double acc = 0.0;
-                for (int q = 0; q < GP; ++q) {
-                    const int l2 = tid - (int)sm.u.mg.c[q];
-                    if (l2 >= 0 && l2 < CB_N) acc += sm.u.mg.m[q * CB_N + l2];
-                }
-                sm.v.coarse[tid] += acc;
-            }
-            __syncthreads();
-        }
-        if (tid == 0) {
-            const double delta = 1e-5 * S;
-            double cum = 0.0;
-            int ba = -1, bb = -1;
-            for (int b = 0; b < CB_N; ++b) {
-                const double nx = cum + sm.v.coarse[b];
-                if (nx >= A - delta && cum <= A + delta) { if (ba < 0) ba = b; bb = b; }
-                cum = nx;
-            }
-            sm.bi[0] = ba; sm.bi[1] = bb;
-            st_dev(&rc->m, m); st_dev(&rc->S, S); st_dev(&rc->A, A);
-        }
-        // the row histogram starts clear for the refine round
-        for (int j = tid; j < RB_N; j += NT) { st_dev(&hist->cnt[j], 0u); st_dev(&hist->mass[j], 0ull); }
-        __syncthreads();
-        const int ba = sm.bi[0], bb = sm.bi[1];
-        if (ba < 0) {  // the cut lies below the coarse range
-            topp_outcome(rc, ro, TP_REREAD, m, 0u, 0, 0.0);
-            return;
-        }
-        // key interval of coarse indices [Ar - bb, Ar - ba]
-        const float cb_lo = Ar - (float)bb, cb_hi = Ar - (float)ba;
-        if (wave_id() == 0) {
-            const uint32_t kfin = row_key(-INFINITY, DT) + 1u, ktop = 0xff7fffffu;  // finite keys
-            const uint32_t k0 = key_search(kfin, ktop, [&](uint32_t k) { return coarse_bin(f32_of_key(k)) >= cb_lo; });
-            const uint32_t k1 = key_search(kfin, ktop, [&](uint32_t k) { return coarse_bin(f32_of_key(k)) > cb_hi; }) - 1u;
-            if (lane_id() == 0) { sm.bu[5] = k0; sm.bu[6] = k1; }
-        }
-        __syncthreads();
-        publish_round(rc, 2u, R_REFINE, sm.bu[5], sm.bu[6], 0u);
-        return;
-    }
-    double above = 0.0;
-    for (int g = tid; g < G; g += NT) above += ld_dev(&rbf[g].above) * sm.chs[g];
-    above = block_sum<double>(above, sm.red);
-    if (rtype == R_REFINE) {
-        // the row histogram: one entry per thread, cleared behind the read
-        const uint32_t cn = ld_dev(&hist->cnt[tid]);
-        const unsigned long long ms = ld_dev(&hist->mass[tid]);
-        sm.u.mg.m[tid] = (double)ms * (1.0 / HIST_SCALE);
-        sm.u.mg.c[tid] = cn;
-        st_dev(&hist->cnt[tid], 0u);
-        st_dev(&hist->mass[tid], 0ull);
-        __syncthreads();
-        if (wave_id() == 0) {
-            // band: sub-bins (descending y) whose cumulative mass interval meets
-            // [A - delta, A + delta]; jb = first to reach A - delta, ja = first
-            // to pass A + delta (or the lowest non-empty one)
-            const double delta = 1e-5 * S0;
-            double ab;
-            const int jb = wave_find_desc<double>(sm.u.mg.m, RB_N, A0 - delta - above, &ab);
-            const int ja = wave_find_desc<double>(sm.u.mg.m, RB_N, A0 + delta - above, &ab);
-            uint32_t cnt = 0;
-            for (int j = lane_id(); j < RB_N; j += 64) cnt += (j >= ja && j <= jb) ? sm.u.mg.c[j] : 0u;
-            cnt = wave_sum(cnt);
-            double tot = 0.0;
-            for (int j = lane_id(); j < RB_N; j += 64) tot += sm.u.mg.m[j];
-            tot = wave_sum(tot);
-            if (lane_id() == 0) {
-                // the band must reach the target from above and below
-                const bool ok = above <= A0 + delta && above + tot >= A0 - delta && cnt > 0u && ja <= jb;
-                sm.bi[0] = ok ? ja : -1; sm.bi[1] = jb; sm.bu[7] = cnt;
-            }
-        }
-        __syncthreads();
-        const int ja = sm.bi[0], jb = sm.bi[1];
-        const uint32_t cnt = sm.bu[7];
-        if (ja < 0) {
-            topp_outcome(rc, ro, TP_REREAD, m, 0u, 0, 0.0);
-            return;
-        }
-        if (wave_id() == 0) {
-            const uint32_t k0 = key_search(klo, khi, [&](uint32_t k) { return sub_bin(f32_of_key(k), blo, bsc) >= ja; });
-            const uint32_t k1 = key_search(klo, khi, [&](uint32_t k) { return sub_bin(f32_of_key(k), blo, bsc) > jb; }) - 1u;
-            if (lane_id() == 0) { sm.bu[5] = k0; sm.bu[6] = k1; }
-        }
-        __syncthreads();
-        const uint32_t k0 = sm.bu[5], k1 = sm.bu[6];
-        __syncthreads();
-        if (cnt <= (uint32_t)SURV_CAP) publish_round(rc, r + 1u, R_COLLECT, k0, k1, nref);
-        else if (k0 >= k1 || nref + 1u >= (uint32_t)MAX_REFINE) topp_outcome(rc, ro, TP_REREAD, m, 0u, 0, 0.0);
-        else publish_round(rc, r + 1u, R_REFINE, k0, k1, nref + 1u);
-        return;
-    }
-    // collect or exact round: the window is in the workspace
-    const bool exact = rtype == R_EXACT;
-    double S = S0, A = A0;
-    if (exact) {
-        double s = 0.0;
-        for (int g = tid; g < G; g += NT) s += ld_dev(&rbf[g].S) * sm.chs[g];
-        S = block_sum<double>(s, sm.red);
-        A = (double)pl.top_p * S;
-    }
-    const uint32_t nw = nw0;
-    if (nw > (uint32_t)SURV_CAP) {
-        topp_outcome(rc, ro, TP_REREAD, m, 0u, 0, 0.0);
-        return;
-    }
-    {
-        constexpr int PER = SURV_CAP / NT;  // window loads, issued together
-        Elem el[PER];
+    constexpr int VEC = Traits<DT>::VEC, NV = EPT / VEC, CH = NT * EPT;
+    const int tid = threadIdx.x;
+    if (vec_ok && base + CH <= V) {
 #pragma unroll
-        for (int q = 0; q < PER; ++q) {
-            const uint32_t i = (uint32_t)(q * NT + tid);
-            el[q] = i < nw ? ld_dev_elem(&win[i]) : Elem{0u, 0};
-        }
+        for (int v = 0; v < NV; ++v) loadvec<DT>(rowp, base + ((int64_t)v * NT + tid) * VEC, &x[v * VEC]);
+    } else {
 #pragma unroll
-        for (int q = 0; q < PER; ++q) {
-            const uint32_t i = (uint32_t)(q * NT + tid);
-            if (i < nw) {
-                sm.u.s.key[i] = el[q].key;
-                sm.u.s.idx[i] = el[q].idx;
-                sm.u.s.e[i] = exp((double)f32_of_key(el[q].key) - md);
+        for (int v = 0; v < NV; ++v) {
+            const int64_t j0 = base + ((int64_t)v * NT + tid) * VEC;
+            if (vec_ok && j0 + VEC <= V) {
+                loadvec<DT>(rowp, j0, &x[v * VEC]);
+            } else {
+#pragma unroll
+                for (int e = 0; e < VEC; ++e) x[v * VEC + e] = (j0 + e < V) ? load1<DT>(rowp, j0 + e) : -INFINITY;
             }
         }
     }
-    __syncthreads();
-    uint32_t cut_key = 0u;
-    int32_t cut_i = 0;
-    double ql = 0.0, wl = 0.0;
-    const int rl = window_resolve(sm, nw, above, A, &cut_key, &cut_i, &ql, &wl);
-    const bool inside = rl >= 0;
-    // the decision is proven when both margins exceed the error of the f32
-    // weights summed into `above` and S
-    const double err = exact ? 0.0 : (WEXP_REL_ERR + 1e-12) * (above + A) + 1e-300;
-    const bool robust = inside && (A - ql) > err && (ql + wl - A) > err;
-    if (!exact && !robust) {
-        publish_round(rc, r + 1u, R_EXACT, klo, khi, nref);
-        return;
-    }
-    if (!inside) {
-        topp_outcome(rc, ro, TP_REREAD, m, 0u, 0, 0.0);
-        return;
-    }
-    // per-chunk kept weight: everything above the window, plus the window's
-    // kept prefix (sorted positions 0 .. rl); the row pass draws from them
-    for (int g = tid; g < G; g += NT) sm.cw[g] = ld_dev(&rbf[g].above) * sm.chs[g];
-    __syncthreads();
-    for (int q = tid; q <= rl; q += NT) {
-        const int32_t j = (int32_t)(0xffffffffu - (uint32_t)sm.u.so.k[q]);
-        atomicAdd(&sm.cw[(int)(j / c.CH)], sm.u.so.e[q]);
-    }
-    __syncthreads();
-    double SK = 0.0;
-    for (int g = tid; g < G; g += NT) { SK += sm.cw[g]; rbf[g].kept = sm.cw[g]; }
-    SK = block_sum<double>(SK, sm.red);
-    topp_outcome(rc, ro, TP_CUT, m, cut_key, cut_i, SK);
 }
 
 // ------------------------------------------------------------------ the kernel
@@ -1595,21 +1268,16 @@ __device__ __forceinline__ uint32_t wave_sort_asc(uint32_t v)
 
 // The chunk pass: one workgroup per (row, chunk).  Loads the chunk into
 // registers and reduces it for the row's mode to the summary the row pass
-// reads.  fp32 top-p rows stay for the refinement rounds, led by the last
-// workgroup of the row to arrive in each round.
+// reads.  fp32 top-p rows also bin their mass coarsely for the row pass.
 template <int DT, int EPT>
-__global__ __launch_bounds__(NT, 5) void k_sample(Args a)
+__global__ __launch_bounds__(NT) void k_sample(Args a)
 {
-    constexpr int VEC = Traits<DT>::VEC, NV = EPT / VEC, CH = NT * EPT;
-    __shared__ Smem sm;
+    constexpr int VEC = Traits<DT>::VEC, CH = NT * EPT;
+    __shared__ ChunkSmem sm;
     const Layout &L = a.L;
     const int tid = threadIdx.x;
     const int G = L.G;
-    Ctl *ctl = reinterpret_cast<Ctl *>(a.ws + L.ctl);
-    // workgroups are dispatched in blockIdx order on every XCD, and a row's
-    // chunks have consecutive indices: a workgroup that waits for row mates
-    // waits only for ones dispatched no later than the row's last chunk
-    const uint32_t task = blockIdx.x;
+    const uint32_t task = blockIdx.x;  // a row's chunks have consecutive indices
     const int row = (int)(task / (uint32_t)G), chunk = (int)(task % (uint32_t)G);
     const int64_t V = a.V;
     const int64_t base = (int64_t)chunk * CH;
@@ -1619,35 +1287,11 @@ __global__ __launch_bounds__(NT, 5) void k_sample(Args a)
     const RowPlan pl = plan_row(P, V);
     ChunkSum *csr = reinterpret_cast<ChunkSum *>(a.ws + L.chunks) + (size_t)row * G;
     ChunkSum *cs = csr + chunk;
-    RowCtl *rc = reinterpret_cast<RowCtl *>(a.ws + L.rowctl) + row;
-    RowOut *ro = reinterpret_cast<RowOut *>(a.ws + L.rowout) + row;
-    RoundBuf *rbr = reinterpret_cast<RoundBuf *>(a.ws + L.rbuf) + (size_t)row * G;
-    RoundBuf *rb = rbr + chunk;
-    if (tid == 0) {
-        sm.args = a;
-        RowCx &c = sm.cx;
-        c.rowp = rowp; c.V = V; c.vec_ok = a.vec_ok; c.m = 0.0f; c.G = G; c.CH = CH; c.row = row; c.T = pl.T;
-        sm.pl = pl;
-    }
+    RoundBuf *rb = reinterpret_cast<RoundBuf *>(a.ws + L.rbuf) + (size_t)row * G + chunk;
 
     if (chunk == 0) trace(a.ws, L, row, 0);
-    // ---- one coalesced read of the chunk into registers; -inf past the row
     float x[EPT];
-    if (a.vec_ok && base + CH <= V) {
-#pragma unroll
-        for (int v = 0; v < NV; ++v) loadvec<DT>(rowp, base + ((int64_t)v * NT + tid) * VEC, &x[v * VEC]);
-    } else {
-#pragma unroll
-        for (int v = 0; v < NV; ++v) {
-            const int64_t j0 = base + ((int64_t)v * NT + tid) * VEC;
-            if (a.vec_ok && j0 + VEC <= V) {
-                loadvec<DT>(rowp, j0, &x[v * VEC]);
-            } else {
-#pragma unroll
-                for (int e = 0; e < VEC; ++e) x[v * VEC + e] = (j0 + e < V) ? load1<DT>(rowp, j0 + e) : -INFINITY;
-            }
-        }
-    }
+    load_chunk<DT, EPT>(rowp, base, V, a.vec_ok, x);
     const int32_t base32 = (int32_t)base;  // V < 2^31
     auto idx_of = [&](int i) -> int32_t { return base32 + (int32_t)((((i / VEC) * NT + tid) * VEC) + (i % VEC)); };
 
@@ -1705,29 +1349,34 @@ __global__ __launch_bounds__(NT, 5) void k_sample(Args a)
             // floor(y / 2); bins more than CB_N below the chunk's are not kept.
             // Each lane owns one column of the bins, so plain read-modify-write
             // suffices (LDS float atomics serialise)
+            // S in float64 from dexp (relative error below 1e-15), so the row
+            // pass can decide the cut against exact masses
             const float Ac = coarse_bin(ymax);
+            exp_table(sm.etab, tid);
 #pragma unroll
-            for (int b = 0; b < CB_N; ++b) sm.u.lp[b][tid] = 0.0f;
+            for (int b = 0; b < CB_N; ++b) sm.lp[b][tid] = 0.0f;
+            __syncthreads();
+            const double ymd = (double)ymax;
             double s = 0.0;
 #pragma unroll
             for (int i = 0; i < EPT; ++i) {
                 const float y = scale_r<DT>(opaque(x[i]), T, rT);
-                const float w = wexp(y, ymax);
-                s += (double)w;
+                const double e = dexp((double)y - ymd, sm.etab);
+                s += e;
                 const float cb = Ac - coarse_bin(y);
-                if (cb < (float)CB_N) { const int cbi = (int)cb; sm.u.lp[cbi][tid] += w; }  // lane-private: no atomic
+                if (cb < (float)CB_N) { const int cbi = (int)cb; sm.lp[cbi][tid] += (float)e; }  // lane-private: no atomic
             }
             Sc = block_sum<double>(s, sm.red);  // its barriers also order the bins
             {
                 const int b = tid >> 4, q = tid & 15;
                 double t = 0.0;
 #pragma unroll
-                for (int l = 0; l < 16; ++l) t += (double)sm.u.lp[b][q * 16 + l];
+                for (int l = 0; l < 16; ++l) t += (double)sm.lp[b][q * 16 + l];
 #pragma unroll
                 for (int o = 8; o > 0; o >>= 1) t += __shfl_xor(t, o, 64);
-                if (q == 0) st_dev(&rb->coarse[b], t);
+                if (q == 0) rb->coarse[b] = t;
             }
-            if (tid == 0) st_dev(&rb->S, Sc);
+            if (tid == 0) rb->S = Sc;
         } else if (live && pl.mode == M_SMALLK) {
             // ---- candidates: every finite x whose scaled key reaches a threshold
             // taken from the per-thread maxima, enough for n_c candidates
@@ -1791,185 +1440,259 @@ __global__ __launch_bounds__(NT, 5) void k_sample(Args a)
             trunc = total < nfin ? 1u : 0u;
         }
         if (tid == 0) {
-            const bool co = topp32;
-            st_sum(co, &cs->xkey, 0u); st_sum(co, &cs->xarg, IDX_ALL);
-            st_sum(co, &cs->ymax, ymax); st_sum(co, &cs->flags, flags); st_sum(co, &cs->S, Sc);
-            st_sum(co, &cs->ncand, ncand); st_sum(co, &cs->nfin, nfin); st_sum(co, &cs->kc, kc); st_sum(co, &cs->trunc, trunc);
+            cs->xkey = 0u; cs->xarg = IDX_ALL; cs->ymax = ymax; cs->flags = flags; cs->S = Sc;
+            cs->ncand = ncand; cs->nfin = nfin; cs->kc = kc; cs->trunc = trunc;
         }
     }
-    if (topp32) publish_barrier();
     if (chunk == 0) trace(a.ws, L, row, 1);
-
-    if (!topp32) return;  // the row pass finishes the row from the summaries
-
-    // ---- fp32 top-p: refinement rounds with the chunk held in registers
-    const Elem *winr = reinterpret_cast<const Elem *>(a.ws + L.win) + (size_t)row * WCAP;
-    RowHist *hist = reinterpret_cast<RowHist *>(a.ws + L.hist) + row;
-    Elem *winw = reinterpret_cast<Elem *>(a.ws + L.win) + (size_t)row * WCAP;
-    const float T = pl.T, rT = 1.0f / pl.T;
-    uint32_t r = 1;
-    bool timed_out = false;
-    for (;;) {
-        if (tid == 0) sm.bu[6] = arrive(rc) + 1u == r * (uint32_t)G ? 1u : 0u;
-        __syncthreads();
-        const bool lead = sm.bu[6] != 0u;
-        __syncthreads();
-        if (lead) {
-            trace(a.ws, L, row, 2 * (int)r);
-            leader_topp<DT>(sm, sm.cx, sm.pl, csr, rbr, rc, hist, winr, ro, r);
-            trace(a.ws, L, row, 2 * (int)r + 1);
-        }
-        if (tid == 0) {
-            const bool ok = wait_round(rc, r, &ctl->error);
-            const uint32_t rd = ld_dev(&rc->round);
-            uint32_t st = 0u;
-            if (!ok) st = 2u;
-            else if (rd == ROUND_DONE) st = 1u;
-            sm.bu[5] = st;
-            if (st == 0u) {  // the round's parameters, loaded together
-                const uint32_t rt = ld_dev(&rc->rtype), k0 = ld_dev(&rc->klo), k1 = ld_dev(&rc->khi);
-                const float lo = ld_dev(&rc->lo), sc = ld_dev(&rc->sc), mr = ld_dev(&rc->m);
-                sm.bu[0] = rt; sm.bu[1] = k0; sm.bu[2] = k1;
-                sm.bf[0] = lo; sm.bf[1] = sc; sm.bf[2] = mr;
-            }
-        }
-        __syncthreads();
-        const uint32_t st = sm.bu[5];
-        if (st != 0u) { timed_out = st == 2u; break; }
-        const uint32_t rtype = uni(sm.bu[0]), klo = uni(sm.bu[1]), khi = uni(sm.bu[2]);
-        const float lo = uni(sm.bf[0]), scb = uni(sm.bf[1]), mrow = uni(sm.bf[2]);
-        __syncthreads();
-        ++r;
-        double above = 0.0;
-        if (rtype == R_REFINE) {
-            sm.u.rf.cnt[tid] = 0u;
-            sm.u.rf.mass[tid] = 0ull;
-            __syncthreads();
-#pragma unroll
-            for (int i = 0; i < EPT; ++i) {
-                const float y = scale_r<DT>(opaque(x[i]), T, rT);
-                const uint32_t k = row_key(y, DT);
-                if (k > khi) above += (double)wexp(y, ymax);
-                else if (k >= klo) {
-                    const int j = sub_bin(y, lo, scb);
-                    // integer LDS atomics: float ones run far slower
-                    atomicAdd(&sm.u.rf.cnt[j], 1u);
-                    atomicAdd(&sm.u.rf.mass[j], (unsigned long long)__float2uint_rn(wexp(y, ymax) * 4294967296.0f));
-                }
-            }
-            above = block_sum<double>(above, sm.red);  // its barriers also order the bins
-            {
-                // into the row histogram, relative to the row max (2^-40 units)
-                const uint32_t cn = sm.u.rf.cnt[tid];
-                if (cn) {
-                    const double f = exp((double)ymax - (double)mrow) * (HIST_SCALE / 4294967296.0);
-                    __hip_atomic_fetch_add(&hist->cnt[tid], cn, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    __hip_atomic_fetch_add(&hist->mass[tid], (unsigned long long)((double)sm.u.rf.mass[tid] * f),
-                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                }
-            }
-            if (tid == 0) st_dev(&rb->above, above);
-        } else if (rtype == R_COLLECT) {
-            uint32_t mine = 0u;
-#pragma unroll
-            for (int i = 0; i < EPT; ++i) {
-                const float y = scale_r<DT>(opaque(x[i]), T, rT);
-                const uint32_t k = row_key(y, DT);
-                if (k > khi) above += (double)wexp(y, ymax);
-                else if (k >= klo) mine++;
-            }
-            uint32_t total;
-            uint32_t off = block_excl_scan<uint32_t>(mine, sm.red, &total);
-            if (tid == 0) sm.bu[4] = total ? __hip_atomic_fetch_add(&rc->wcount, total, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0u;
-            __syncthreads();
-            const uint32_t wbase = sm.bu[4];
-            if (mine) {
-#pragma unroll
-                for (int i = 0; i < EPT; ++i) {
-                    const float y = scale_r<DT>(opaque(x[i]), T, rT);
-                    const uint32_t k = row_key(y, DT);
-                    if (k <= khi && k >= klo) {
-                        const uint32_t pos = wbase + off++;
-                        if (pos < (uint32_t)WCAP) st_dev_elem(&winw[pos], k, idx_of(i));
-                    }
-                }
-            }
-            above = block_sum<double>(above, sm.red);
-            if (tid == 0) st_dev(&rb->above, above);
-        } else {  // R_EXACT: float64 weights, rare: the chunk is re-read in a rolled loop
-            double s = 0.0;
-            const double ymd = (double)ymax;
-            const int64_t cend = base + CH < V ? base + CH : V;
-            for (int64_t j = base + tid; j < cend; j += NT) {
-                const float y = scale_y<DT>(load1<DT>(rowp, j), T);
-                const double e = y == -INFINITY ? 0.0 : exp((double)y - ymd);
-                s += e;
-                if (row_key(y, DT) > khi) above += e;
-            }
-            s = block_sum<double>(s, sm.red);
-            above = block_sum<double>(above, sm.red);
-            if (tid == 0) { st_dev(&rb->S, s); st_dev(&rb->above, above); }
-        }
-        publish_barrier();
-    }
-    if (tid == 0) {
-        if (timed_out) {
-            a.out_ids[row] = -1;
-            if (a.out_status) a.out_status[row] = MIS_ROW_INTERNAL;
-        }
-        // the last workgroup to leave clears the row's control words
-        const uint32_t ex = __hip_atomic_fetch_add(&rc->exited, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (ex + 1u == (uint32_t)G) {
-            trace(a.ws, L, row, 14);
-            st_dev(&rc->arr, 0u); st_dev(&rc->round, 0u); st_dev(&rc->wcount, 0u);
-            st_dev(&rc->rtype, 0u); st_dev(&rc->nref, 0u); st_dev(&rc->exited, 0u);
-        }
-    }
 }
 
 // ------------------------------------------------------------------ the row pass
 
-// fp32 top-p row after its rounds: draw from the per-chunk kept weights, or
-// re-read the row when the rounds handed it over.
-template <int DT>
-__device__ __noinline__ void finish_topp(Smem &sm, RowCx &c, const RowPlan &pl, const RoundBuf *rbf, RowOut *ro,
-                                         const Args &a, int32_t outcome)
+// LDS of the row pass beyond Smem: the fine histogram of an fp32 top-p row
+constexpr int FB2 = 2048;          // fine bins over a band
+struct FineSmem {
+    uint32_t cnt[FB2];
+    unsigned long long mass[FB2];  // weights relative to the row max, 2^-32 units;
+                                   // read back in place as doubles
+};
+
+// Reads the whole row with UNROLL 16-byte loads in flight per thread and
+// calls f(j, x) for every element with x >= xfloor (a 16-byte group below it
+// costs one max and one compare); after each chunk's elements it calls
+// g(chunk) with all threads (per-chunk reductions hang off g).  A chunk is
+// ept / VEC loads per thread, a power of two.  Indices are 32-bit (V <= 2^30).
+template <int DT, int UNROLL, class F, class Gf>
+__device__ __forceinline__ void sweep_row(const RowCx &c, float xfloor, F &&f, Gf &&g)
 {
-    const float m = ro->m;
-    c.m = m;
-    const double md = (double)m;
-    if (outcome == TP_INVALID) {
-        write_row(ro, a, c.row, -1, MIS_ROW_INVALID, pl.mode, m, 0u, 0, 0.0);
-    } else if (outcome == TP_REREAD) {
-        final_generic<DT>(sm, c, pl, ro, a);
-    } else if (outcome == TP_CUT) {
-        const uint32_t cut_key = ro->cut_key;
-        const int32_t cut_i = ro->cut_i;
-        for (int g = threadIdx.x; g < c.G; g += NT) sm.cw[g] = rbf[g].kept;
-        int gsel;
-        double resid, SK;
-        pick_chunk(sm, c.G, pl.u, &gsel, &resid, &SK);
-        int64_t id = -1;
-        if (gsel >= 0) {
-            const float T = pl.T;
-            id = draw_in_chunk<DT>(sm, c, gsel, resid, [&](float xv, int64_t j) -> double {
-                const float y = scale_y<DT>(xv, T);
-                return (y != -INFINITY && kept_by_cut(row_key(y, DT), j, cut_key, cut_i)) ? exp((double)y - md) : 0.0;
-            });
+    constexpr int VEC = Traits<DT>::VEC;
+    const int CH = (int)c.CH, V = (int)c.V;
+    const int per_chunk = CH / (NT * VEC);
+    const int sh = __builtin_ctz((unsigned)per_chunk);
+    const int total = c.G * per_chunk;  // loads per thread over the row
+    const bool vec_ok = c.vec_ok != 0;
+    const char *rowp = c.rowp;
+    for (int base = 0; base < total; base += UNROLL) {
+        float xs[UNROLL][VEC];
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u) {
+            const int fl = base + u, gq = fl >> sh, v = fl & (per_chunk - 1);
+            const int j0 = gq * CH + (v * NT + (int)threadIdx.x) * VEC;
+            if (fl < total && vec_ok && j0 + VEC <= V) {
+                loadvec<DT>(rowp, j0, xs[u]);
+            } else {
+#pragma unroll
+                for (int e = 0; e < VEC; ++e) xs[u][e] = (fl < total && j0 + e < V) ? load1<DT>(rowp, j0 + e) : -INFINITY;
+            }
         }
-        write_row(ro, a, c.row, id, id >= 0 ? MIS_ROW_OK : MIS_ROW_INVALID, pl.mode, m, cut_key, cut_i, SK);
-    } else {  // the rounds did not finish (a bounded wait expired)
-        write_row(ro, a, c.row, -1, MIS_ROW_INTERNAL, pl.mode, m, 0u, 0, 0.0);
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u) {
+            const int fl = base + u, gq = fl >> sh, v = fl & (per_chunk - 1);
+            const int j0 = gq * CH + (v * NT + (int)threadIdx.x) * VEC;
+            if (fl < total) {
+                float mx = xs[u][0];
+#pragma unroll
+                for (int e = 1; e < VEC; ++e) mx = fmaxf(mx, xs[u][e]);
+                if (mx >= xfloor) {
+#pragma unroll
+                    for (int e = 0; e < VEC; ++e)
+                        if (xs[u][e] >= xfloor && j0 + e < V) f(j0 + e, xs[u][e]);
+                }
+                if (v == per_chunk - 1) g(gq);
+            }
+        }
     }
 }
 
-// One workgroup per row: merges the chunk summaries and finishes the row
-// (greedy, temperature, small top-k), draws for fp32 top-p rows whose cut the
-// rounds resolved, and re-reads the row for everything else.
+// An fp32 top-p row, by one workgroup, from the chunk pass's S (float64) and
+// coarse bins:
+//   1. A = top_p * S; the coarse bins whose cumulative mass can reach A
+//      (margin 1e-5 S over their float32 sums) give a band of keys;
+//   2. passes over the row (re-read from the Infinity Cache), each looking
+//      only at raw values from the band's floor up to the previous band's
+//      top: elements above the band add their float64 weight to their
+//      chunk's kept mass; band elements go to 2048 linear fine bins and to
+//      the survivor list.  While the band holds more than SURV_CAP elements,
+//      the fine bins narrow it (margin 1e-6 S + 2^-31 per element over the
+//      bins' float32 weights) and the next pass runs;
+//   3. the survivors' float64 weights, their sorted cut (window_resolve),
+//      its decision margin checked against the float64 error bound;
+//   4. per-chunk kept weights, the chunk holding the draw, the draw.
+// Falls back to the generic re-read path where a step does not apply.
+template <int DT>
+__device__ __forceinline__ void topp32_row(Smem &sm, FineSmem &fs, RowCx &c, const RowPlan &pl, const ChunkSum *csr,
+                                        const RoundBuf *rbf, RowOut *ro, const Args &a)
+{
+    static_assert(DT == F32, "fp32 rows only");
+    const int tid = threadIdx.x, G = c.G;
+    exp_table(sm.etab, tid);  // (row_scales' barriers publish it)
+    uint32_t bad;
+    const float m = row_scales(sm, csr, G, &bad);
+    c.m = m;
+    const double md = (double)m;
+    if (bad != 0u || m == -INFINITY) {
+        write_row(ro, a, c.row, -1, MIS_ROW_INVALID, pl.mode, m, 0u, 0, 0.0);
+        return;
+    }
+    const float T = pl.T, rT = 1.0f / pl.T;
+    // ---- 1. S and the coarse band
+    double s = 0.0;
+    for (int g = tid; g < G; g += NT) s += ldp(&rbf[g].S) * sm.chs[g];
+    const double S = block_sum<double>(s, sm.red);
+    const double A = (double)pl.top_p * S;
+    const float Ar = coarse_bin(m);
+    if (tid < CB_N) sm.v.coarse[tid] = 0.0;
+    __syncthreads();
+    for (int g = tid; g < G; g += NT) {
+        const float yg = ldp(&csr[g].ymax);
+        if (yg == -INFINITY) continue;
+        const int off = (int)(Ar - coarse_bin(yg));
+        for (int lb = 0; lb + off < CB_N; ++lb) atomicAdd(&sm.v.coarse[lb + off], ldp(&rbf[g].coarse[lb]) * sm.chs[g]);
+    }
+    __syncthreads();
+    if (tid == 0) {
+        const double delta = 1e-5 * S;
+        double cum = 0.0;
+        int ba = -1, bb = -1;
+        for (int b = 0; b < CB_N; ++b) {
+            const double nx = cum + sm.v.coarse[b];
+            if (nx >= A - delta && cum <= A + delta) { if (ba < 0) ba = b; bb = b; }
+            cum = nx;
+        }
+        sm.bi[0] = ba; sm.bi[1] = bb;
+    }
+    __syncthreads();
+    const int ba = sm.bi[0], bb = sm.bi[1];
+    __syncthreads();
+    if (ba < 0) { trace(a.ws, a.L, c.row, 21); final_generic<DT>(sm, c, pl, ro, a); return; }  // the cut lies below the coarse range
+    trace(a.ws, a.L, c.row, 17);
+    uint32_t klo, khi;
+    {
+        const float cb_lo = Ar - (float)bb, cb_hi = Ar - (float)ba;
+        if (wave_id() == 0) {
+            const uint32_t kfin = row_key(-INFINITY, DT) + 1u, ktop = 0xff7fffffu;  // finite keys
+            const uint32_t k0 = key_search(kfin, ktop, [&](uint32_t k) { return coarse_bin(f32_of_key(k)) >= cb_lo; });
+            const uint32_t k1 = key_search(kfin, ktop, [&](uint32_t k) { return coarse_bin(f32_of_key(k)) > cb_hi; }) - 1u;
+            if (lane_id() == 0) { sm.bu[5] = k0; sm.bu[6] = k1; }
+        }
+        __syncthreads();
+        klo = sm.bu[5]; khi = sm.bu[6];
+        __syncthreads();
+    }
+    // ---- 2. passes: kept mass above the band per chunk, the band's fine bins
+    for (int g = tid; g < G; g += NT) sm.cw[g] = 0.0;
+    uint32_t xprev = 0xff800000u;  // raw key of +inf: nothing counted yet
+    uint32_t nband = 0xffffffffu;
+    for (int it = 0; it < 3; ++it) {
+        uint32_t xlo, xhi;
+        x_interval<DT>(sm, klo, khi, T, &xlo, &xhi);
+        if (it == 0) trace(a.ws, a.L, c.row, 25);
+        const float lo = f32_of_key(klo), hi = f32_of_key(khi);
+        const float scf = hi > lo ? (float)FB2 / (hi - lo) : 0.0f;
+        for (int j = tid; j < FB2; j += NT) { fs.cnt[j] = 0u; fs.mass[j] = 0ull; }
+        if (tid == 0) sm.bu[3] = 0u;
+        __syncthreads();
+        if (it == 0) trace(a.ws, a.L, c.row, 26);
+        double acc = 0.0;
+        // raw-value bounds: x >= xlof <=> key(x / T) >= klo, x <= xhif <=> key(x / T) <= khi
+        const float xlof = f32_of_key(xlo), xhif = f32_of_key(xhi), xprevf = f32_of_key(xprev);
+        sweep_row<DT, 32>(c, xlof, [&](int j, float x) {
+            if (!(x <= xprevf)) return;  // counted by an earlier pass
+            const float y = scale_r<DT>(x, T, rT);
+            if (x > xhif) { acc += dexp((double)y - md, sm.etab); return; }
+            const int b = (int)fminf(fmaxf(floorf((y - lo) * scf), 0.0f), (float)(FB2 - 1));
+            atomicAdd(&fs.cnt[b], 1u);
+            atomicAdd(&fs.mass[b], (unsigned long long)__float2uint_rn(wexp(y, m) * 2147483648.0f));
+            // survivor list: one LDS atomic per wave
+            const uint64_t mk = __ballot(1);
+            const int lead = __builtin_ctzll(mk);
+            uint32_t base = 0u;
+            if (lane_id() == lead) base = atomicAdd(&sm.bu[3], (uint32_t)__popcll(mk));
+            base = (uint32_t)__shfl((int)base, lead, 64);
+            const uint32_t q = base + (uint32_t)__popcll(mk & ((1ull << lane_id()) - 1ull));
+            if (q < (uint32_t)SURV_CAP) { sm.u.s.key[q] = row_key(y, DT); sm.u.s.idx[q] = (int32_t)j; }
+        }, [&](int gq) {
+            const double w = wave_sum(acc);
+            if (lane_id() == 0 && w != 0.0) atomicAdd(&sm.cw[gq], w);
+            acc = 0.0;
+        });
+        __syncthreads();
+        nband = sm.bu[3];
+        xprev = xhi;
+        trace(a.ws, a.L, c.row, 18 + it);
+        if (nband <= (uint32_t)SURV_CAP || !(hi > lo) || it == 2) break;
+        // narrow: fine bins (descending y) whose cumulative mass interval meets [A - delta, A + delta]
+        double ab = 0.0;
+        for (int g = tid; g < G; g += NT) ab += sm.cw[g];
+        const double above = block_sum<double>(ab, sm.red);
+        double *dmass = reinterpret_cast<double *>(fs.mass);  // the sums as doubles, in place
+        for (int j = tid; j < FB2; j += NT) dmass[j] = (double)fs.mass[j] * (1.0 / 2147483648.0);
+        __syncthreads();
+        if (wave_id() == 0) {
+            const double delta = 1e-6 * S + (double)nband * 4.7e-10;
+            double tmp;
+            const int jb = wave_find_desc<double>(dmass, FB2, A - delta - above, &tmp);
+            const int ja = wave_find_desc<double>(dmass, FB2, A + delta - above, &tmp);
+            uint32_t cnt = 0u;
+            for (int j = lane_id(); j < FB2; j += 64) cnt += (j >= ja && j <= jb) ? fs.cnt[j] : 0u;
+            cnt = wave_sum(cnt);
+            if (lane_id() == 0) { sm.bi[0] = (ja <= jb && cnt > 0u) ? ja : -1; sm.bi[1] = jb; }
+        }
+        __syncthreads();
+        const int ja = sm.bi[0], jb = sm.bi[1];
+        __syncthreads();
+        if (ja < 0) break;  // (caught below: nband > SURV_CAP)
+        if (wave_id() == 0) {
+            auto jof = [&](uint32_t k) -> int { return (int)fminf(fmaxf(floorf((f32_of_key(k) - lo) * scf), 0.0f), (float)(FB2 - 1)); };
+            const uint32_t k0 = key_search(klo, khi, [&](uint32_t k) { return jof(k) >= ja; });
+            const uint32_t k1 = key_search(klo, khi, [&](uint32_t k) { return jof(k) > jb; }) - 1u;
+            if (lane_id() == 0) { sm.bu[5] = k0; sm.bu[6] = k1; }
+        }
+        __syncthreads();
+        klo = sm.bu[5]; khi = sm.bu[6];
+        __syncthreads();
+    }
+    if (nband > (uint32_t)SURV_CAP || nband == 0u) { trace(a.ws, a.L, c.row, 22); final_generic<DT>(sm, c, pl, ro, a); return; }
+    // ---- 3. the survivors' float64 weights and the cut
+    for (int q = tid; q < (int)nband; q += NT) sm.u.s.e[q] = dexp((double)f32_of_key(sm.u.s.key[q]) - md, sm.etab);
+    double ab = 0.0;
+    for (int g = tid; g < G; g += NT) ab += sm.cw[g];
+    const double above = block_sum<double>(ab, sm.red);  // (its barriers publish the weights)
+    uint32_t cut_key = 0u;
+    int32_t cut_i = 0;
+    double ql = 0.0, wl = 0.0;
+    const int rl = window_resolve(sm, nband, above, A, &cut_key, &cut_i, &ql, &wl);
+    // S, the mass above and the survivors' weights carry relative errors below
+    // 1e-15 each (dexp) plus float64 summation rounding over at most 2^30 terms
+    const double err = 1e-12 * (above + A) + 1e-300;
+    if (!(rl >= 0 && (A - ql) > err && (ql + wl - A) > err)) { trace(a.ws, a.L, c.row, 23); final_generic<DT>(sm, c, pl, ro, a); return; }
+    trace(a.ws, a.L, c.row, 24);
+    // ---- 4. per-chunk kept weights (above the window + its kept prefix), the draw
+    for (int q = tid; q <= rl; q += NT) {
+        const int32_t j = (int32_t)(0xffffffffu - (uint32_t)sm.u.so.k[q]);
+        atomicAdd(&sm.cw[(int)(j / c.CH)], sm.u.so.e[q]);
+    }
+    int gsel;
+    double resid, SK;
+    pick_chunk(sm, G, pl.u, &gsel, &resid, &SK);
+    int64_t id = -1;
+    if (gsel >= 0) {
+        id = draw_in_chunk<DT>(sm, c, gsel, resid, [&](float xv, int64_t j) -> double {
+            const float y = scale_y<DT>(xv, T);
+            return (y != -INFINITY && kept_by_cut(row_key(y, DT), j, cut_key, cut_i)) ? exp((double)y - md) : 0.0;
+        });
+    }
+    write_row(ro, a, c.row, id, id >= 0 ? MIS_ROW_OK : MIS_ROW_INVALID, pl.mode, m, cut_key, cut_i, SK);
+}
+
+// One workgroup per row: merges the chunk summaries and finishes the row:
+// greedy, temperature, small top-k from the summaries; fp32 top-p from the
+// coarse bins and re-reads of the row; the generic re-read path otherwise.
 template <int DT>
 __global__ __launch_bounds__(NT) void k_final(Args a)
 {
     __shared__ Smem sm;
+    __shared__ FineSmem fs;
     const Layout &L = a.L;
     const int row = blockIdx.x;
     RowOut *ro = reinterpret_cast<RowOut *>(a.ws + L.rowout) + row;
@@ -1980,20 +1703,13 @@ __global__ __launch_bounds__(NT) void k_final(Args a)
         c.V = a.V; c.vec_ok = a.vec_ok; c.m = 0.0f; c.G = L.G; c.CH = (int64_t)NT * L.ept; c.row = row;
         sm.pl = plan_row(a.params[row], a.V);
         c.T = sm.pl.T;
-        sm.bi[6] = ro->topp;
     }
-    __syncthreads();
-    const int32_t outcome = sm.bi[6];
     trace(a.ws, L, row, 16);
     __syncthreads();
     const ChunkSum *csr = reinterpret_cast<const ChunkSum *>(a.ws + L.chunks) + (size_t)row * L.G;
     const RoundBuf *rbf = reinterpret_cast<const RoundBuf *>(a.ws + L.rbuf) + (size_t)row * L.G;
-    if (DT == F32 && sm.pl.mode == M_TOPP) {
-        finish_topp<DT>(sm, sm.cx, sm.pl, rbf, ro, sm.args, outcome);
-        if (threadIdx.x == 0) ro->topp = TP_NONE;
-    } else {
-        leader_row<DT>(sm, sm.cx, sm.pl, csr, ro, sm.args);
-    }
+    if (DT == F32 && sm.pl.mode == M_TOPP) topp32_row<F32>(sm, fs, sm.cx, sm.pl, csr, rbf, ro, sm.args);
+    else leader_row<DT>(sm, sm.cx, sm.pl, csr, ro, sm.args);
     trace(a.ws, L, row, 31);
 }
 
@@ -2058,7 +1774,6 @@ static hipError_t launch_dt(const Args &a, float *probs, uint32_t *keep, hipStre
     if (ev && (e = hipEventRecord((hipEvent_t)ev[0], st)) != hipSuccess) return e;
     switch (a.L.ept) {
     case 64: e = launch_sample<DT, 64>(a, st); break;
-    case 32: e = launch_sample<DT, 32>(a, st); break;
     default: e = launch_sample<DT, 16>(a, st); break;
     }
     if (e != hipSuccess) return e;
@@ -2104,7 +1819,7 @@ static int sample_impl(const void *logits, int dtype, int64_t B, int64_t V, int6
     if (dtype < 0 || dtype > 2 || B < 0 || V <= 0 || row_stride < V) return MIS_ERR_INVALID_ARG;
     if (B == 0) return MIS_OK;
     if (!logits || !params || !out_ids || !workspace) return MIS_ERR_INVALID_ARG;
-    if (V > (int64_t)1 << 30 || B > B_MAX) return MIS_ERR_UNSUPPORTED;
+    if (V > (int64_t)1 << 30 || B > 0x7fffffff) return MIS_ERR_UNSUPPORTED;
     const Layout L = make_layout(B, V, dtype);
     if (L.G > G_MAX || (int64_t)L.B * L.G > 0x7fffffff) return MIS_ERR_UNSUPPORTED;
     if (workspace_bytes < L.total || ((uintptr_t)workspace & 255u) != 0) return MIS_ERR_WORKSPACE;

@@ -91,8 +91,8 @@ class Sampler:
         ws = self._workspace.get(idx)
         if ws is None or ws.numel() < need:
             ws = torch.empty(need, dtype=torch.uint8, device=device)
-            # the kernels keep per-row arrival counters at the start of the
-            # workspace; they must start at zero and every call leaves them so
+            # the kernels keep no state in it between calls; the init call is
+            # part of the ABI contract and cheap
             _native.workspace_init(ws.data_ptr(), ws.numel(), torch.cuda.current_stream(device).cuda_stream)
             self._workspace[idx] = ws
         return ws
