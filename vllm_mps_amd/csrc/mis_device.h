@@ -159,8 +159,10 @@ template <class T> __device__ __forceinline__ T wave_incl_scan(T v)
     return v;
 }
 
-// LDS scratch for the block reductions: NWAVE + 1 slots of 8 bytes
-struct Red { double d[NWAVE + 1]; int64_t l[NWAVE + 1]; uint32_t u[NWAVE + 1]; float f[NWAVE + 1]; };
+// LDS scratch for the block reductions of up to 16 waves (1024 threads);
+// the helpers take the block's wave count NW as a template argument
+constexpr int NWAVE_MAX = 16;
+struct Red { double d[NWAVE_MAX + 1]; int64_t l[NWAVE_MAX + 1]; uint32_t u[NWAVE_MAX + 1]; float f[NWAVE_MAX + 1]; };
 
 template <class T> __device__ __forceinline__ T *red_of(Red &r);
 template <> __device__ __forceinline__ double *red_of<double>(Red &r) { return r.d; }
@@ -168,7 +170,7 @@ template <> __device__ __forceinline__ int64_t *red_of<int64_t>(Red &r) { return
 template <> __device__ __forceinline__ uint32_t *red_of<uint32_t>(Red &r) { return r.u; }
 template <> __device__ __forceinline__ float *red_of<float>(Red &r) { return r.f; }
 
-template <class T> __device__ __forceinline__ T block_excl_scan(T v, Red &rr, T *total)
+template <class T, int NW = NWAVE> __device__ __forceinline__ T block_excl_scan(T v, Red &rr, T *total)
 {
     T *red = red_of<T>(rr);
     const T inc = wave_incl_scan(v);
@@ -176,45 +178,45 @@ template <class T> __device__ __forceinline__ T block_excl_scan(T v, Red &rr, T 
     __syncthreads();
     if (threadIdx.x == 0) {
         T run = T(0);
-        for (int w = 0; w < NWAVE; ++w) { const T t = red[w]; red[w] = run; run += t; }
-        red[NWAVE] = run;
+        for (int w = 0; w < NW; ++w) { const T t = red[w]; red[w] = run; run += t; }
+        red[NW] = run;
     }
     __syncthreads();
     const T res = inc - v + red[wave_id()];
-    *total = red[NWAVE];
+    *total = red[NW];
     __syncthreads();
     return res;
 }
-template <class T> __device__ __forceinline__ T block_sum(T v, Red &rr)
+template <class T, int NW = NWAVE> __device__ __forceinline__ T block_sum(T v, Red &rr)
 {
     T *red = red_of<T>(rr);
     v = wave_sum(v);
     if (lane_id() == 0) red[wave_id()] = v;
     __syncthreads();
     T t = T(0);
-    for (int w = 0; w < NWAVE; ++w) t += red[w];
+    for (int w = 0; w < NW; ++w) t += red[w];
     __syncthreads();
     return t;
 }
-template <class T> __device__ __forceinline__ T block_max(T v, Red &rr)
+template <class T, int NW = NWAVE> __device__ __forceinline__ T block_max(T v, Red &rr)
 {
     T *red = red_of<T>(rr);
     v = wave_max(v);
     if (lane_id() == 0) red[wave_id()] = v;
     __syncthreads();
     T t = red[0];
-    for (int w = 1; w < NWAVE; ++w) t = red[w] > t ? red[w] : t;
+    for (int w = 1; w < NW; ++w) t = red[w] > t ? red[w] : t;
     __syncthreads();
     return t;
 }
-template <class T> __device__ __forceinline__ T block_min(T v, Red &rr)
+template <class T, int NW = NWAVE> __device__ __forceinline__ T block_min(T v, Red &rr)
 {
     T *red = red_of<T>(rr);
     v = wave_min(v);
     if (lane_id() == 0) red[wave_id()] = v;
     __syncthreads();
     T t = red[0];
-    for (int w = 1; w < NWAVE; ++w) t = red[w] < t ? red[w] : t;
+    for (int w = 1; w < NW; ++w) t = red[w] < t ? red[w] : t;
     __syncthreads();
     return t;
 }
@@ -320,28 +322,76 @@ __device__ __forceinline__ int wave_find_asc(const double *v, int n, double targ
 // Bitonic sort, descending, of n <= cap (u64 key, f64 value) pairs in LDS by
 // all threads of the block; entries n .. pow2(n)-1 are padded with key 0, so
 // the arrays must hold pow2(n) entries.
+// Bitonic sort, descending, of k[0..n) with payload e (n <= CAP; CAP and the
+// block size NTH powers of two).  Padding keys are 0, so every real key must
+// be > 0.  Element i sits in thread i / PT (PT = CAP / NTH, at most 4) at
+// register slot i % PT: compare-exchanges between slots of one thread work on
+// registers, between lanes of one wave on shuffles, and only partners in
+// other waves go through LDS (k and e, CAP entries each).
+template <int NTH, int CAP>
 __device__ __forceinline__ void block_sort_desc(uint64_t *k, double *e, int n)
 {
+    constexpr int PT = CAP / NTH;
+    static_assert(PT == 1 || PT == 2 || PT == 4, "1, 2 or 4 elements per thread");
+    const int tid = threadIdx.x;
     int npow = 1;
     while (npow < n) npow <<= 1;
-    for (int i = n + (int)threadIdx.x; i < npow; i += NT) { k[i] = 0ull; e[i] = 0.0; }
-    __syncthreads();
+    uint64_t kv[PT];
+    double ev[PT];
+#pragma unroll
+    for (int r = 0; r < PT; ++r) {
+        const int i = tid * PT + r;
+        kv[r] = i < n ? k[i] : 0ull;
+        ev[r] = i < n ? e[i] : 0.0;
+    }
+    // the pair (r, r + jj) of one thread, stage (kk, jj)
+    auto cx = [&](int r, int p, int kk) {
+        const int i = tid * PT + r;
+        const bool desc = (i & kk) == 0;
+        if (desc ? (kv[r] < kv[p]) : (kv[r] > kv[p])) {
+            const uint64_t tk = kv[r]; kv[r] = kv[p]; kv[p] = tk;
+            const double te = ev[r]; ev[r] = ev[p]; ev[p] = te;
+        }
+    };
     for (int kk = 2; kk <= npow; kk <<= 1) {
         for (int j = kk >> 1; j > 0; j >>= 1) {
-            for (int i = threadIdx.x; i < npow; i += NT) {
-                const int ixj = i ^ j;
-                if (ixj > i) {
-                    const bool desc = (i & kk) == 0;
-                    const uint64_t a = k[i], b = k[ixj];
-                    if (desc ? (a < b) : (a > b)) {
-                        k[i] = b; k[ixj] = a;
-                        const double t = e[i]; e[i] = e[ixj]; e[ixj] = t;
-                    }
+            if (j < PT) {
+                if constexpr (PT == 2) {
+                    cx(0, 1, kk);
+                } else if constexpr (PT == 4) {
+                    if (j == 1) { cx(0, 1, kk); cx(2, 3, kk); }
+                    else { cx(0, 2, kk); cx(1, 3, kk); }
+                }
+            } else if (j < PT * 64) {
+                const int lm = j / PT;
+#pragma unroll
+                for (int r = 0; r < PT; ++r) {
+                    const int i = tid * PT + r;
+                    const uint64_t k2 = __shfl_xor(kv[r], lm, 64);
+                    const double e2 = __shfl_xor(ev[r], lm, 64);
+                    const bool take_max = ((i & j) == 0) == ((i & kk) == 0);
+                    if (take_max ? (k2 > kv[r]) : (k2 < kv[r])) { kv[r] = k2; ev[r] = e2; }
+                }
+            } else {
+                __syncthreads();
+#pragma unroll
+                for (int r = 0; r < PT; ++r) { k[tid * PT + r] = kv[r]; e[tid * PT + r] = ev[r]; }
+                __syncthreads();
+#pragma unroll
+                for (int r = 0; r < PT; ++r) {
+                    const int i = tid * PT + r;
+                    const uint64_t k2 = k[i ^ j];
+                    const double e2 = e[i ^ j];
+                    const bool take_max = ((i & j) == 0) == ((i & kk) == 0);
+                    if (take_max ? (k2 > kv[r]) : (k2 < kv[r])) { kv[r] = k2; ev[r] = e2; }
                 }
             }
-            __syncthreads();
         }
     }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < PT; ++r) { k[tid * PT + r] = kv[r]; e[tid * PT + r] = ev[r]; }
+    __syncthreads();
 }
 
 // ------------------------------------------------------------------ raw-key intervals

@@ -106,10 +106,36 @@ struct RowOut {                 // 64 B per row, read by k_emit
 struct Cand { float x; int32_t idx; };
 struct Elem { uint32_t key; int32_t idx; };
 
+// fp32 top-p passes (k_tp_*): per (row, chunk) fine bins over the row's
+// coarse band, per row the band keys, per-chunk kept masses and survivors
+constexpr int FH = 512;             // fine bins per chunk over the coarse band
+constexpr double FIX_ONE = 1099511627776.0;  // 2^40: fine-bin masses as integers of exp(y - m)
+struct TopChunk {
+    double above;                   // float64 mass of the chunk's elements above the coarse band
+    double pad[31];
+    uint32_t cnt[FH];
+    unsigned long long mass[FH];
+};
+static_assert(sizeof(TopChunk) % 256 == 0, "TopChunk size");
+enum : uint32_t { TR_ACTIVE = 1, TR_DEFER = 2 };
+struct TopRow {
+    uint32_t status, count;         // TR_*; survivors appended by the collect pass
+    uint32_t klo, khi;              // coarse band (row keys)
+    uint32_t xlo, xhi;              // its raw-key interval
+    uint32_t klo2, khi2;            // final band (row keys)
+    uint32_t xlo2, xhi2;            // its raw-key interval
+    float m, lo, scf, pad0;         // row max of y; fine-bin grid y -> (y - lo) * scf
+    double S, A, fix_err;           // sum of exp(y - m), top_p * S, bound of the fixed-point sums
+    double pad[22];
+    double cw[G_MAX];               // per-chunk kept mass above the final band
+    Elem list[SURV_CAP];            // the final band's elements
+};
+static_assert(sizeof(TopRow) % 256 == 0, "TopRow size");
+
 struct Layout {
     int64_t B, V;
     int ept, G;
-    size_t rowout, chunks, rbuf, cand, total;
+    size_t rowout, chunks, rbuf, cand, topc, topr, total;
 };
 
 static inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -122,7 +148,6 @@ static Layout make_layout(int64_t B, int64_t V, int dtype)
     Layout L;
     L.B = B; L.V = V;
     auto chunks = [&](int ept) { return (V + (int64_t)NT * ept - 1) / ((int64_t)NT * ept); };
-    (void)dtype;
     L.ept = 16;
     if (chunks(L.ept) > G_MAX) L.ept = 64;
     L.G = (int)chunks(L.ept);
@@ -132,6 +157,10 @@ static Layout make_layout(int64_t B, int64_t V, int dtype)
     L.chunks = off; off = align256(off + sizeof(ChunkSum) * BG);
     L.rbuf = off;   off = align256(off + sizeof(RoundBuf) * BG);
     L.cand = off;   off = align256(off + sizeof(Cand) * (size_t)CAND_CAP * BG);
+    // fp32 top-p: per-chunk fine bins and per-row state of the top-p passes
+    const bool f32 = dtype == MIS_DTYPE_F32;
+    L.topc = off;   off = align256(off + (f32 ? sizeof(TopChunk) * BG : 0));
+    L.topr = off;   off = align256(off + (f32 ? sizeof(TopRow) * (size_t)B : 0));
     L.total = off;
     return L;
 }
@@ -313,16 +342,16 @@ __device__ __forceinline__ void write_row(RowOut *ro, const Args &a, int row, in
 // Inverse CDF inside chunk g: the first kept index whose running weight (index
 // order) exceeds `resid`; wfun(x, j) gives the weight (0 = not kept).  When
 // rounding leaves `resid` out of reach, the chunk's last kept index.
-template <int DT, class WF>
+template <int DT, int NTH = NT, class WF>
 __device__ __forceinline__ int64_t draw_in_chunk(Smem &sm, const RowCx &c, int g, double resid, WF &&wfun)
 {
     // Thread t takes the contiguous elements [cbeg + t*per, cbeg + (t+1)*per)
     // of the chunk, loaded up front (16-byte vectors where aligned), so the
     // weights are computed from registers in both passes.
-    constexpr int VEC = Traits<DT>::VEC, MAXPER = 64;
+    constexpr int VEC = Traits<DT>::VEC, MAXPER = 64 * NT / NTH;  // elements per thread, at most
     const int64_t cbeg = (int64_t)g * c.CH;
     const int64_t cend = cbeg + c.CH < c.V ? cbeg + c.CH : c.V;
-    const int per = (int)(c.CH / NT);  // 8..64, a multiple of VEC
+    const int per = (int)(c.CH / NTH);  // 8..64, a multiple of VEC
     const int64_t jb = cbeg + (int64_t)threadIdx.x * per;
     float xs[MAXPER];
 #pragma unroll
@@ -347,7 +376,7 @@ __device__ __forceinline__ int64_t draw_in_chunk(Smem &sm, const RowCx &c, int g
         }
     }
     double tot;
-    const double before = block_excl_scan<double>(local, sm.red, &tot);
+    const double before = block_excl_scan<double, NTH / 64>(local, sm.red, &tot);
     if (threadIdx.x == 0) sm.bq[0] = 0xffffffffffffffffull;
     __syncthreads();
     if (local > 0.0 && before <= resid && resid < before + local) {
@@ -370,7 +399,7 @@ __device__ __forceinline__ int64_t draw_in_chunk(Smem &sm, const RowCx &c, int g
     const unsigned long long pk = sm.bq[0];
     __syncthreads();
     if (pk != 0xffffffffffffffffull) return (int64_t)pk;
-    return block_max<int64_t>(lastk, sm.red);
+    return block_max<int64_t, NTH / 64>(lastk, sm.red);
 }
 
 // Chunk holding u * sum(sm.cw) and the residual weight inside it.
@@ -757,31 +786,32 @@ __device__ __forceinline__ void final_generic(Smem &sm, const RowCx &c, const Ro
 // key << 32 | ~idx, mass); the last kept element is found by a block scan.
 // Returns its sorted position, or -1 when the cut is not inside the window.
 // *q_last = mass before the last kept element, *w_last = its weight.
+template <int NTH = NT>
 __device__ __forceinline__ int window_resolve(Smem &sm, uint32_t n, double above, double A, uint32_t *cut_key, int32_t *cut_i,
                               double *q_last, double *w_last)
 {
-    constexpr int PT = SURV_CAP / NT;
+    constexpr int PT = SURV_CAP / NTH;
     const int tid = threadIdx.x;
     uint64_t kt[PT];
     double et[PT];
 #pragma unroll
     for (int q = 0; q < PT; ++q) {
-        const int i = q * NT + tid;
+        const int i = q * NTH + tid;
         const bool in = i < (int)n;
         kt[q] = in ? (((uint64_t)sm.u.s.key[i] << 32) | (uint64_t)(0xffffffffu - (uint32_t)sm.u.s.idx[i])) : 0ull;
         et[q] = in ? sm.u.s.e[i] : 0.0;
     }
     __syncthreads();
 #pragma unroll
-    for (int q = 0; q < PT; ++q) { sm.u.so.k[q * NT + tid] = kt[q]; sm.u.so.e[q * NT + tid] = et[q]; }
+    for (int q = 0; q < PT; ++q) { sm.u.so.k[q * NTH + tid] = kt[q]; sm.u.so.e[q * NTH + tid] = et[q]; }
     __syncthreads();
-    block_sort_desc(sm.u.so.k, sm.u.so.e, (int)n);
+    block_sort_desc<NTH, SURV_CAP>(sm.u.so.k, sm.u.so.e, (int)n);
     // thread t scans the sorted positions [t*PT, t*PT + PT)
     double local = 0.0;
 #pragma unroll
     for (int q = 0; q < PT; ++q) { const int r = tid * PT + q; local += r < (int)n ? sm.u.so.e[r] : 0.0; }
     double tot;
-    const double off = block_excl_scan<double>(local, sm.red, &tot);
+    const double off = block_excl_scan<double, NTH / 64>(local, sm.red, &tot);
     if (tid == 0) { sm.bi[4] = -1; }
     __syncthreads();
     double run = above + off;
@@ -916,7 +946,7 @@ __device__ __forceinline__ bool leader_smallk(Smem &sm, const RowCx &c, const Ro
             __syncthreads();
             const int nb = (int)min(sm.bu[3], (uint32_t)SURV_CAP);
             __syncthreads();
-            block_sort_desc(sm.u.so.k, sm.u.so.e, nb);
+            block_sort_desc<NT, SURV_CAP>(sm.u.so.k, sm.u.so.e, nb);
             xk_thr = (uint32_t)sm.u.so.k[(int)((uint32_t)pl.kk - above) - 1];
             __syncthreads();
         }
@@ -997,8 +1027,6 @@ __device__ __forceinline__ bool leader_smallk(Smem &sm, const RowCx &c, const Ro
             __syncthreads();
         } else {
             // 16-bit rounding chain over the survivors in stable descending order
-            int npow = 1;
-            while (npow < (int)ns) npow <<= 1;
             constexpr int PT = SURV_CAP / NT;
             uint64_t kt[PT];
             double et[PT];
@@ -1015,22 +1043,7 @@ __device__ __forceinline__ bool leader_smallk(Smem &sm, const RowCx &c, const Ro
                 sm.u.so.e[i] = et[q];
             }
             __syncthreads();
-            for (int kk = 2; kk <= npow; kk <<= 1) {      // bitonic sort, descending
-                for (int j = kk >> 1; j > 0; j >>= 1) {
-                    for (int i = threadIdx.x; i < npow; i += NT) {
-                        const int ixj = i ^ j;
-                        if (ixj > i) {
-                            const bool desc = (i & kk) == 0;
-                            const uint64_t x = sm.u.so.k[i], y = sm.u.so.k[ixj];
-                            if (desc ? (x < y) : (x > y)) {
-                                sm.u.so.k[i] = y; sm.u.so.k[ixj] = x;
-                                const double t = sm.u.so.e[i]; sm.u.so.e[i] = sm.u.so.e[ixj]; sm.u.so.e[ixj] = t;
-                            }
-                        }
-                    }
-                    __syncthreads();
-                }
-            }
+            block_sort_desc<NT, SURV_CAP>(sm.u.so.k, sm.u.so.e, (int)ns);
             if (threadIdx.x == 0) {
                 const float thr16 = rn_dtype(pl.top_p, DT);
                 float F = 0.0f;
@@ -1199,21 +1212,22 @@ __device__ __forceinline__ void leader_row(Smem &sm, RowCx &c, const RowPlan &pl
 // Per-chunk scale factors exp(ymax_c - m) into sm.chs; returns the row max m
 // and whether any chunk flagged NaN / +inf.  One load pair per chunk and
 // thread, issued together.
+template <int NTH = NT>
 __device__ __forceinline__ float row_scales(Smem &sm, const ChunkSum *csr, int G, uint32_t *bad)
 {
     uint32_t anyflag = 0u;
     float m = -INFINITY;
-    for (int g = threadIdx.x; g < G; g += NT) {
+    for (int g = threadIdx.x; g < G; g += NTH) {
         const uint32_t f = ldp(&csr[g].flags);
         const float yg = ldp(&csr[g].ymax);
         anyflag |= f;
         m = fmaxf(m, yg);
         sm.chs[g] = (double)yg;
     }
-    anyflag = block_sum<uint32_t>(anyflag ? 1u : 0u, sm.red);
-    m = block_max<float>(m, sm.red);
+    anyflag = block_sum<uint32_t, NTH / 64>(anyflag ? 1u : 0u, sm.red);
+    m = block_max<float, NTH / 64>(m, sm.red);
     const double md = (double)m;
-    for (int g = threadIdx.x; g < G; g += NT) {
+    for (int g = threadIdx.x; g < G; g += NTH) {
         const double yg = sm.chs[g];
         sm.chs[g] = (yg == -INFINITY || m == -INFINITY) ? 0.0 : exp(yg - md);
     }
@@ -1449,93 +1463,62 @@ __global__ __launch_bounds__(NT) void k_sample(Args a)
 
 // ------------------------------------------------------------------ the row pass
 
-// LDS of the row pass beyond Smem: the fine histogram of an fp32 top-p row
-constexpr int FB2 = 2048;          // fine bins over a band
-struct FineSmem {
-    uint32_t cnt[FB2];
-    unsigned long long mass[FB2];  // weights relative to the row max, 2^-32 units;
-                                   // read back in place as doubles
-};
+// ------------------------------------------------------------------ fp32 top-p rows
+//
+// Five launches spread an fp32 top-p row over the whole GPU (the chunk pass's
+// float64 S and coarse bins come first):
+//   k_tp_prep    one workgroup per row: row max, S, A = top_p * S, the coarse
+//                band of keys whose cumulative mass can reach A (margin 1e-5 S
+//                over the float32 bin sums) and its raw-value interval;
+//   k_tp_hist    one workgroup per (row, chunk), grid-stride: re-reads the
+//                chunk (Infinity Cache); elements above the band add their
+//                float64 weight (dexp) to the chunk's above-mass, band
+//                elements go to FH linear fine bins (count, weight in 2^-40
+//                units of the row max's weight);
+//   k_tp_merge   one workgroup per row: merges the fine bins, finds the bins
+//                whose cumulative mass can hold the cut (exact to the
+//                fixed-point bound) and their keys, and each chunk's kept mass
+//                above them;
+//   k_tp_collect one workgroup per (row, chunk), grid-stride: appends the
+//                elements of that final band to the row's survivor list;
+//   k_tp_final   one workgroup per row: the survivors' float64 weights, their
+//                sorted cut (window_resolve) with its decision margin checked
+//                against the error bound, then the draw.
+// A row where a step does not apply is left to the row pass's generic path
+// (RowOut status ROW_DEFER).
 
-// Reads the whole row with UNROLL 16-byte loads in flight per thread and
-// calls f(j, x) for every element with x >= xfloor (a 16-byte group below it
-// costs one max and one compare); after each chunk's elements it calls
-// g(chunk) with all threads (per-chunk reductions hang off g).  A chunk is
-// ept / VEC loads per thread, a power of two.  Indices are 32-bit (V <= 2^30).
-template <int DT, int UNROLL, class F, class Gf>
-__device__ __forceinline__ void sweep_row(const RowCx &c, float xfloor, F &&f, Gf &&g)
+constexpr int ROW_DEFER = 16;       // RowOut status: k_final's generic path finishes the row
+constexpr int TP_GRID = 2048;       // workgroups of the grid-stride passes
+
+__device__ __forceinline__ TopRow *top_row(const Args &a, int row)
 {
-    constexpr int VEC = Traits<DT>::VEC;
-    const int CH = (int)c.CH, V = (int)c.V;
-    const int per_chunk = CH / (NT * VEC);
-    const int sh = __builtin_ctz((unsigned)per_chunk);
-    const int total = c.G * per_chunk;  // loads per thread over the row
-    const bool vec_ok = c.vec_ok != 0;
-    const char *rowp = c.rowp;
-    for (int base = 0; base < total; base += UNROLL) {
-        float xs[UNROLL][VEC];
-#pragma unroll
-        for (int u = 0; u < UNROLL; ++u) {
-            const int fl = base + u, gq = fl >> sh, v = fl & (per_chunk - 1);
-            const int j0 = gq * CH + (v * NT + (int)threadIdx.x) * VEC;
-            if (fl < total && vec_ok && j0 + VEC <= V) {
-                loadvec<DT>(rowp, j0, xs[u]);
-            } else {
-#pragma unroll
-                for (int e = 0; e < VEC; ++e) xs[u][e] = (fl < total && j0 + e < V) ? load1<DT>(rowp, j0 + e) : -INFINITY;
-            }
-        }
-#pragma unroll
-        for (int u = 0; u < UNROLL; ++u) {
-            const int fl = base + u, gq = fl >> sh, v = fl & (per_chunk - 1);
-            const int j0 = gq * CH + (v * NT + (int)threadIdx.x) * VEC;
-            if (fl < total) {
-                float mx = xs[u][0];
-#pragma unroll
-                for (int e = 1; e < VEC; ++e) mx = fmaxf(mx, xs[u][e]);
-                if (mx >= xfloor) {
-#pragma unroll
-                    for (int e = 0; e < VEC; ++e)
-                        if (xs[u][e] >= xfloor && j0 + e < V) f(j0 + e, xs[u][e]);
-                }
-                if (v == per_chunk - 1) g(gq);
-            }
-        }
-    }
+    return reinterpret_cast<TopRow *>(a.ws + a.L.topr) + row;
+}
+__device__ __forceinline__ TopChunk *top_chunk(const Args &a, int row, int g)
+{
+    return reinterpret_cast<TopChunk *>(a.ws + a.L.topc) + (size_t)row * a.L.G + g;
+}
+__device__ __forceinline__ int fine_bin(float y, float lo, float scf)
+{
+    return (int)fminf(fmaxf(floorf((y - lo) * scf), 0.0f), (float)(FH - 1));
 }
 
-// An fp32 top-p row, by one workgroup, from the chunk pass's S (float64) and
-// coarse bins:
-//   1. A = top_p * S; the coarse bins whose cumulative mass can reach A
-//      (margin 1e-5 S over their float32 sums) give a band of keys;
-//   2. passes over the row (re-read from the Infinity Cache), each looking
-//      only at raw values from the band's floor up to the previous band's
-//      top: elements above the band add their float64 weight to their
-//      chunk's kept mass; band elements go to 2048 linear fine bins and to
-//      the survivor list.  While the band holds more than SURV_CAP elements,
-//      the fine bins narrow it (margin 1e-6 S + 2^-31 per element over the
-//      bins' float32 weights) and the next pass runs;
-//   3. the survivors' float64 weights, their sorted cut (window_resolve),
-//      its decision margin checked against the float64 error bound;
-//   4. per-chunk kept weights, the chunk holding the draw, the draw.
-// Falls back to the generic re-read path where a step does not apply.
-template <int DT>
-__device__ __forceinline__ void topp32_row(Smem &sm, FineSmem &fs, RowCx &c, const RowPlan &pl, const ChunkSum *csr,
-                                        const RoundBuf *rbf, RowOut *ro, const Args &a)
+__global__ __launch_bounds__(NT) void k_tp_prep(Args a)
 {
-    static_assert(DT == F32, "fp32 rows only");
-    const int tid = threadIdx.x, G = c.G;
-    exp_table(sm.etab, tid);  // (row_scales' barriers publish it)
+    __shared__ Smem sm;
+    const Layout &L = a.L;
+    const int row = blockIdx.x, tid = threadIdx.x;
+    const RowPlan pl = plan_row(a.params[row], a.V);
+    if (pl.mode != M_TOPP) return;
+    TopRow *tr = top_row(a, row);
+    const ChunkSum *csr = reinterpret_cast<const ChunkSum *>(a.ws + L.chunks) + (size_t)row * L.G;
+    const RoundBuf *rbf = reinterpret_cast<const RoundBuf *>(a.ws + L.rbuf) + (size_t)row * L.G;
+    const int G = L.G;
+    trace(a.ws, L, row, 2);
     uint32_t bad;
     const float m = row_scales(sm, csr, G, &bad);
-    c.m = m;
-    const double md = (double)m;
-    if (bad != 0u || m == -INFINITY) {
-        write_row(ro, a, c.row, -1, MIS_ROW_INVALID, pl.mode, m, 0u, 0, 0.0);
-        return;
-    }
-    const float T = pl.T, rT = 1.0f / pl.T;
-    // ---- 1. S and the coarse band
+    trace(a.ws, L, row, 3);
+    if (bad != 0u || m == -INFINITY) { if (tid == 0) tr->status = TR_DEFER; return; }
     double s = 0.0;
     for (int g = tid; g < G; g += NT) s += ldp(&rbf[g].S) * sm.chs[g];
     const double S = block_sum<double>(s, sm.red);
@@ -1563,136 +1546,299 @@ __device__ __forceinline__ void topp32_row(Smem &sm, FineSmem &fs, RowCx &c, con
     }
     __syncthreads();
     const int ba = sm.bi[0], bb = sm.bi[1];
+    if (ba < 0) { if (tid == 0) tr->status = TR_DEFER; return; }  // the cut lies below the coarse range
+    const float cb_lo = Ar - (float)bb, cb_hi = Ar - (float)ba;
+    if (wave_id() == 0) {
+        const uint32_t kfin = row_key(-INFINITY, F32) + 1u, ktop = 0xff7fffffu;  // finite keys
+        const uint32_t k0 = key_search(kfin, ktop, [&](uint32_t k) { return coarse_bin(f32_of_key(k)) >= cb_lo; });
+        const uint32_t k1 = key_search(kfin, ktop, [&](uint32_t k) { return coarse_bin(f32_of_key(k)) > cb_hi; }) - 1u;
+        if (lane_id() == 0) { sm.bu[5] = k0; sm.bu[6] = k1; }
+    }
     __syncthreads();
-    if (ba < 0) { trace(a.ws, a.L, c.row, 21); final_generic<DT>(sm, c, pl, ro, a); return; }  // the cut lies below the coarse range
-    trace(a.ws, a.L, c.row, 17);
-    uint32_t klo, khi;
-    {
-        const float cb_lo = Ar - (float)bb, cb_hi = Ar - (float)ba;
-        if (wave_id() == 0) {
-            const uint32_t kfin = row_key(-INFINITY, DT) + 1u, ktop = 0xff7fffffu;  // finite keys
-            const uint32_t k0 = key_search(kfin, ktop, [&](uint32_t k) { return coarse_bin(f32_of_key(k)) >= cb_lo; });
-            const uint32_t k1 = key_search(kfin, ktop, [&](uint32_t k) { return coarse_bin(f32_of_key(k)) > cb_hi; }) - 1u;
-            if (lane_id() == 0) { sm.bu[5] = k0; sm.bu[6] = k1; }
-        }
-        __syncthreads();
-        klo = sm.bu[5]; khi = sm.bu[6];
-        __syncthreads();
-    }
-    // ---- 2. passes: kept mass above the band per chunk, the band's fine bins
-    for (int g = tid; g < G; g += NT) sm.cw[g] = 0.0;
-    uint32_t xprev = 0xff800000u;  // raw key of +inf: nothing counted yet
-    uint32_t nband = 0xffffffffu;
-    for (int it = 0; it < 3; ++it) {
-        uint32_t xlo, xhi;
-        x_interval<DT>(sm, klo, khi, T, &xlo, &xhi);
-        if (it == 0) trace(a.ws, a.L, c.row, 25);
+    trace(a.ws, L, row, 4);
+    const uint32_t klo = sm.bu[5], khi = sm.bu[6];
+    uint32_t xlo, xhi;
+    x_interval<F32>(sm, klo, khi, pl.T, &xlo, &xhi);
+    trace(a.ws, L, row, 5);
+    if (tid == 0) {
         const float lo = f32_of_key(klo), hi = f32_of_key(khi);
-        const float scf = hi > lo ? (float)FB2 / (hi - lo) : 0.0f;
-        for (int j = tid; j < FB2; j += NT) { fs.cnt[j] = 0u; fs.mass[j] = 0ull; }
-        if (tid == 0) sm.bu[3] = 0u;
-        __syncthreads();
-        if (it == 0) trace(a.ws, a.L, c.row, 26);
+        tr->klo = klo; tr->khi = khi; tr->xlo = xlo; tr->xhi = xhi;
+        tr->m = m; tr->lo = lo; tr->scf = hi > lo ? (float)FH / (hi - lo) : 0.0f;
+        tr->S = S; tr->A = A;
+        tr->status = TR_ACTIVE;
+    }
+}
+
+template <int EPT>
+__global__ __launch_bounds__(NT) void k_tp_hist(Args a)
+{
+    __shared__ uint32_t cnt[FH];
+    __shared__ unsigned long long mass[FH];
+    __shared__ double etab[ETAB_N];
+    __shared__ Red red;
+    const Layout &L = a.L;
+    const int tid = threadIdx.x;
+    exp_table(etab, tid);
+    const int64_t tasks = L.B * L.G;
+    for (int64_t t = blockIdx.x; t < tasks; t += gridDim.x) {
+        const int row = (int)(t / L.G), g = (int)(t % L.G);
+        const RowPlan pl = plan_row(a.params[row], a.V);
+        if (pl.mode != M_TOPP) continue;
+        const TopRow *tr = top_row(a, row);
+        if (ldp(&tr->status) != TR_ACTIVE) continue;
+        const float xlof = f32_of_key(ldp(&tr->xlo)), xhif = f32_of_key(ldp(&tr->xhi));
+        const float m = ldp(&tr->m), lo = ldp(&tr->lo), scf = ldp(&tr->scf), T = pl.T, rT = 1.0f / pl.T;
+        const double md = (double)m;
+        for (int b = tid; b < FH; b += NT) { cnt[b] = 0u; mass[b] = 0ull; }
+        float x[EPT];
+        const int64_t base = (int64_t)g * NT * EPT;
+        load_chunk<F32, EPT>(a.logits + (int64_t)row * a.stride_bytes, base, a.V, a.vec_ok, x);
+        __syncthreads();  // (also publishes etab on the first task)
         double acc = 0.0;
-        // raw-value bounds: x >= xlof <=> key(x / T) >= klo, x <= xhif <=> key(x / T) <= khi
-        const float xlof = f32_of_key(xlo), xhif = f32_of_key(xhi), xprevf = f32_of_key(xprev);
-        sweep_row<DT, 32>(c, xlof, [&](int j, float x) {
-            if (!(x <= xprevf)) return;  // counted by an earlier pass
-            const float y = scale_r<DT>(x, T, rT);
-            if (x > xhif) { acc += dexp((double)y - md, sm.etab); return; }
-            const int b = (int)fminf(fmaxf(floorf((y - lo) * scf), 0.0f), (float)(FB2 - 1));
-            atomicAdd(&fs.cnt[b], 1u);
-            atomicAdd(&fs.mass[b], (unsigned long long)__float2uint_rn(wexp(y, m) * 2147483648.0f));
-            // survivor list: one LDS atomic per wave
-            const uint64_t mk = __ballot(1);
-            const int lead = __builtin_ctzll(mk);
-            uint32_t base = 0u;
-            if (lane_id() == lead) base = atomicAdd(&sm.bu[3], (uint32_t)__popcll(mk));
-            base = (uint32_t)__shfl((int)base, lead, 64);
-            const uint32_t q = base + (uint32_t)__popcll(mk & ((1ull << lane_id()) - 1ull));
-            if (q < (uint32_t)SURV_CAP) { sm.u.s.key[q] = row_key(y, DT); sm.u.s.idx[q] = (int32_t)j; }
-        }, [&](int gq) {
-            const double w = wave_sum(acc);
-            if (lane_id() == 0 && w != 0.0) atomicAdd(&sm.cw[gq], w);
-            acc = 0.0;
-        });
-        __syncthreads();
-        nband = sm.bu[3];
-        xprev = xhi;
-        trace(a.ws, a.L, c.row, 18 + it);
-        if (nband <= (uint32_t)SURV_CAP || !(hi > lo) || it == 2) break;
-        // narrow: fine bins (descending y) whose cumulative mass interval meets [A - delta, A + delta]
-        double ab = 0.0;
-        for (int g = tid; g < G; g += NT) ab += sm.cw[g];
-        const double above = block_sum<double>(ab, sm.red);
-        double *dmass = reinterpret_cast<double *>(fs.mass);  // the sums as doubles, in place
-        for (int j = tid; j < FB2; j += NT) dmass[j] = (double)fs.mass[j] * (1.0 / 2147483648.0);
-        __syncthreads();
-        if (wave_id() == 0) {
-            const double delta = 1e-6 * S + (double)nband * 4.7e-10;
-            double tmp;
-            const int jb = wave_find_desc<double>(dmass, FB2, A - delta - above, &tmp);
-            const int ja = wave_find_desc<double>(dmass, FB2, A + delta - above, &tmp);
-            uint32_t cnt = 0u;
-            for (int j = lane_id(); j < FB2; j += 64) cnt += (j >= ja && j <= jb) ? fs.cnt[j] : 0u;
-            cnt = wave_sum(cnt);
-            if (lane_id() == 0) { sm.bi[0] = (ja <= jb && cnt > 0u) ? ja : -1; sm.bi[1] = jb; }
+#pragma unroll
+        for (int i = 0; i < EPT; ++i) {
+            const float xi = x[i];
+            if (xi >= xlof) {
+                const float y = scale_r<F32>(xi, T, rT);
+                const double e = dexp((double)y - md, etab);
+                if (xi > xhif) {
+                    acc += e;
+                } else {
+                    const int b = fine_bin(y, lo, scf);
+                    atomicAdd(&cnt[b], 1u);
+                    atomicAdd(&mass[b], (unsigned long long)rint(e * FIX_ONE));
+                }
+            }
         }
-        __syncthreads();
-        const int ja = sm.bi[0], jb = sm.bi[1];
-        __syncthreads();
-        if (ja < 0) break;  // (caught below: nband > SURV_CAP)
-        if (wave_id() == 0) {
-            auto jof = [&](uint32_t k) -> int { return (int)fminf(fmaxf(floorf((f32_of_key(k) - lo) * scf), 0.0f), (float)(FB2 - 1)); };
-            const uint32_t k0 = key_search(klo, khi, [&](uint32_t k) { return jof(k) >= ja; });
-            const uint32_t k1 = key_search(klo, khi, [&](uint32_t k) { return jof(k) > jb; }) - 1u;
-            if (lane_id() == 0) { sm.bu[5] = k0; sm.bu[6] = k1; }
-        }
-        __syncthreads();
-        klo = sm.bu[5]; khi = sm.bu[6];
+        const double above = block_sum<double>(acc, red);  // (its barriers publish the bins)
+        TopChunk *tc = top_chunk(a, row, g);
+        if (tid == 0) tc->above = above;
+        for (int b = tid; b < FH; b += NT) { tc->cnt[b] = cnt[b]; tc->mass[b] = mass[b]; }
         __syncthreads();
     }
-    if (nband > (uint32_t)SURV_CAP || nband == 0u) { trace(a.ws, a.L, c.row, 22); final_generic<DT>(sm, c, pl, ro, a); return; }
-    // ---- 3. the survivors' float64 weights and the cut
-    for (int q = tid; q < (int)nband; q += NT) sm.u.s.e[q] = dexp((double)f32_of_key(sm.u.s.key[q]) - md, sm.etab);
+}
+
+__global__ __launch_bounds__(NT) void k_tp_merge(Args a)
+{
+    __shared__ uint32_t cnt[FH];
+    __shared__ double mass[FH];
+    __shared__ Red red;
+    __shared__ int32_t bi[2];
+    __shared__ uint32_t bu[2];
+    const Layout &L = a.L;
+    const int row = blockIdx.x, tid = threadIdx.x, G = L.G;
+    const RowPlan pl = plan_row(a.params[row], a.V);
+    if (pl.mode != M_TOPP) return;
+    TopRow *tr = top_row(a, row);
+    if (ldp(&tr->status) != TR_ACTIVE) return;
+    const double S = ldp(&tr->S), A = ldp(&tr->A);
+    trace(a.ws, L, row, 6);
+    // merged fine bins (exact integer sums, then doubles) and the mass above
+    // the band; each thread keeps 8 chunks' loads of its bins in flight
+    static_assert(FH == 2 * NT, "two bins per thread");
+    {
+        uint32_t c0 = 0u, c1 = 0u;
+        unsigned long long m0 = 0ull, m1 = 0ull;
+        for (int g0 = 0; g0 < G; g0 += 8) {
+            uint32_t cc[16];
+            unsigned long long mm[16];
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                const bool in = g0 + q < G;
+                const TopChunk *tc = top_chunk(a, row, in ? g0 + q : 0);
+                cc[2 * q] = in ? tc->cnt[tid] : 0u;
+                cc[2 * q + 1] = in ? tc->cnt[tid + NT] : 0u;
+                mm[2 * q] = in ? tc->mass[tid] : 0ull;
+                mm[2 * q + 1] = in ? tc->mass[tid + NT] : 0ull;
+            }
+#pragma unroll
+            for (int q = 0; q < 8; ++q) { c0 += cc[2 * q]; c1 += cc[2 * q + 1]; m0 += mm[2 * q]; m1 += mm[2 * q + 1]; }
+        }
+        cnt[tid] = c0; cnt[tid + NT] = c1;
+        mass[tid] = (double)m0 * (1.0 / FIX_ONE);
+        mass[tid + NT] = (double)m1 * (1.0 / FIX_ONE);
+    }
     double ab = 0.0;
-    for (int g = tid; g < G; g += NT) ab += sm.cw[g];
-    const double above = block_sum<double>(ab, sm.red);  // (its barriers publish the weights)
+    for (int g = tid; g < G; g += NT) ab += ldp(&top_chunk(a, row, g)->above);
+    const double above = block_sum<double>(ab, red);  // (its barriers publish the bins)
+    trace(a.ws, L, row, 7);
+    if (wave_id() == 0) {
+        // every integer weight is off by at most 1/2 unit: delta covers them
+        uint32_t n = 0u;
+        for (int b = lane_id(); b < FH; b += 64) n += cnt[b];
+        n = wave_sum(n);
+        const double delta = 1e-12 * S + (double)n * (0.5 / FIX_ONE);
+        double tmp;
+        const int jb = wave_find_desc<double>(mass, FH, A - delta - above, &tmp);
+        const int ja = wave_find_desc<double>(mass, FH, A + delta - above, &tmp);
+        uint32_t c2 = 0u, nab = 0u;
+        for (int b = lane_id(); b < FH; b += 64) { c2 += (b >= ja && b <= jb) ? cnt[b] : 0u; nab += b > jb ? cnt[b] : 0u; }
+        c2 = wave_sum(c2);
+        nab = wave_sum(nab);
+        if (lane_id() == 0) {
+            const bool ok = ja <= jb && c2 > 0u && c2 <= (uint32_t)SURV_CAP;
+            bi[0] = ok ? ja : -1; bi[1] = jb; bu[0] = nab;
+        }
+    }
+    __syncthreads();
+    const int ja = bi[0], jb = bi[1];
+    trace(a.ws, L, row, 8);
+    if (ja < 0) { if (tid == 0) tr->status = TR_DEFER; return; }
+    const float lo = ldp(&tr->lo), scf = ldp(&tr->scf);
+    if (wave_id() == 0) {
+        const uint32_t klo = ldp(&tr->klo), khi = ldp(&tr->khi);
+        const uint32_t k0 = key_search(klo, khi, [&](uint32_t k) { return fine_bin(f32_of_key(k), lo, scf) >= ja; });
+        const uint32_t k1 = key_search(klo, khi, [&](uint32_t k) { return fine_bin(f32_of_key(k), lo, scf) > jb; }) - 1u;
+        const uint32_t x0 = x_lower<F32>(k0, pl.T), x1 = x_upper<F32>(k1, pl.T);
+        if (lane_id() == 0) {
+            tr->klo2 = k0; tr->khi2 = k1; tr->xlo2 = x0; tr->xhi2 = x1;
+            tr->fix_err = (double)bu[0] * (0.5 / FIX_ONE);
+            tr->count = 0u;
+        }
+    }
+    trace(a.ws, L, row, 9);
+    // each chunk's kept mass above the final band: its above-mass plus its
+    // fine bins above jb (one wave per chunk)
+    for (int g = wave_id(); g < G; g += NWAVE) {
+        const TopChunk *tc = top_chunk(a, row, g);
+        unsigned long long mm[FH / 64];
+#pragma unroll
+        for (int q = 0; q < FH / 64; ++q) { const int b = q * 64 + lane_id(); mm[q] = b > jb ? tc->mass[b] : 0ull; }
+        unsigned long long ms = 0ull;
+#pragma unroll
+        for (int q = 0; q < FH / 64; ++q) ms += mm[q];
+        ms = wave_sum(ms);
+        if (lane_id() == 0) tr->cw[g] = ldp(&tc->above) + (double)ms * (1.0 / FIX_ONE);
+    }
+    trace(a.ws, L, row, 10);
+}
+
+template <int EPT>
+__global__ __launch_bounds__(NT) void k_tp_collect(Args a)
+{
+    __shared__ Red red;
+    __shared__ uint32_t base_s;
+    const Layout &L = a.L;
+    const int tid = threadIdx.x;
+    constexpr int VEC = Traits<F32>::VEC;
+    const int64_t tasks = L.B * L.G;
+    for (int64_t t = blockIdx.x; t < tasks; t += gridDim.x) {
+        const int row = (int)(t / L.G), g = (int)(t % L.G);
+        const RowPlan pl = plan_row(a.params[row], a.V);
+        if (pl.mode != M_TOPP) continue;
+        TopRow *tr = top_row(a, row);
+        if (ldp(&tr->status) != TR_ACTIVE) continue;
+        const float x0 = f32_of_key(ldp(&tr->xlo2)), x1 = f32_of_key(ldp(&tr->xhi2));
+        float x[EPT];
+        const int64_t base = (int64_t)g * NT * EPT;
+        load_chunk<F32, EPT>(a.logits + (int64_t)row * a.stride_bytes, base, a.V, a.vec_ok, x);
+        uint32_t mine = 0u;
+#pragma unroll
+        for (int i = 0; i < EPT; ++i) mine += (x[i] >= x0 && x[i] <= x1) ? 1u : 0u;
+        uint32_t total;
+        const uint32_t off = block_excl_scan<uint32_t>(mine, red, &total);
+        if (total == 0u) continue;
+        if (tid == 0) base_s = atomicAdd(&tr->count, total);
+        __syncthreads();
+        uint32_t q = base_s + off;
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < EPT; ++i) {
+            if (x[i] >= x0 && x[i] <= x1) {
+                if (q < (uint32_t)SURV_CAP) {
+                    const int32_t j = (int32_t)(base + (((i / VEC) * NT + tid) * VEC) + (i % VEC));
+                    tr->list[q].key = row_key(scale_y<F32>(x[i], pl.T), F32);
+                    tr->list[q].idx = j;
+                }
+                ++q;
+            }
+        }
+    }
+}
+
+__global__ __launch_bounds__(NT) void k_tp_final(Args a)
+{
+    __shared__ Smem sm;
+    const Layout &L = a.L;
+    const int row = blockIdx.x, tid = threadIdx.x, G = L.G;
+    const RowPlan pl = plan_row(a.params[row], a.V);
+    if (pl.mode != M_TOPP) return;
+    TopRow *tr = top_row(a, row);
+    RowOut *ro = reinterpret_cast<RowOut *>(a.ws + L.rowout) + row;
+    const uint32_t n = ldp(&tr->count);
+    if (ldp(&tr->status) != TR_ACTIVE || n == 0u || n > (uint32_t)SURV_CAP) {
+        if (tid == 0) ro->status = ROW_DEFER;
+        return;
+    }
+    RowCx c;
+    c.rowp = a.logits + (int64_t)row * a.stride_bytes;
+    c.V = a.V; c.vec_ok = a.vec_ok; c.G = G; c.CH = (int64_t)NT * L.ept; c.row = row; c.T = pl.T;
+    const float m = ldp(&tr->m);
+    c.m = m;
+    const double md = (double)m, A = ldp(&tr->A);
+    trace(a.ws, L, row, 11);
+    exp_table(sm.etab, tid);
+    __syncthreads();
+    {
+        constexpr int PT = SURV_CAP / NT;
+        Elem el[PT];
+#pragma unroll
+        for (int q = 0; q < PT; ++q) { const int i = q * NT + tid; if (i < (int)n) el[q] = tr->list[i]; }
+#pragma unroll
+        for (int q = 0; q < PT; ++q) {
+            const int i = q * NT + tid;
+            if (i < (int)n) {
+                sm.u.s.key[i] = el[q].key;
+                sm.u.s.idx[i] = el[q].idx;
+                sm.u.s.e[i] = dexp((double)f32_of_key(el[q].key) - md, sm.etab);
+            }
+        }
+    }
+    double ab = 0.0;
+    for (int g = tid; g < G; g += NT) { const double w = ldp(&tr->cw[g]); sm.cw[g] = w; ab += w; }
+    const double above = block_sum<double>(ab, sm.red);  // (its barriers publish the survivors)
+    trace(a.ws, L, row, 12);
     uint32_t cut_key = 0u;
     int32_t cut_i = 0;
     double ql = 0.0, wl = 0.0;
-    const int rl = window_resolve(sm, nband, above, A, &cut_key, &cut_i, &ql, &wl);
-    // S, the mass above and the survivors' weights carry relative errors below
-    // 1e-15 each (dexp) plus float64 summation rounding over at most 2^30 terms
-    const double err = 1e-12 * (above + A) + 1e-300;
-    if (!(rl >= 0 && (A - ql) > err && (ql + wl - A) > err)) { trace(a.ws, a.L, c.row, 23); final_generic<DT>(sm, c, pl, ro, a); return; }
-    trace(a.ws, a.L, c.row, 24);
-    // ---- 4. per-chunk kept weights (above the window + its kept prefix), the draw
+    const int rl = window_resolve(sm, n, above, A, &cut_key, &cut_i, &ql, &wl);
+    // S, the above-masses and the survivors' weights carry relative errors
+    // below 1e-15 each (dexp) plus float64 summation rounding; the fixed-point
+    // bins above the band carry fix_err
+    const double err = 1e-12 * (above + A) + ldp(&tr->fix_err) + 1e-300;
+    trace(a.ws, L, row, 13);
+    if (!(rl >= 0 && (A - ql) > err && (ql + wl - A) > err)) {
+        if (tid == 0) ro->status = ROW_DEFER;
+        return;
+    }
+    const int chsh = __builtin_ctz((unsigned)c.CH);
     for (int q = tid; q <= rl; q += NT) {
         const int32_t j = (int32_t)(0xffffffffu - (uint32_t)sm.u.so.k[q]);
-        atomicAdd(&sm.cw[(int)(j / c.CH)], sm.u.so.e[q]);
+        atomicAdd(&sm.cw[j >> chsh], sm.u.so.e[q]);
     }
     int gsel;
     double resid, SK;
     pick_chunk(sm, G, pl.u, &gsel, &resid, &SK);
+    trace(a.ws, L, row, 14);
     int64_t id = -1;
     if (gsel >= 0) {
-        id = draw_in_chunk<DT>(sm, c, gsel, resid, [&](float xv, int64_t j) -> double {
-            const float y = scale_y<DT>(xv, T);
-            return (y != -INFINITY && kept_by_cut(row_key(y, DT), j, cut_key, cut_i)) ? exp((double)y - md) : 0.0;
+        const float T = pl.T;
+        id = draw_in_chunk<F32>(sm, c, gsel, resid, [&](float xv, int64_t j) -> double {
+            const float y = scale_y<F32>(xv, T);
+            return (y != -INFINITY && kept_by_cut(row_key(y, F32), j, cut_key, cut_i)) ? exp((double)y - md) : 0.0;
         });
     }
-    write_row(ro, a, c.row, id, id >= 0 ? MIS_ROW_OK : MIS_ROW_INVALID, pl.mode, m, cut_key, cut_i, SK);
+    write_row(ro, a, row, id, id >= 0 ? MIS_ROW_OK : MIS_ROW_INVALID, pl.mode, m, cut_key, cut_i, SK);
+    trace(a.ws, L, row, 15);
 }
 
 // One workgroup per row: merges the chunk summaries and finishes the row:
-// greedy, temperature, small top-k from the summaries; fp32 top-p from the
-// coarse bins and re-reads of the row; the generic re-read path otherwise.
+// greedy, temperature, small top-k from the summaries; the generic re-read
+// path otherwise.  fp32 top-p rows are the k_tp_* passes'.
 template <int DT>
 __global__ __launch_bounds__(NT) void k_final(Args a)
 {
     __shared__ Smem sm;
-    __shared__ FineSmem fs;
     const Layout &L = a.L;
     const int row = blockIdx.x;
     RowOut *ro = reinterpret_cast<RowOut *>(a.ws + L.rowout) + row;
@@ -1707,9 +1853,9 @@ __global__ __launch_bounds__(NT) void k_final(Args a)
     trace(a.ws, L, row, 16);
     __syncthreads();
     const ChunkSum *csr = reinterpret_cast<const ChunkSum *>(a.ws + L.chunks) + (size_t)row * L.G;
-    const RoundBuf *rbf = reinterpret_cast<const RoundBuf *>(a.ws + L.rbuf) + (size_t)row * L.G;
-    if (DT == F32 && sm.pl.mode == M_TOPP) topp32_row<F32>(sm, fs, sm.cx, sm.pl, csr, rbf, ro, sm.args);
-    else leader_row<DT>(sm, sm.cx, sm.pl, csr, ro, sm.args);
+    // fp32 top-p rows were finished by k_tp_final unless it left them to the generic path
+    if (DT == F32 && sm.pl.mode == M_TOPP && ldp(&ro->status) != ROW_DEFER) return;
+    leader_row<DT>(sm, sm.cx, sm.pl, csr, ro, sm.args);
     trace(a.ws, L, row, 31);
 }
 
@@ -1766,7 +1912,8 @@ static hipError_t launch_sample(const Args &a, hipStream_t st)
 }
 
 // events (optional): [0] before the chunk pass, [1] between the chunk pass
-// and the row pass, [2] after the row pass (before the debug emit)
+// and the row pass (k_tp_* + k_final), [2] after the row pass (before the
+// debug emit)
 template <int DT>
 static hipError_t launch_dt(const Args &a, float *probs, uint32_t *keep, hipStream_t st, void *const *ev)
 {
@@ -1778,6 +1925,19 @@ static hipError_t launch_dt(const Args &a, float *probs, uint32_t *keep, hipStre
     }
     if (e != hipSuccess) return e;
     if (ev && (e = hipEventRecord((hipEvent_t)ev[1], st)) != hipSuccess) return e;
+    if (DT == F32) {
+        // fp32 top-p rows (the other rows' workgroups return at once)
+        const unsigned B = (unsigned)a.L.B;
+        const unsigned tg = (unsigned)(a.L.B * a.L.G < TP_GRID ? a.L.B * a.L.G : TP_GRID);
+        hipLaunchKernelGGL(k_tp_prep, dim3(B), dim3(NT), 0, st, a);
+        if (a.L.ept == 64) hipLaunchKernelGGL((k_tp_hist<64>), dim3(tg), dim3(NT), 0, st, a);
+        else hipLaunchKernelGGL((k_tp_hist<16>), dim3(tg), dim3(NT), 0, st, a);
+        hipLaunchKernelGGL(k_tp_merge, dim3(B), dim3(NT), 0, st, a);
+        if (a.L.ept == 64) hipLaunchKernelGGL((k_tp_collect<64>), dim3(tg), dim3(NT), 0, st, a);
+        else hipLaunchKernelGGL((k_tp_collect<16>), dim3(tg), dim3(NT), 0, st, a);
+        hipLaunchKernelGGL(k_tp_final, dim3(B), dim3(NT), 0, st, a);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
     hipLaunchKernelGGL((k_final<DT>), dim3((unsigned)a.L.B), dim3(NT), 0, st, a);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     if (ev && (e = hipEventRecord((hipEvent_t)ev[2], st)) != hipSuccess) return e;
