@@ -127,7 +127,7 @@ def main():
 
     import torch
     from vllm_mps_amd import workloads as W
-    from vllm_mps_amd.sampler import Sampler, pack_params
+    from vllm_mps_amd.sampler import Sampler, pack_params, row_kinds
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
@@ -137,14 +137,17 @@ def main():
     bytes_alg = W.algorithmic_bytes(B, V, w.dtype)
     nbuf = max(1, math.ceil(args.rotate_gib * (1 << 30) / (B * V * esz)))
     base = w.to_torch(dev)
+    base_dtype = base.dtype
     bufs = [base.clone() for _ in range(nbuf)]
     del base
     packed = pack_params(torch.from_numpy(w.temperature.copy()).to(dev), torch.from_numpy(w.top_k.copy()).to(dev),
                          torch.from_numpy(w.top_p.copy()).to(dev), torch.from_numpy(w.uniform.copy()).to(dev))
     out = torch.empty(B, dtype=torch.int64, device=dev)
+    # the engine knows its requests' parameters on the host: the row-kind hint
+    kinds = row_kinds(w.temperature, w.top_k, w.top_p, V, base_dtype)
     s = Sampler()
     for i in range(args.warmup):
-        s.sample_packed(bufs[i % nbuf], packed, out=out)
+        s.sample_packed(bufs[i % nbuf], packed, out=out, kinds=kinds)
     torch.cuda.synchronize()
 
     K = args.steps
@@ -156,7 +159,7 @@ def main():
     torch.cuda.synchronize()
     start.record()
     for i in range(K):
-        s.sample_packed(bufs[(args.warmup + i) % nbuf], packed, out=out, events=evs[i])
+        s.sample_packed(bufs[(args.warmup + i) % nbuf], packed, out=out, events=evs[i], kinds=kinds)
     end.record()
     torch.cuda.synchronize()
     total_ms = start.elapsed_time(end)

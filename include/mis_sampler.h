@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define MIS_ABI_VERSION 2
+#define MIS_ABI_VERSION 3
 
 /* logits element type */
 enum { MIS_DTYPE_F32 = 0, MIS_DTYPE_F16 = 1, MIS_DTYPE_BF16 = 2 };
@@ -119,6 +119,28 @@ int mis_sample_profiled(const void *logits, int dtype, int64_t B, int64_t V, int
                         const mis_row_params *params, int64_t *out_ids, int32_t *out_status,
                         float *out_probs, uint32_t *out_keep, void *workspace, size_t workspace_bytes,
                         void *stream, void *const *events);
+
+/*
+ * Row kinds a batch holds, for mis_sample_ex(): a performance hint only.
+ *   MIS_KIND_TOPP32  fp32 logits, 0 < temperature, top_k off (0 or >= V),
+ *                    top_p < 1 (the rows the top-p passes serve)
+ *   MIS_KIND_OTHER   every other row
+ * A clear bit lets the library skip the launches only that kind needs; the
+ * results are the same for any `kinds` (rows of a kind whose bit is clear
+ * take the generic path), so a wrong hint costs time, never correctness.
+ */
+enum { MIS_KIND_TOPP32 = 1, MIS_KIND_OTHER = 2, MIS_KIND_ALL = 3 };
+
+/*
+ * mis_sample() with a row-kind hint and optional events (NULL, or three
+ * hipEvent_t recorded as by mis_sample_profiled()).  No counterpart in the
+ * reference: its sampler runs on the host, which knows each request's
+ * SamplingParams; the engine's batch builder passes what it knows.
+ */
+int mis_sample_ex(const void *logits, int dtype, int64_t B, int64_t V, int64_t row_stride,
+                  const mis_row_params *params, int64_t *out_ids, int32_t *out_status,
+                  float *out_probs, uint32_t *out_keep, void *workspace, size_t workspace_bytes,
+                  void *stream, unsigned kinds, void *const *events);
 
 /* Human-readable text for an API return code. */
 const char *mis_strerror(int code);

@@ -12,7 +12,7 @@ def params_of(w: W.Workload) -> np.ndarray:
     return O.make_params(w.temperature, w.top_k, w.top_p, w.uniform)
 
 
-def run_gpu(w: W.Workload, device, debug: bool = True, stride_pad: int = 0, sampler=None) -> dict:
+def run_gpu(w: W.Workload, device, debug: bool = True, stride_pad: int = 0, sampler=None, kinds=None) -> dict:
     import torch
     from vllm_mps_amd.sampler import Sampler, pack_params
 
@@ -28,7 +28,7 @@ def run_gpu(w: W.Workload, device, debug: bool = True, stride_pad: int = 0, samp
     probs = torch.full((B, V), -1.0, dtype=torch.float32, device=device) if debug else None
     keep = torch.zeros((B, (V + 31) // 32), dtype=torch.int32, device=device) if debug else None
     s = Sampler() if sampler is None else sampler
-    ids = s.sample_packed(t, packed, status_out=status, probs_out=probs, keep_out=keep)
+    ids = s.sample_packed(t, packed, status_out=status, probs_out=probs, keep_out=keep, kinds=kinds)
     torch.cuda.synchronize(device)
     out = dict(ids=ids.cpu().numpy(), status=status.cpu().numpy())
     if debug:
@@ -41,8 +41,8 @@ def run_oracle(w: W.Workload, debug: bool = True) -> dict:
     return O.sample_rows(w.logits, w.dtype, params_of(w), want_probs=debug, want_keep=debug)
 
 
-def check(w: W.Workload, device, debug: bool = True, stride_pad: int = 0, sampler=None) -> C.Report:
-    g = run_gpu(w, device, debug=debug, stride_pad=stride_pad, sampler=sampler)
+def check(w: W.Workload, device, debug: bool = True, stride_pad: int = 0, sampler=None, kinds=None) -> C.Report:
+    g = run_gpu(w, device, debug=debug, stride_pad=stride_pad, sampler=sampler, kinds=kinds)
     o = run_oracle(w, debug=debug)
     return C.compare(w.dtype, params_of(w), g, o)
 

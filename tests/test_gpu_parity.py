@@ -30,6 +30,14 @@ def test_config_c3_full(device):
     assert len(rep.exempt_mask) == 0, rep.exempt_mask
 
 
+@pytest.mark.parametrize("kinds", [0, 1, 2, 3])
+def test_row_kind_hints(kinds, device):
+    """The row-kind hint only selects launches: C3's first 64 rows (both
+    kinds) give the oracle's results under every hint, wrong ones included."""
+    w = W.make_c3().rows(np.arange(64))
+    _run(f"C3[:64] kinds={kinds}", w, device, kinds=kinds)
+
+
 def test_config_c5_subset(device):
     w = W.make_c5(rows=96)
     _run("C5[:96]", w, device)

@@ -94,3 +94,19 @@ def test_bench_refuses_multi_gpu():
                          text=True)
     assert out.returncode == 2
     assert "one GPU only" in out.stderr
+
+
+def test_row_kinds_hint():
+    """Host-side row-kind hint: fp32 top-p rows (T > 0, top-k off, top_p < 1)
+    versus every other row; 16-bit batches have no fp32 top-p rows."""
+    import torch
+    from vllm_mps_amd.sampler import KIND_OTHER, KIND_TOPP32, row_kinds
+    V = 100
+    assert row_kinds([1.0], [0], [0.9], V, torch.float32) == KIND_TOPP32
+    assert row_kinds([1.0], [V], [0.9], V, torch.float32) == KIND_TOPP32      # k >= V is off
+    assert row_kinds([1.0], [20], [0.9], V, torch.float32) == KIND_OTHER       # small-k branch
+    assert row_kinds([0.0], [0], [0.9], V, torch.float32) == KIND_OTHER        # greedy
+    assert row_kinds([1.0], [0], [1.0], V, torch.float32) == KIND_OTHER        # top-p off
+    assert row_kinds([1.0, 0.0], [0, 0], [0.5, 1.0], V, torch.float32) == KIND_TOPP32 | KIND_OTHER
+    assert row_kinds([1.0], [0], [0.9], V, torch.float16) == KIND_OTHER
+    assert row_kinds([], [], [], V, torch.float32) == 0

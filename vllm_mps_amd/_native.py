@@ -12,9 +12,11 @@ from . import build as _build
 
 DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
 ROW_OK, ROW_BAD_PARAM, ROW_INVALID, ROW_UNSUPPORTED, ROW_INTERNAL = 0, 1, 2, 3, 4
-ABI_VERSION = 2
+ABI_VERSION = 3
+KIND_TOPP32 = 1  # MIS_KIND_TOPP32
+KIND_OTHER = 2   # MIS_KIND_OTHER
 
-EXPORTED = ("mis_workspace_bytes", "mis_workspace_init", "mis_sample", "mis_sample_profiled", "mis_strerror", "mis_last_hip_error",
+EXPORTED = ("mis_workspace_bytes", "mis_workspace_init", "mis_sample", "mis_sample_profiled", "mis_sample_ex", "mis_strerror", "mis_last_hip_error",
             "mis_abi_version")
 
 _lib = None
@@ -48,6 +50,9 @@ def load():
     lib.mis_sample_profiled.argtypes = [vp, ctypes.c_int, i64, i64, i64, vp, vp, vp, vp, vp, vp, ctypes.c_size_t, vp,
                                         ctypes.POINTER(vp)]
     lib.mis_sample_profiled.restype = ctypes.c_int
+    lib.mis_sample_ex.argtypes = [vp, ctypes.c_int, i64, i64, i64, vp, vp, vp, vp, vp, vp, ctypes.c_size_t, vp,
+                                  ctypes.c_uint, vp]
+    lib.mis_sample_ex.restype = ctypes.c_int
     lib.mis_strerror.argtypes = [ctypes.c_int]
     lib.mis_strerror.restype = ctypes.c_char_p
     lib.mis_last_hip_error.restype = ctypes.c_int
@@ -72,9 +77,13 @@ def workspace_init(ws_ptr: int, ws_bytes: int, stream: int) -> None:
 
 def sample(logits_ptr: int, dtype: int, B: int, V: int, row_stride: int, params_ptr: int, ids_ptr: int,
            status_ptr: int | None, probs_ptr: int | None, keep_ptr: int | None, ws_ptr: int, ws_bytes: int,
-           stream: int, events: tuple[int, int, int] | None = None) -> None:
+           stream: int, events: tuple[int, int, int] | None = None, kinds: int | None = None) -> None:
     lib = load()
-    if events is None:
+    if kinds is not None:
+        ev = None if events is None else (ctypes.c_void_p * 3)(*events)
+        rc = lib.mis_sample_ex(logits_ptr, dtype, B, V, row_stride, params_ptr, ids_ptr, status_ptr, probs_ptr,
+                               keep_ptr, ws_ptr, ws_bytes, stream, kinds, ev)
+    elif events is None:
         rc = lib.mis_sample(logits_ptr, dtype, B, V, row_stride, params_ptr, ids_ptr, status_ptr, probs_ptr,
                             keep_ptr, ws_ptr, ws_bytes, stream)
     else:

@@ -159,6 +159,20 @@ template <class T> __device__ __forceinline__ T wave_incl_scan(T v)
     return v;
 }
 
+// Slot of this lane in an append to a list whose fill is *counter (LDS): one
+// atomic per wave instead of one per element.  Valid where pred holds; lanes
+// not executing the call take no part.
+__device__ __forceinline__ uint32_t wave_append(bool pred, uint32_t *counter)
+{
+    const uint64_t mk = __ballot(pred);
+    if (mk == 0ull) return 0u;
+    const int lead = __builtin_ctzll(__ballot(1));
+    uint32_t base = 0u;
+    if (lane_id() == lead) base = atomicAdd(counter, (uint32_t)__popcll(mk));
+    base = (uint32_t)__shfl((int)base, lead, 64);
+    return base + (uint32_t)__popcll(mk & ((1ull << lane_id()) - 1ull));
+}
+
 // LDS scratch for the block reductions of up to 16 waves (1024 threads);
 // the helpers take the block's wave count NW as a template argument
 constexpr int NWAVE_MAX = 16;

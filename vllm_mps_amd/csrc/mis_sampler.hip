@@ -44,6 +44,8 @@
 #include <math.h>
 #include <stdint.h>
 
+#include <mutex>
+
 #include "mis_device.h"
 #include "mis_sampler.h"
 
@@ -52,6 +54,7 @@ namespace mis {
 constexpr int K_SMALL = 1024;      // largest k' served by the candidate path
 constexpr int CAND_CAP = 2048;     // candidates one chunk may emit
 constexpr int SURV_CAP = 1024;     // top-k survivors / top-p window held in LDS
+constexpr int CCAP = 4096;         // small-k candidates of a row cached in LDS
 constexpr int G_MAX = 256;         // chunks per row
 constexpr int CB_N = 16;           // coarse top-p bins (lane-private)
 constexpr float CB_SCALE = 0.5f;   // coarse bin = floor(y * CB_SCALE): 2 units of y
@@ -250,6 +253,7 @@ struct Smem {
     } v;
     double cw[G_MAX];          // per-chunk kept weight
     double etab[ETAB_N];       // 2^(j/64) for dexp
+    Cand cc[CCAP];             // a small-k row's candidates
     double chs[G_MAX];         // per-chunk rescale to the row max
     double sub_m[256];         // round-local histograms
     uint32_t sub_c[256];
@@ -854,14 +858,15 @@ __device__ __forceinline__ bool leader_smallk(Smem &sm, const RowCx &c, const Ro
     // candidate counts -> prefix offsets (thread 0, G <= 256); candidate f of
     // the row is candidate f - pre[g] of the chunk g with pre[g] <= f < pre[g+1]
     uint32_t *pre = reinterpret_cast<uint32_t *>(sm.chs);
-    for (int g = threadIdx.x; g < c.G; g += NT) sm.sub_c[g] = ncand_of(&cs[g]);
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        uint32_t run = 0;
-        for (int g = 0; g < c.G; ++g) { pre[g] = run; run += sm.sub_c[g]; }
-        pre[c.G] = run;
+    {
+        static_assert(G_MAX <= NT, "one chunk per thread");
+        const uint32_t nc = (int)threadIdx.x < c.G ? ncand_of(&cs[threadIdx.x]) : 0u;
+        uint32_t tot;
+        const uint32_t off = block_excl_scan<uint32_t>(nc, sm.red, &tot);
+        if ((int)threadIdx.x < c.G) pre[threadIdx.x] = off;
+        if (threadIdx.x == 0) pre[c.G] = tot;
+        __syncthreads();
     }
-    __syncthreads();
     const uint32_t ntot = pre[c.G];
     const int G = c.G;
     // chunk facts: overflow, truncation, finite counts
@@ -889,6 +894,28 @@ __device__ __forceinline__ bool leader_smallk(Smem &sm, const RowCx &c, const Ro
         return cand + (size_t)lo * CAND_CAP + (f - pre[lo]);
     };
     constexpr int BATCH = 8;  // candidate loads in flight per thread
+    // the row's candidates, copied once into LDS when they fit
+    const bool cached = ntot <= (uint32_t)CCAP;
+    if (cached) {
+        for (uint32_t f0 = 0; f0 < ntot; f0 += NT * BATCH) {
+            const Cand *cp[BATCH];
+#pragma unroll
+            for (int u = 0; u < BATCH; ++u) {
+                const uint32_t f = f0 + (uint32_t)(u * NT) + threadIdx.x;
+                cp[u] = cand_ptr(f < ntot ? f : 0u);
+            }
+            Cand cv[BATCH];
+#pragma unroll
+            for (int u = 0; u < BATCH; ++u) cv[u] = ldp_cand(cp[u]);
+#pragma unroll
+            for (int u = 0; u < BATCH; ++u) {
+                const uint32_t f = f0 + (uint32_t)(u * NT) + threadIdx.x;
+                if (f < ntot) sm.cc[f] = cv[u];
+            }
+        }
+        __syncthreads();
+    }
+    auto cand_at = [&](uint32_t f) -> Cand { return cached ? sm.cc[f] : ldp_cand(cand_ptr(f)); };
     // k'-th largest raw value over the candidates: linear bins between the
     // smallest and largest candidate (values that differ spread over the bins,
     // so the LDS counters see few conflicts), then the boundary bin's
@@ -898,15 +925,12 @@ __device__ __forceinline__ bool leader_smallk(Smem &sm, const RowCx &c, const Ro
     if (!all_fin) {
         auto for_cands = [&](auto &&fn) {
             for (uint32_t f0 = 0; f0 < ntot; f0 += NT * BATCH) {
-                const Cand *cp[BATCH];
+                float xv[BATCH];
 #pragma unroll
                 for (int u = 0; u < BATCH; ++u) {
                     const uint32_t f = f0 + (uint32_t)(u * NT) + threadIdx.x;
-                    cp[u] = cand_ptr(f < ntot ? f : 0u);
+                    xv[u] = cand_at(f < ntot ? f : 0u).x;
                 }
-                float xv[BATCH];
-#pragma unroll
-                for (int u = 0; u < BATCH; ++u) xv[u] = ldp_cand(cp[u]).x;
 #pragma unroll
                 for (int u = 0; u < BATCH; ++u)
                     if (f0 + (uint32_t)(u * NT) + threadIdx.x < ntot) fn(xv[u]);
@@ -938,10 +962,9 @@ __device__ __forceinline__ bool leader_smallk(Smem &sm, const RowCx &c, const Ro
             if (threadIdx.x == 0) sm.bu[3] = 0u;
             __syncthreads();
             for_cands([&](float x) {
-                if (bin_of(x) == bsel) {
-                    const uint32_t q = atomicAdd(&sm.bu[3], 1u);
-                    if (q < (uint32_t)SURV_CAP) { sm.u.so.k[q] = key_of_f32(x); sm.u.so.e[q] = 0.0; }
-                }
+                const bool in = bin_of(x) == bsel;
+                const uint32_t q = wave_append(in, &sm.bu[3]);
+                if (in && q < (uint32_t)SURV_CAP) { sm.u.so.k[q] = key_of_f32(x); sm.u.so.e[q] = 0.0; }
             });
             __syncthreads();
             const int nb = (int)min(sm.bu[3], (uint32_t)SURV_CAP);
@@ -967,26 +990,20 @@ __device__ __forceinline__ bool leader_smallk(Smem &sm, const RowCx &c, const Ro
     if (threadIdx.x == 0) sm.bu[3] = 0u;
     __syncthreads();
     for (uint32_t f0 = 0; f0 < ntot; f0 += NT * BATCH) {
-        const Cand *cp[BATCH];
-#pragma unroll
-        for (int u = 0; u < BATCH; ++u) {
-            const uint32_t f = f0 + (uint32_t)(u * NT) + threadIdx.x;
-            cp[u] = cand_ptr(f < ntot ? f : 0u);
-        }
         Cand cv[BATCH];
 #pragma unroll
-        for (int u = 0; u < BATCH; ++u) cv[u] = ldp_cand(cp[u]);
+        for (int u = 0; u < BATCH; ++u) {
+            const uint32_t f = f0 + (uint32_t)(u * NT) + threadIdx.x;
+            cv[u] = cand_at(f < ntot ? f : 0u);
+        }
 #pragma unroll
         for (int u = 0; u < BATCH; ++u) {
             const uint32_t f = f0 + (uint32_t)(u * NT) + threadIdx.x;
-            if (f < ntot) {
-                const float y = scale_y<DT>(cv[u].x, c.T);
-                const uint32_t k = row_key(y, DT);
-                if (k >= thr_key) {
-                    const uint32_t p = atomicAdd(&sm.bu[3], 1u);
-                    if (p < (uint32_t)SURV_CAP) { sm.u.s.key[p] = k; sm.u.s.idx[p] = cv[u].idx; sm.u.s.e[p] = exp((double)y - md); }
-                }
-            }
+            const float y = scale_y<DT>(cv[u].x, c.T);
+            const uint32_t k = row_key(y, DT);
+            const bool in = f < ntot && k >= thr_key;
+            const uint32_t p = wave_append(in, &sm.bu[3]);
+            if (in && p < (uint32_t)SURV_CAP) { sm.u.s.key[p] = k; sm.u.s.idx[p] = cv[u].idx; sm.u.s.e[p] = exp((double)y - md); }
         }
     }
     __syncthreads();
@@ -1832,11 +1849,13 @@ __global__ __launch_bounds__(NT) void k_tp_final(Args a)
     trace(a.ws, L, row, 15);
 }
 
+enum : int { FIN_ALL = 0, FIN_OTHERS = 1, FIN_DEFERRED = 2, FIN_REST = 3 };
+
 // One workgroup per row: merges the chunk summaries and finishes the row:
 // greedy, temperature, small top-k from the summaries; the generic re-read
 // path otherwise.  fp32 top-p rows are the k_tp_* passes'.
 template <int DT>
-__global__ __launch_bounds__(NT) void k_final(Args a)
+__global__ __launch_bounds__(NT) void k_final(Args a, int phase)
 {
     __shared__ Smem sm;
     const Layout &L = a.L;
@@ -1853,8 +1872,14 @@ __global__ __launch_bounds__(NT) void k_final(Args a)
     trace(a.ws, L, row, 16);
     __syncthreads();
     const ChunkSum *csr = reinterpret_cast<const ChunkSum *>(a.ws + L.chunks) + (size_t)row * L.G;
-    // fp32 top-p rows were finished by k_tp_final unless it left them to the generic path
-    if (DT == F32 && sm.pl.mode == M_TOPP && ldp(&ro->status) != ROW_DEFER) return;
+    // phase FIN_ALL: every row (no k_tp_* passes ran); FIN_OTHERS: every row
+    // but the fp32 top-p rows (beside the k_tp_* passes); FIN_DEFERRED: the
+    // fp32 top-p rows those passes left to the generic path; FIN_REST: both
+    const bool topp32 = DT == F32 && sm.pl.mode == M_TOPP;
+    const bool deferred = topp32 && phase != FIN_ALL && phase != FIN_OTHERS && ldp(&ro->status) == ROW_DEFER;
+    if (phase == FIN_OTHERS && topp32) return;
+    if (phase == FIN_DEFERRED && !deferred) return;
+    if (phase == FIN_REST && topp32 && !deferred) return;
     leader_row<DT>(sm, sm.cx, sm.pl, csr, ro, sm.args);
     trace(a.ws, L, row, 31);
 }
@@ -1903,6 +1928,34 @@ __global__ __launch_bounds__(NT) void k_emit(const char *__restrict__ logits, in
 
 static thread_local int g_last_hip = 0;
 
+// Per device: a second stream (default priority) and the two events that
+// fork it from the caller's stream and join it back, made on the first call
+// on that device and kept until the process ends.  Calls that overlap on one
+// device share them, as they would share a workspace: such calls race.
+struct Side { hipStream_t s; hipEvent_t fork, join; };
+constexpr int MAX_DEVICES = 64;
+static Side g_side[MAX_DEVICES];
+static std::mutex g_side_mu;
+static hipError_t side_of_current(Side **out)
+{
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= MAX_DEVICES) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lk(g_side_mu);
+    Side &sd = g_side[dev];
+    if (!sd.s) {
+        hipStream_t s = nullptr;
+        hipEvent_t f = nullptr, j = nullptr;
+        if ((e = hipStreamCreateWithFlags(&s, hipStreamNonBlocking)) != hipSuccess) return e;
+        if ((e = hipEventCreateWithFlags(&f, hipEventDisableTiming)) != hipSuccess) return e;
+        if ((e = hipEventCreateWithFlags(&j, hipEventDisableTiming)) != hipSuccess) return e;
+        sd.fork = f; sd.join = j; sd.s = s;
+    }
+    *out = &sd;
+    return hipSuccess;
+}
+
 template <int DT, int EPT>
 static hipError_t launch_sample(const Args &a, hipStream_t st)
 {
@@ -1915,7 +1968,8 @@ static hipError_t launch_sample(const Args &a, hipStream_t st)
 // and the row pass (k_tp_* + k_final), [2] after the row pass (before the
 // debug emit)
 template <int DT>
-static hipError_t launch_dt(const Args &a, float *probs, uint32_t *keep, hipStream_t st, void *const *ev)
+static hipError_t launch_dt(const Args &a, float *probs, uint32_t *keep, hipStream_t st, unsigned kinds,
+                            void *const *ev)
 {
     hipError_t e;
     if (ev && (e = hipEventRecord((hipEvent_t)ev[0], st)) != hipSuccess) return e;
@@ -1925,9 +1979,21 @@ static hipError_t launch_dt(const Args &a, float *probs, uint32_t *keep, hipStre
     }
     if (e != hipSuccess) return e;
     if (ev && (e = hipEventRecord((hipEvent_t)ev[1], st)) != hipSuccess) return e;
-    if (DT == F32) {
-        // fp32 top-p rows (the other rows' workgroups return at once)
-        const unsigned B = (unsigned)a.L.B;
+    const unsigned B = (unsigned)a.L.B;
+    if (DT == F32 && (kinds & MIS_KIND_TOPP32)) {
+        // fp32 top-p rows: the k_tp_* passes on the caller's stream.  With
+        // other rows present their row pass runs beside them on the side
+        // stream; the rows the passes deferred follow.
+        const bool side = (kinds & MIS_KIND_OTHER) != 0;
+        Side *sd = nullptr;
+        if (side) {
+            if ((e = side_of_current(&sd)) != hipSuccess) return e;
+            if ((e = hipEventRecord(sd->fork, st)) != hipSuccess) return e;
+            if ((e = hipStreamWaitEvent(sd->s, sd->fork, 0)) != hipSuccess) return e;
+            hipLaunchKernelGGL((k_final<DT>), dim3(B), dim3(NT), 0, sd->s, a, (int)FIN_OTHERS);
+            if ((e = hipGetLastError()) != hipSuccess) return e;
+            if ((e = hipEventRecord(sd->join, sd->s)) != hipSuccess) return e;
+        }
         const unsigned tg = (unsigned)(a.L.B * a.L.G < TP_GRID ? a.L.B * a.L.G : TP_GRID);
         hipLaunchKernelGGL(k_tp_prep, dim3(B), dim3(NT), 0, st, a);
         if (a.L.ept == 64) hipLaunchKernelGGL((k_tp_hist<64>), dim3(tg), dim3(NT), 0, st, a);
@@ -1937,8 +2003,11 @@ static hipError_t launch_dt(const Args &a, float *probs, uint32_t *keep, hipStre
         else hipLaunchKernelGGL((k_tp_collect<16>), dim3(tg), dim3(NT), 0, st, a);
         hipLaunchKernelGGL(k_tp_final, dim3(B), dim3(NT), 0, st, a);
         if ((e = hipGetLastError()) != hipSuccess) return e;
+        if (side && (e = hipStreamWaitEvent(st, sd->join, 0)) != hipSuccess) return e;
+        hipLaunchKernelGGL((k_final<DT>), dim3(B), dim3(NT), 0, st, a, (int)(side ? FIN_DEFERRED : FIN_REST));
+    } else {
+        hipLaunchKernelGGL((k_final<DT>), dim3(B), dim3(NT), 0, st, a, (int)FIN_ALL);
     }
-    hipLaunchKernelGGL((k_final<DT>), dim3((unsigned)a.L.B), dim3(NT), 0, st, a);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     if (ev && (e = hipEventRecord((hipEvent_t)ev[2], st)) != hipSuccess) return e;
     if (probs || keep) {
@@ -1973,7 +2042,7 @@ int mis_workspace_init(void *workspace, size_t workspace_bytes, void *stream)
 static int sample_impl(const void *logits, int dtype, int64_t B, int64_t V, int64_t row_stride,
                        const mis_row_params *params, int64_t *out_ids, int32_t *out_status, float *out_probs,
                        uint32_t *out_keep, void *workspace, size_t workspace_bytes, void *stream,
-                       void *const *events)
+                       unsigned kinds, void *const *events)
 {
     using namespace mis;
     if (dtype < 0 || dtype > 2 || B < 0 || V <= 0 || row_stride < V) return MIS_ERR_INVALID_ARG;
@@ -1996,9 +2065,9 @@ static int sample_impl(const void *logits, int dtype, int64_t B, int64_t V, int6
     a.out_status = out_status;
     hipStream_t st = (hipStream_t)stream;
     hipError_t e;
-    if (dtype == MIS_DTYPE_F32) e = launch_dt<F32>(a, out_probs, out_keep, st, events);
-    else if (dtype == MIS_DTYPE_F16) e = launch_dt<F16>(a, out_probs, out_keep, st, events);
-    else e = launch_dt<BF16>(a, out_probs, out_keep, st, events);
+    if (dtype == MIS_DTYPE_F32) e = launch_dt<F32>(a, out_probs, out_keep, st, kinds, events);
+    else if (dtype == MIS_DTYPE_F16) e = launch_dt<F16>(a, out_probs, out_keep, st, kinds, events);
+    else e = launch_dt<BF16>(a, out_probs, out_keep, st, kinds, events);
     if (e != hipSuccess) { g_last_hip = (int)e; return MIS_ERR_HIP; }
     return MIS_OK;
 }
@@ -2008,7 +2077,7 @@ int mis_sample(const void *logits, int dtype, int64_t B, int64_t V, int64_t row_
                uint32_t *out_keep, void *workspace, size_t workspace_bytes, void *stream)
 {
     return sample_impl(logits, dtype, B, V, row_stride, params, out_ids, out_status, out_probs, out_keep,
-                       workspace, workspace_bytes, stream, nullptr);
+                       workspace, workspace_bytes, stream, MIS_KIND_ALL, nullptr);
 }
 
 int mis_sample_profiled(const void *logits, int dtype, int64_t B, int64_t V, int64_t row_stride,
@@ -2018,7 +2087,18 @@ int mis_sample_profiled(const void *logits, int dtype, int64_t B, int64_t V, int
 {
     if (!events || !events[0] || !events[1] || !events[2]) return MIS_ERR_INVALID_ARG;
     return sample_impl(logits, dtype, B, V, row_stride, params, out_ids, out_status, out_probs, out_keep,
-                       workspace, workspace_bytes, stream, events);
+                       workspace, workspace_bytes, stream, MIS_KIND_ALL, events);
+}
+
+int mis_sample_ex(const void *logits, int dtype, int64_t B, int64_t V, int64_t row_stride,
+                  const mis_row_params *params, int64_t *out_ids, int32_t *out_status, float *out_probs,
+                  uint32_t *out_keep, void *workspace, size_t workspace_bytes, void *stream, unsigned kinds,
+                  void *const *events)
+{
+    if ((kinds & ~(unsigned)MIS_KIND_ALL) != 0u) return MIS_ERR_INVALID_ARG;
+    if (events && (!events[0] || !events[1] || !events[2])) return MIS_ERR_INVALID_ARG;
+    return sample_impl(logits, dtype, B, V, row_stride, params, out_ids, out_status, out_probs, out_keep,
+                       workspace, workspace_bytes, stream, kinds, events);
 }
 
 const char *mis_strerror(int code)

@@ -70,6 +70,30 @@ def host_row_params(params: Sequence[SamplingParams], dtype: torch.dtype) -> np.
     return out
 
 
+KIND_TOPP32 = _native.KIND_TOPP32
+KIND_OTHER = _native.KIND_OTHER
+
+
+def row_kinds(temperature, top_k, top_p, V: int, dtype: torch.dtype) -> int:
+    """Row-kind hint for ``mis_sample_ex`` from host-side per-row parameters
+    (sequences or arrays of floats/ints): which kinds the batch holds.  fp32
+    logits with 0 < T, top-k off (0 or >= V) and top_p < 1 are the fp32
+    top-p kind; every other row is OTHER.  Only a performance hint: the
+    results do not depend on it."""
+    t = np.asarray(temperature, dtype=np.float64).reshape(-1)
+    k = np.asarray(top_k, dtype=np.int64).reshape(-1)
+    p = np.asarray(top_p, dtype=np.float64).reshape(-1)
+    if dtype != torch.float32:
+        return KIND_OTHER if t.size else 0
+    topp = (t > 0) & ((k == 0) | (k >= V)) & (np.float32(1.0) > p.astype(np.float32)) & (p > 0)
+    kinds = 0
+    if topp.any():
+        kinds |= KIND_TOPP32
+    if (~topp).any():
+        kinds |= KIND_OTHER
+    return kinds
+
+
 def pack_params(temperature: torch.Tensor, top_k: torch.Tensor, top_p: torch.Tensor, uniform: torch.Tensor) -> torch.Tensor:
     """Device [B, 4] int32 buffer laid out as ``mis_row_params``."""
     return torch.stack([temperature.to(torch.float32).view(torch.int32), top_k.to(torch.int32),
@@ -100,11 +124,12 @@ class Sampler:
     # -- batched device entry point ---------------------------------------
     def sample_packed(self, logits: torch.Tensor, packed: torch.Tensor, *, out: torch.Tensor | None = None,
                       status_out: torch.Tensor | None = None, probs_out: torch.Tensor | None = None,
-                      keep_out: torch.Tensor | None = None, events=None) -> torch.Tensor:
+                      keep_out: torch.Tensor | None = None, events=None, kinds: int | None = None) -> torch.Tensor:
         """One launch sequence over ``logits[B, V]`` with a device ``packed``
         [B, 4] int32 parameter buffer (see ``pack_params``).  ``events``: three
         recorded ``torch.cuda.Event`` objects to time the chunk pass and the
-        finalize (see ``mis_sample_profiled``)."""
+        row pass (see ``mis_sample_profiled``).  ``kinds``: the row-kind hint
+        (``row_kinds``), None for "any"."""
         if logits.dim() != 2:
             raise ValueError("logits must be [B, V]")
         if logits.device.type != "cuda":
@@ -126,7 +151,8 @@ class Sampler:
         ptr = lambda t: None if t is None else t.data_ptr()
         evs = None if events is None else tuple(int(e.cuda_event) for e in events)
         _native.sample(logits.data_ptr(), code, B, V, logits.stride(0), packed.data_ptr(), out.data_ptr(),
-                       ptr(status_out), ptr(probs_out), ptr(keep_out), ws.data_ptr(), ws.numel(), stream, evs)
+                       ptr(status_out), ptr(probs_out), ptr(keep_out), ws.data_ptr(), ws.numel(), stream, evs,
+                       kinds=kinds)
         return out
 
     def sample_rows(self, logits: torch.Tensor, params: Sequence[SamplingParams],
@@ -138,7 +164,10 @@ class Sampler:
         dev = logits.device
         if dev.type != "cuda":
             raise _native.MisError("the MI355X sampler needs logits on a ROCm device; there is no CPU path")
-        host = torch.from_numpy(host_row_params(params, logits.dtype))
+        hp = host_row_params(params, logits.dtype)
+        host = torch.from_numpy(hp)
+        hf = hp.view(np.float32)
+        buffers.setdefault("kinds", row_kinds(hf[:, 0], hp[:, 1], hf[:, 2], logits.shape[1], logits.dtype))
         if uniforms is None:
             uniforms = torch.rand(B, device=dev, dtype=torch.float32, generator=self.generator)
         packed = torch.empty((B, 4), dtype=torch.int32, device=dev)
