@@ -120,14 +120,14 @@ struct TopChunk {
     unsigned long long mass[FH];
 };
 static_assert(sizeof(TopChunk) % 256 == 0, "TopChunk size");
-enum : uint32_t { TR_ACTIVE = 1, TR_DEFER = 2 };
+enum : uint32_t { TR_NONE = 0, TR_ACTIVE = 1, TR_DEFER = 2 };
 struct TopRow {
     uint32_t status, count;         // TR_*; survivors appended by the collect pass
     uint32_t klo, khi;              // coarse band (row keys)
     uint32_t xlo, xhi;              // its raw-key interval
-    uint32_t klo2, khi2;            // final band (row keys)
-    uint32_t xlo2, xhi2;            // its raw-key interval
-    float m, lo, scf, pad0;         // row max of y; fine-bin grid y -> (y - lo) * scf
+    int32_t ja, jb;                 // final band: fine bins [ja, jb]
+    uint32_t pad1[2];
+    float m, lo, scf, T;            // row max of y; fine-bin grid y -> (y - lo) * scf; temperature
     double S, A, fix_err;           // sum of exp(y - m), top_p * S, bound of the fixed-point sums
     double pad[22];
     double cw[G_MAX];               // per-chunk kept mass above the final band
@@ -1492,12 +1492,12 @@ __global__ __launch_bounds__(NT) void k_sample(Args a)
 //                float64 weight (dexp) to the chunk's above-mass, band
 //                elements go to FH linear fine bins (count, weight in 2^-40
 //                units of the row max's weight);
-//   k_tp_merge   one workgroup per row: merges the fine bins, finds the bins
-//                whose cumulative mass can hold the cut (exact to the
-//                fixed-point bound) and their keys, and each chunk's kept mass
-//                above them;
-//   k_tp_collect one workgroup per (row, chunk), grid-stride: appends the
-//                elements of that final band to the row's survivor list;
+//   k_tp_merge   one workgroup per row: merges the fine bins and finds the
+//                bins whose cumulative mass can hold the cut (exact to the
+//                fixed-point bound): the final band;
+//   k_tp_collect one workgroup per (row, chunk), grid-stride: the chunk's
+//                kept mass above the final band, and the band's elements
+//                appended to the row's survivor list;
 //   k_tp_final   one workgroup per row: the survivors' float64 weights, their
 //                sorted cut (window_resolve) with its decision margin checked
 //                against the error bound, then the draw.
@@ -1526,8 +1526,8 @@ __global__ __launch_bounds__(NT) void k_tp_prep(Args a)
     const Layout &L = a.L;
     const int row = blockIdx.x, tid = threadIdx.x;
     const RowPlan pl = plan_row(a.params[row], a.V);
-    if (pl.mode != M_TOPP) return;
     TopRow *tr = top_row(a, row);
+    if (pl.mode != M_TOPP) { if (tid == 0) tr->status = TR_NONE; return; }  // the later passes read only this
     const ChunkSum *csr = reinterpret_cast<const ChunkSum *>(a.ws + L.chunks) + (size_t)row * L.G;
     const RoundBuf *rbf = reinterpret_cast<const RoundBuf *>(a.ws + L.rbuf) + (size_t)row * L.G;
     const int G = L.G;
@@ -1566,9 +1566,16 @@ __global__ __launch_bounds__(NT) void k_tp_prep(Args a)
     if (ba < 0) { if (tid == 0) tr->status = TR_DEFER; return; }  // the cut lies below the coarse range
     const float cb_lo = Ar - (float)bb, cb_hi = Ar - (float)ba;
     if (wave_id() == 0) {
+        // floor(y / 2) >= c <=> y >= 2c: the band's keys in closed form,
+        // checked at both edges (a key search where the check fails)
         const uint32_t kfin = row_key(-INFINITY, F32) + 1u, ktop = 0xff7fffffu;  // finite keys
-        const uint32_t k0 = key_search(kfin, ktop, [&](uint32_t k) { return coarse_bin(f32_of_key(k)) >= cb_lo; });
-        const uint32_t k1 = key_search(kfin, ktop, [&](uint32_t k) { return coarse_bin(f32_of_key(k)) > cb_hi; }) - 1u;
+        auto ge_lo = [&](uint32_t k) { return coarse_bin(f32_of_key(k)) >= cb_lo; };
+        auto gt_hi = [&](uint32_t k) { return coarse_bin(f32_of_key(k)) > cb_hi; };
+        uint32_t k0 = key_of_f32(2.0f * cb_lo), k1 = key_of_f32(2.0f * (cb_hi + 1.0f)) - 1u;
+        const bool ok0 = k0 >= kfin && k0 <= ktop && ge_lo(k0) && (k0 == kfin || !ge_lo(k0 - 1u));
+        const bool ok1 = k1 >= kfin && k1 <= ktop && !gt_hi(k1) && (k1 == ktop || gt_hi(k1 + 1u));
+        if (!ok0) k0 = key_search(kfin, ktop, ge_lo);
+        if (!ok1) k1 = key_search(kfin, ktop, gt_hi) - 1u;
         if (lane_id() == 0) { sm.bu[5] = k0; sm.bu[6] = k1; }
     }
     __syncthreads();
@@ -1580,8 +1587,9 @@ __global__ __launch_bounds__(NT) void k_tp_prep(Args a)
     if (tid == 0) {
         const float lo = f32_of_key(klo), hi = f32_of_key(khi);
         tr->klo = klo; tr->khi = khi; tr->xlo = xlo; tr->xhi = xhi;
-        tr->m = m; tr->lo = lo; tr->scf = hi > lo ? (float)FH / (hi - lo) : 0.0f;
+        tr->m = m; tr->lo = lo; tr->scf = hi > lo ? (float)FH / (hi - lo) : 0.0f; tr->T = pl.T;
         tr->S = S; tr->A = A;
+        tr->count = 0u;
         tr->status = TR_ACTIVE;
     }
 }
@@ -1599,12 +1607,10 @@ __global__ __launch_bounds__(NT) void k_tp_hist(Args a)
     const int64_t tasks = L.B * L.G;
     for (int64_t t = blockIdx.x; t < tasks; t += gridDim.x) {
         const int row = (int)(t / L.G), g = (int)(t % L.G);
-        const RowPlan pl = plan_row(a.params[row], a.V);
-        if (pl.mode != M_TOPP) continue;
         const TopRow *tr = top_row(a, row);
         if (ldp(&tr->status) != TR_ACTIVE) continue;
         const float xlof = f32_of_key(ldp(&tr->xlo)), xhif = f32_of_key(ldp(&tr->xhi));
-        const float m = ldp(&tr->m), lo = ldp(&tr->lo), scf = ldp(&tr->scf), T = pl.T, rT = 1.0f / pl.T;
+        const float m = ldp(&tr->m), lo = ldp(&tr->lo), scf = ldp(&tr->scf), T = ldp(&tr->T), rT = 1.0f / T;
         const double md = (double)m;
         for (int b = tid; b < FH; b += NT) { cnt[b] = 0u; mass[b] = 0ull; }
         float x[EPT];
@@ -1644,8 +1650,6 @@ __global__ __launch_bounds__(NT) void k_tp_merge(Args a)
     __shared__ uint32_t bu[2];
     const Layout &L = a.L;
     const int row = blockIdx.x, tid = threadIdx.x, G = L.G;
-    const RowPlan pl = plan_row(a.params[row], a.V);
-    if (pl.mode != M_TOPP) return;
     TopRow *tr = top_row(a, row);
     if (ldp(&tr->status) != TR_ACTIVE) return;
     const double S = ldp(&tr->S), A = ldp(&tr->A);
@@ -1701,32 +1705,7 @@ __global__ __launch_bounds__(NT) void k_tp_merge(Args a)
     const int ja = bi[0], jb = bi[1];
     trace(a.ws, L, row, 8);
     if (ja < 0) { if (tid == 0) tr->status = TR_DEFER; return; }
-    const float lo = ldp(&tr->lo), scf = ldp(&tr->scf);
-    if (wave_id() == 0) {
-        const uint32_t klo = ldp(&tr->klo), khi = ldp(&tr->khi);
-        const uint32_t k0 = key_search(klo, khi, [&](uint32_t k) { return fine_bin(f32_of_key(k), lo, scf) >= ja; });
-        const uint32_t k1 = key_search(klo, khi, [&](uint32_t k) { return fine_bin(f32_of_key(k), lo, scf) > jb; }) - 1u;
-        const uint32_t x0 = x_lower<F32>(k0, pl.T), x1 = x_upper<F32>(k1, pl.T);
-        if (lane_id() == 0) {
-            tr->klo2 = k0; tr->khi2 = k1; tr->xlo2 = x0; tr->xhi2 = x1;
-            tr->fix_err = (double)bu[0] * (0.5 / FIX_ONE);
-            tr->count = 0u;
-        }
-    }
-    trace(a.ws, L, row, 9);
-    // each chunk's kept mass above the final band: its above-mass plus its
-    // fine bins above jb (one wave per chunk)
-    for (int g = wave_id(); g < G; g += NWAVE) {
-        const TopChunk *tc = top_chunk(a, row, g);
-        unsigned long long mm[FH / 64];
-#pragma unroll
-        for (int q = 0; q < FH / 64; ++q) { const int b = q * 64 + lane_id(); mm[q] = b > jb ? tc->mass[b] : 0ull; }
-        unsigned long long ms = 0ull;
-#pragma unroll
-        for (int q = 0; q < FH / 64; ++q) ms += mm[q];
-        ms = wave_sum(ms);
-        if (lane_id() == 0) tr->cw[g] = ldp(&tc->above) + (double)ms * (1.0 / FIX_ONE);
-    }
+    if (tid == 0) { tr->ja = ja; tr->jb = jb; tr->fix_err = (double)bu[0] * (0.5 / FIX_ONE); }
     trace(a.ws, L, row, 10);
 }
 
@@ -1738,22 +1717,35 @@ __global__ __launch_bounds__(NT) void k_tp_collect(Args a)
     const Layout &L = a.L;
     const int tid = threadIdx.x;
     constexpr int VEC = Traits<F32>::VEC;
+    static_assert(FH == 2 * NT, "two bins per thread");
     const int64_t tasks = L.B * L.G;
     for (int64_t t = blockIdx.x; t < tasks; t += gridDim.x) {
         const int row = (int)(t / L.G), g = (int)(t % L.G);
-        const RowPlan pl = plan_row(a.params[row], a.V);
-        if (pl.mode != M_TOPP) continue;
         TopRow *tr = top_row(a, row);
         if (ldp(&tr->status) != TR_ACTIVE) continue;
-        const float x0 = f32_of_key(ldp(&tr->xlo2)), x1 = f32_of_key(ldp(&tr->xhi2));
+        const float xlof = f32_of_key(ldp(&tr->xlo)), xhif = f32_of_key(ldp(&tr->xhi));
+        const float lo = ldp(&tr->lo), scf = ldp(&tr->scf), T = ldp(&tr->T), rT = 1.0f / T;
+        const int ja = ldp(&tr->ja), jb = ldp(&tr->jb);
         float x[EPT];
         const int64_t base = (int64_t)g * NT * EPT;
         load_chunk<F32, EPT>(a.logits + (int64_t)row * a.stride_bytes, base, a.V, a.vec_ok, x);
-        uint32_t mine = 0u;
+        // the chunk's kept mass above the final band: its above-mass plus its
+        // fine bins above jb
+        const TopChunk *tc = top_chunk(a, row, g);
+        const unsigned long long m0 = tid > jb ? tc->mass[tid] : 0ull, m1 = tid + NT > jb ? tc->mass[tid + NT] : 0ull;
+        const double cwg = block_sum<double>((double)(m0 + m1) * (1.0 / FIX_ONE), red);
+        if (tid == 0) tr->cw[g] = ldp(&tc->above) + cwg;
+        // the final band's elements: raw values in the coarse band whose fine bin is in [ja, jb]
+        uint64_t fb = 0ull;  // bit i: element i is in the final band
 #pragma unroll
-        for (int i = 0; i < EPT; ++i) mine += (x[i] >= x0 && x[i] <= x1) ? 1u : 0u;
+        for (int i = 0; i < EPT; ++i) {
+            if (x[i] >= xlof && x[i] <= xhif) {
+                const int b = fine_bin(scale_r<F32>(x[i], T, rT), lo, scf);
+                fb |= (b >= ja && b <= jb) ? (1ull << i) : 0ull;
+            }
+        }
         uint32_t total;
-        const uint32_t off = block_excl_scan<uint32_t>(mine, red, &total);
+        const uint32_t off = block_excl_scan<uint32_t>((uint32_t)__popcll(fb), red, &total);
         if (total == 0u) continue;
         if (tid == 0) base_s = atomicAdd(&tr->count, total);
         __syncthreads();
@@ -1761,10 +1753,10 @@ __global__ __launch_bounds__(NT) void k_tp_collect(Args a)
         __syncthreads();
 #pragma unroll
         for (int i = 0; i < EPT; ++i) {
-            if (x[i] >= x0 && x[i] <= x1) {
+            if (fb & (1ull << i)) {
                 if (q < (uint32_t)SURV_CAP) {
                     const int32_t j = (int32_t)(base + (((i / VEC) * NT + tid) * VEC) + (i % VEC));
-                    tr->list[q].key = row_key(scale_y<F32>(x[i], pl.T), F32);
+                    tr->list[q].key = row_key(scale_r<F32>(x[i], T, rT), F32);
                     tr->list[q].idx = j;
                 }
                 ++q;
@@ -1773,20 +1765,23 @@ __global__ __launch_bounds__(NT) void k_tp_collect(Args a)
     }
 }
 
-__global__ __launch_bounds__(NT) void k_tp_final(Args a)
+constexpr int NTF = 1024;           // threads of k_tp_final (16 waves)
+
+__global__ __launch_bounds__(NTF) void k_tp_final(Args a)
 {
     __shared__ Smem sm;
     const Layout &L = a.L;
     const int row = blockIdx.x, tid = threadIdx.x, G = L.G;
-    const RowPlan pl = plan_row(a.params[row], a.V);
-    if (pl.mode != M_TOPP) return;
     TopRow *tr = top_row(a, row);
+    const uint32_t st = ldp(&tr->status);
+    if (st == TR_NONE) return;
     RowOut *ro = reinterpret_cast<RowOut *>(a.ws + L.rowout) + row;
     const uint32_t n = ldp(&tr->count);
-    if (ldp(&tr->status) != TR_ACTIVE || n == 0u || n > (uint32_t)SURV_CAP) {
+    if (st != TR_ACTIVE || n == 0u || n > (uint32_t)SURV_CAP) {
         if (tid == 0) ro->status = ROW_DEFER;
         return;
     }
+    const RowPlan pl = plan_row(a.params[row], a.V);
     RowCx c;
     c.rowp = a.logits + (int64_t)row * a.stride_bytes;
     c.V = a.V; c.vec_ok = a.vec_ok; c.G = G; c.CH = (int64_t)NT * L.ept; c.row = row; c.T = pl.T;
@@ -1797,13 +1792,13 @@ __global__ __launch_bounds__(NT) void k_tp_final(Args a)
     exp_table(sm.etab, tid);
     __syncthreads();
     {
-        constexpr int PT = SURV_CAP / NT;
+        constexpr int PT = SURV_CAP / NTF;
         Elem el[PT];
 #pragma unroll
-        for (int q = 0; q < PT; ++q) { const int i = q * NT + tid; if (i < (int)n) el[q] = tr->list[i]; }
+        for (int q = 0; q < PT; ++q) { const int i = q * NTF + tid; if (i < (int)n) el[q] = tr->list[i]; }
 #pragma unroll
         for (int q = 0; q < PT; ++q) {
-            const int i = q * NT + tid;
+            const int i = q * NTF + tid;
             if (i < (int)n) {
                 sm.u.s.key[i] = el[q].key;
                 sm.u.s.idx[i] = el[q].idx;
@@ -1812,13 +1807,13 @@ __global__ __launch_bounds__(NT) void k_tp_final(Args a)
         }
     }
     double ab = 0.0;
-    for (int g = tid; g < G; g += NT) { const double w = ldp(&tr->cw[g]); sm.cw[g] = w; ab += w; }
-    const double above = block_sum<double>(ab, sm.red);  // (its barriers publish the survivors)
+    for (int g = tid; g < G; g += NTF) { const double w = ldp(&tr->cw[g]); sm.cw[g] = w; ab += w; }
+    const double above = block_sum<double, NTF / 64>(ab, sm.red);  // (its barriers publish the survivors)
     trace(a.ws, L, row, 12);
     uint32_t cut_key = 0u;
     int32_t cut_i = 0;
     double ql = 0.0, wl = 0.0;
-    const int rl = window_resolve(sm, n, above, A, &cut_key, &cut_i, &ql, &wl);
+    const int rl = window_resolve<NTF>(sm, n, above, A, &cut_key, &cut_i, &ql, &wl);
     // S, the above-masses and the survivors' weights carry relative errors
     // below 1e-15 each (dexp) plus float64 summation rounding; the fixed-point
     // bins above the band carry fix_err
@@ -1829,7 +1824,7 @@ __global__ __launch_bounds__(NT) void k_tp_final(Args a)
         return;
     }
     const int chsh = __builtin_ctz((unsigned)c.CH);
-    for (int q = tid; q <= rl; q += NT) {
+    for (int q = tid; q <= rl; q += NTF) {
         const int32_t j = (int32_t)(0xffffffffu - (uint32_t)sm.u.so.k[q]);
         atomicAdd(&sm.cw[j >> chsh], sm.u.so.e[q]);
     }
@@ -1839,10 +1834,10 @@ __global__ __launch_bounds__(NT) void k_tp_final(Args a)
     trace(a.ws, L, row, 14);
     int64_t id = -1;
     if (gsel >= 0) {
-        const float T = pl.T;
-        id = draw_in_chunk<F32>(sm, c, gsel, resid, [&](float xv, int64_t j) -> double {
-            const float y = scale_y<F32>(xv, T);
-            return (y != -INFINITY && kept_by_cut(row_key(y, F32), j, cut_key, cut_i)) ? exp((double)y - md) : 0.0;
+        const float T = pl.T, rT = 1.0f / pl.T;
+        id = draw_in_chunk<F32, NTF>(sm, c, gsel, resid, [&](float xv, int64_t j) -> double {
+            const float y = scale_r<F32>(xv, T, rT);
+            return (y != -INFINITY && kept_by_cut(row_key(y, F32), j, cut_key, cut_i)) ? dexp((double)y - md, sm.etab) : 0.0;
         });
     }
     write_row(ro, a, row, id, id >= 0 ? MIS_ROW_OK : MIS_ROW_INVALID, pl.mode, m, cut_key, cut_i, SK);
@@ -2001,7 +1996,7 @@ static hipError_t launch_dt(const Args &a, float *probs, uint32_t *keep, hipStre
         hipLaunchKernelGGL(k_tp_merge, dim3(B), dim3(NT), 0, st, a);
         if (a.L.ept == 64) hipLaunchKernelGGL((k_tp_collect<64>), dim3(tg), dim3(NT), 0, st, a);
         else hipLaunchKernelGGL((k_tp_collect<16>), dim3(tg), dim3(NT), 0, st, a);
-        hipLaunchKernelGGL(k_tp_final, dim3(B), dim3(NT), 0, st, a);
+        hipLaunchKernelGGL(k_tp_final, dim3(B), dim3(NTF), 0, st, a);
         if ((e = hipGetLastError()) != hipSuccess) return e;
         if (side && (e = hipStreamWaitEvent(st, sd->join, 0)) != hipSuccess) return e;
         hipLaunchKernelGGL((k_final<DT>), dim3(B), dim3(NT), 0, st, a, (int)(side ? FIN_DEFERRED : FIN_REST));
