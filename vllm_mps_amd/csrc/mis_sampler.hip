@@ -54,7 +54,7 @@ namespace mis {
 constexpr int K_SMALL = 1024;      // largest k' served by the candidate path
 constexpr int CAND_CAP = 2048;     // candidates one chunk may emit
 constexpr int SURV_CAP = 1024;     // top-k survivors / top-p window held in LDS
-constexpr int CCAP = 4096;         // small-k candidates of a row cached in LDS
+constexpr int CCAP = 8192;         // small-k candidates of a row cached in LDS (64 KB)
 constexpr int G_MAX = 256;         // chunks per row
 constexpr int CB_N = 16;           // coarse top-p bins (lane-private)
 constexpr float CB_SCALE = 0.5f;   // coarse bin = floor(y * CB_SCALE): 2 units of y
@@ -915,7 +915,7 @@ __device__ __forceinline__ bool leader_smallk(Smem &sm, const RowCx &c, const Ro
         }
         __syncthreads();
     }
-    auto cand_at = [&](uint32_t f) -> Cand { return cached ? sm.cc[f] : ldp_cand(cand_ptr(f)); };
+    trace(a.ws, a.L, c.row, 21);
     // k'-th largest raw value over the candidates: linear bins between the
     // smallest and largest candidate (values that differ spread over the bins,
     // so the LDS counters see few conflicts), then the boundary bin's
@@ -926,10 +926,21 @@ __device__ __forceinline__ bool leader_smallk(Smem &sm, const RowCx &c, const Ro
         auto for_cands = [&](auto &&fn) {
             for (uint32_t f0 = 0; f0 < ntot; f0 += NT * BATCH) {
                 float xv[BATCH];
+                if (cached) {
 #pragma unroll
-                for (int u = 0; u < BATCH; ++u) {
-                    const uint32_t f = f0 + (uint32_t)(u * NT) + threadIdx.x;
-                    xv[u] = cand_at(f < ntot ? f : 0u).x;
+                    for (int u = 0; u < BATCH; ++u) {
+                        const uint32_t f = f0 + (uint32_t)(u * NT) + threadIdx.x;
+                        xv[u] = sm.cc[f < ntot ? f : 0u].x;
+                    }
+                } else {
+                    const Cand *cp[BATCH];
+#pragma unroll
+                    for (int u = 0; u < BATCH; ++u) {
+                        const uint32_t f = f0 + (uint32_t)(u * NT) + threadIdx.x;
+                        cp[u] = cand_ptr(f < ntot ? f : 0u);
+                    }
+#pragma unroll
+                    for (int u = 0; u < BATCH; ++u) xv[u] = ldp_cand(cp[u]).x;
                 }
 #pragma unroll
                 for (int u = 0; u < BATCH; ++u)
@@ -940,6 +951,7 @@ __device__ __forceinline__ bool leader_smallk(Smem &sm, const RowCx &c, const Ro
         for_cands([&](float x) { cmin = fminf(cmin, x); cmax = fmaxf(cmax, x); });
         cmin = block_min<float>(cmin, sm.red);
         cmax = block_max<float>(cmax, sm.red);
+        trace(a.ws, a.L, c.row, 22);
         if (!(cmax > cmin)) {
             xk_thr = key_of_f32(cmax);  // every candidate holds the same value
         } else {
@@ -957,6 +969,7 @@ __device__ __forceinline__ bool leader_smallk(Smem &sm, const RowCx &c, const Ro
             __syncthreads();
             const int bsel = (int)sm.bu[0];
             const uint32_t above = sm.bu[1], nbin = sm.bu[2];
+            trace(a.ws, a.L, c.row, 23);
             if (nbin > (uint32_t)SURV_CAP || (uint32_t)pl.kk <= above) return false;
             __syncthreads();
             if (threadIdx.x == 0) sm.bu[3] = 0u;
@@ -969,6 +982,7 @@ __device__ __forceinline__ bool leader_smallk(Smem &sm, const RowCx &c, const Ro
             __syncthreads();
             const int nb = (int)min(sm.bu[3], (uint32_t)SURV_CAP);
             __syncthreads();
+            trace(a.ws, a.L, c.row, 24);
             block_sort_desc<NT, SURV_CAP>(sm.u.so.k, sm.u.so.e, nb);
             xk_thr = (uint32_t)sm.u.so.k[(int)((uint32_t)pl.kk - above) - 1];
             __syncthreads();
@@ -991,10 +1005,21 @@ __device__ __forceinline__ bool leader_smallk(Smem &sm, const RowCx &c, const Ro
     __syncthreads();
     for (uint32_t f0 = 0; f0 < ntot; f0 += NT * BATCH) {
         Cand cv[BATCH];
+        if (cached) {
 #pragma unroll
-        for (int u = 0; u < BATCH; ++u) {
-            const uint32_t f = f0 + (uint32_t)(u * NT) + threadIdx.x;
-            cv[u] = cand_at(f < ntot ? f : 0u);
+            for (int u = 0; u < BATCH; ++u) {
+                const uint32_t f = f0 + (uint32_t)(u * NT) + threadIdx.x;
+                cv[u] = sm.cc[f < ntot ? f : 0u];
+            }
+        } else {
+            const Cand *cp[BATCH];
+#pragma unroll
+            for (int u = 0; u < BATCH; ++u) {
+                const uint32_t f = f0 + (uint32_t)(u * NT) + threadIdx.x;
+                cp[u] = cand_ptr(f < ntot ? f : 0u);
+            }
+#pragma unroll
+            for (int u = 0; u < BATCH; ++u) cv[u] = ldp_cand(cp[u]);
         }
 #pragma unroll
         for (int u = 0; u < BATCH; ++u) {
