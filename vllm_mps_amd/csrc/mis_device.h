@@ -82,6 +82,36 @@ template <int DT> __device__ __forceinline__ float scale_r(float x, float T, flo
     return DT == F32 ? q : rn_dtype(q, DT);
 }
 
+// scale_r over N register values in place, with the generic division taken
+// in one wave-uniform branch for the (rare) elements that need it instead of
+// a branch per element.  N <= 64.
+template <int DT, int N> __device__ __forceinline__ void scale_all(float (&x)[N], float T, float r)
+{
+    static_assert(N <= 64, "one mask bit per element");
+    uint64_t slow = 0ull;
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        const float xi = x[i];
+        const float q0 = xi * r;
+        const float aq = fabsf(q0);
+        const bool sl = !(aq < 0x1p127f) || aq < 0x1p-100f || fabsf(xi) < 0x1p-100f;
+        const float e0 = fmaf(-q0, T, xi);
+        const float q1 = fmaf(e0, r, q0);
+        const float e1 = fmaf(-q1, T, xi);
+        x[i] = sl ? xi : fmaf(e1, r, q1);
+        slow |= sl ? (1ull << i) : 0ull;
+    }
+    if (__ballot(slow != 0ull) != 0ull) {
+#pragma unroll
+        for (int i = 0; i < N; ++i)
+            if (slow & (1ull << i)) x[i] = x[i] / T;
+    }
+    if (DT != F32) {
+#pragma unroll
+        for (int i = 0; i < N; ++i) x[i] = rn_dtype(x[i], DT);
+    }
+}
+
 // exp(y - ym) for y <= ym in binary32 with a bounded relative error: the
 // difference and its base-2 scaling are formed in binary64 (exact difference,
 // one rounding of 2^-53), split into n + f with |f| <= 1/2, and 2^f comes from

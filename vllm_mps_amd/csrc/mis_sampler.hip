@@ -54,6 +54,7 @@ namespace mis {
 constexpr int K_SMALL = 1024;      // largest k' served by the candidate path
 constexpr int CAND_CAP = 2048;     // candidates one chunk may emit
 constexpr int SURV_CAP = 1024;     // top-k survivors / top-p window held in LDS
+constexpr int EPT_DEFAULT = 32;    // elements per thread of the chunk pass (64 when G would exceed G_MAX)
 constexpr int CCAP = 8192;         // small-k candidates of a row cached in LDS (64 KB)
 constexpr int G_MAX = 256;         // chunks per row
 constexpr int CB_N = 16;           // coarse top-p bins (lane-private)
@@ -151,7 +152,7 @@ static Layout make_layout(int64_t B, int64_t V, int dtype)
     Layout L;
     L.B = B; L.V = V;
     auto chunks = [&](int ept) { return (V + (int64_t)NT * ept - 1) / ((int64_t)NT * ept); };
-    L.ept = 16;
+    L.ept = EPT_DEFAULT;
     if (chunks(L.ept) > G_MAX) L.ept = 64;
     L.G = (int)chunks(L.ept);
     const size_t BG = (size_t)B * L.G;
@@ -1383,9 +1384,25 @@ __global__ __launch_bounds__(NT) void k_sample(Args a)
             nan |= x[i] != x[i] ? 1u : 0u;
             nf += x[i] != -INFINITY ? 1u : 0u;
         }
-        const float xmax = block_max<float>(tmax, sm.red);
-        const uint32_t anynan = block_sum<uint32_t>(nan, sm.red);
-        const uint32_t nfin = block_sum<uint32_t>(nf, sm.red);
+        // chunk max, NaN count and finite count in one block reduction
+        float xmax;
+        uint32_t anynan, nfin;
+        {
+            const float wm = wave_max(tmax);
+            const uint32_t wn = wave_sum(nan), wf = wave_sum(nf);
+            if (lane_id() == 0) { sm.red.f[wave_id()] = wm; sm.red.u[wave_id()] = wn; sm.red.l[wave_id()] = (int64_t)wf; }
+            __syncthreads();
+            xmax = sm.red.f[0];
+            anynan = sm.red.u[0];
+            nfin = (uint32_t)sm.red.l[0];
+#pragma unroll
+            for (int w = 1; w < NWAVE; ++w) {
+                xmax = sm.red.f[w] > xmax ? sm.red.f[w] : xmax;
+                anynan += sm.red.u[w];
+                nfin += (uint32_t)sm.red.l[w];
+            }
+            __syncthreads();
+        }
         uint32_t flags = anynan ? FLAG_NAN : 0u;
         if (xmax != -INFINITY) {
             ymax = scale_y<DT>(xmax, pl.T);  // scaling is monotone
@@ -1414,9 +1431,10 @@ __global__ __launch_bounds__(NT) void k_sample(Args a)
             __syncthreads();
             const double ymd = (double)ymax;
             double s = 0.0;
+            scale_all<DT, EPT>(x, T, rT);  // x now holds y
 #pragma unroll
             for (int i = 0; i < EPT; ++i) {
-                const float y = scale_r<DT>(opaque(x[i]), T, rT);
+                const float y = x[i];
                 const double e = dexp((double)y - ymd, sm.etab);
                 s += e;
                 const float cb = Ac - coarse_bin(y);
@@ -1467,13 +1485,7 @@ __global__ __launch_bounds__(NT) void k_sample(Args a)
                 // close under the ties the scaling creates
                 const uint32_t sk = row_key(scale_y<DT>(f32_of_key(tkey), T), DT);
                 kc = sk;
-                if (wave_id() == 0) {
-                    const uint32_t xl = x_lower<DT>(sk, T);
-                    if (lane_id() == 0) sm.bu[3] = xl;
-                }
-                __syncthreads();
-                xlo = sm.bu[3];
-                __syncthreads();
+                xlo = x_lower<DT>(sk, T);  // every wave finds the same floor: no barrier
             }
             uint32_t mine = 0u;
 #pragma unroll
@@ -1995,6 +2007,7 @@ static hipError_t launch_dt(const Args &a, float *probs, uint32_t *keep, hipStre
     if (ev && (e = hipEventRecord((hipEvent_t)ev[0], st)) != hipSuccess) return e;
     switch (a.L.ept) {
     case 64: e = launch_sample<DT, 64>(a, st); break;
+    case 32: e = launch_sample<DT, 32>(a, st); break;
     default: e = launch_sample<DT, 16>(a, st); break;
     }
     if (e != hipSuccess) return e;
@@ -2017,9 +2030,11 @@ static hipError_t launch_dt(const Args &a, float *probs, uint32_t *keep, hipStre
         const unsigned tg = (unsigned)(a.L.B * a.L.G < TP_GRID ? a.L.B * a.L.G : TP_GRID);
         hipLaunchKernelGGL(k_tp_prep, dim3(B), dim3(NT), 0, st, a);
         if (a.L.ept == 64) hipLaunchKernelGGL((k_tp_hist<64>), dim3(tg), dim3(NT), 0, st, a);
+        else if (a.L.ept == 32) hipLaunchKernelGGL((k_tp_hist<32>), dim3(tg), dim3(NT), 0, st, a);
         else hipLaunchKernelGGL((k_tp_hist<16>), dim3(tg), dim3(NT), 0, st, a);
         hipLaunchKernelGGL(k_tp_merge, dim3(B), dim3(NT), 0, st, a);
         if (a.L.ept == 64) hipLaunchKernelGGL((k_tp_collect<64>), dim3(tg), dim3(NT), 0, st, a);
+        else if (a.L.ept == 32) hipLaunchKernelGGL((k_tp_collect<32>), dim3(tg), dim3(NT), 0, st, a);
         else hipLaunchKernelGGL((k_tp_collect<16>), dim3(tg), dim3(NT), 0, st, a);
         hipLaunchKernelGGL(k_tp_final, dim3(B), dim3(NTF), 0, st, a);
         if ((e = hipGetLastError()) != hipSuccess) return e;
