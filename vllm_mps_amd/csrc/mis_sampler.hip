@@ -347,8 +347,8 @@ __device__ __forceinline__ void write_row(RowOut *ro, const Args &a, int row, in
 // Inverse CDF inside chunk g: the first kept index whose running weight (index
 // order) exceeds `resid`; wfun(x, j) gives the weight (0 = not kept).  When
 // rounding leaves `resid` out of reach, the chunk's last kept index.
-template <int DT, int NTH = NT, class WF>
-__device__ __forceinline__ int64_t draw_in_chunk(Smem &sm, const RowCx &c, int g, double resid, WF &&wfun)
+template <int DT, int NTH = NT, class WF, class SM>
+__device__ __forceinline__ int64_t draw_in_chunk(SM &sm, const RowCx &c, int g, double resid, WF &&wfun)
 {
     // Thread t takes the contiguous elements [cbeg + t*per, cbeg + (t+1)*per)
     // of the chunk, loaded up front (16-byte vectors where aligned), so the
@@ -408,7 +408,8 @@ __device__ __forceinline__ int64_t draw_in_chunk(Smem &sm, const RowCx &c, int g
 }
 
 // Chunk holding u * sum(sm.cw) and the residual weight inside it.
-__device__ __forceinline__ void pick_chunk(Smem &sm, int G, float u, int *g_out, double *resid_out, double *S_out)
+template <class SM>
+__device__ __forceinline__ void pick_chunk(SM &sm, int G, float u, int *g_out, double *resid_out, double *S_out)
 {
     __syncthreads();
     if (wave_id() == 0) {
@@ -791,8 +792,8 @@ __device__ __forceinline__ void final_generic(Smem &sm, const RowCx &c, const Ro
 // key << 32 | ~idx, mass); the last kept element is found by a block scan.
 // Returns its sorted position, or -1 when the cut is not inside the window.
 // *q_last = mass before the last kept element, *w_last = its weight.
-template <int NTH = NT>
-__device__ __forceinline__ int window_resolve(Smem &sm, uint32_t n, double above, double A, uint32_t *cut_key, int32_t *cut_i,
+template <int NTH = NT, class SM>
+__device__ __forceinline__ int window_resolve(SM &sm, uint32_t n, double above, double A, uint32_t *cut_key, int32_t *cut_i,
                               double *q_last, double *w_last)
 {
     constexpr int PT = SURV_CAP / NTH;
@@ -830,7 +831,10 @@ __device__ __forceinline__ int window_resolve(Smem &sm, uint32_t n, double above
             run += sm.u.so.e[r];
         }
     }
-    atomicMax(&sm.bi[4], cand);
+    {
+        const int wc = wave_max(cand);  // one LDS atomic per wave
+        if (lane_id() == 0) atomicMax(&sm.bi[4], wc);
+    }
     __syncthreads();
     const int rl = sm.bi[4];
     if (rl >= 0 && cand == rl) sm.bd[5] = qc;
@@ -1255,8 +1259,8 @@ __device__ __forceinline__ void leader_row(Smem &sm, RowCx &c, const RowPlan &pl
 // Per-chunk scale factors exp(ymax_c - m) into sm.chs; returns the row max m
 // and whether any chunk flagged NaN / +inf.  One load pair per chunk and
 // thread, issued together.
-template <int NTH = NT>
-__device__ __forceinline__ float row_scales(Smem &sm, const ChunkSum *csr, int G, uint32_t *bad)
+template <int NTH = NT, class SM>
+__device__ __forceinline__ float row_scales(SM &sm, const ChunkSum *csr, int G, uint32_t *bad)
 {
     uint32_t anyflag = 0u;
     float m = -INFINITY;
@@ -1542,6 +1546,24 @@ __global__ __launch_bounds__(NT) void k_sample(Args a)
 // (RowOut status ROW_DEFER).
 
 constexpr int ROW_DEFER = 16;       // RowOut status: k_final's generic path finishes the row
+
+// LDS of the top-p per-row kernels: only what their steps use (the row
+// pass's Smem also caches small-k candidates)
+struct TopRowSmem {
+    union {
+        struct { uint32_t key[SURV_CAP]; int32_t idx[SURV_CAP]; double e[SURV_CAP]; } s;
+        struct { uint64_t k[SURV_CAP]; double e[SURV_CAP]; } so;
+    } u;
+    union { double coarse[CB_N]; } v;
+    double cw[G_MAX];
+    double chs[G_MAX];
+    double etab[ETAB_N];
+    Red red;
+    uint32_t bu[8];
+    int32_t bi[8];
+    double bd[8];
+    unsigned long long bq[2];
+};
 constexpr int TP_GRID = 2048;       // workgroups of the grid-stride passes
 
 __device__ __forceinline__ TopRow *top_row(const Args &a, int row)
@@ -1559,7 +1581,7 @@ __device__ __forceinline__ int fine_bin(float y, float lo, float scf)
 
 __global__ __launch_bounds__(NT) void k_tp_prep(Args a)
 {
-    __shared__ Smem sm;
+    __shared__ TopRowSmem sm;
     const Layout &L = a.L;
     const int row = blockIdx.x, tid = threadIdx.x;
     const RowPlan pl = plan_row(a.params[row], a.V);
@@ -1806,7 +1828,7 @@ constexpr int NTF = 1024;           // threads of k_tp_final (16 waves)
 
 __global__ __launch_bounds__(NTF) void k_tp_final(Args a)
 {
-    __shared__ Smem sm;
+    __shared__ TopRowSmem sm;
     const Layout &L = a.L;
     const int row = blockIdx.x, tid = threadIdx.x, G = L.G;
     TopRow *tr = top_row(a, row);
