@@ -59,8 +59,8 @@ constexpr int CCAP = 8192;         // small-k candidates of a row cached in LDS 
 constexpr int G_MAX = 256;         // chunks per row
 constexpr int CB_N = 16;           // coarse top-p bins (lane-private)
 constexpr float CB_SCALE = 0.5f;   // coarse bin = floor(y * CB_SCALE): 2 units of y
-constexpr int REGION_BINS = 1;     // L1 bins per 16-bit chain pass (re-read path)
-constexpr int RUN_CAP = REGION_BINS * 256;
+constexpr int REGION_MAX = 16;     // L1 bins per 16-bit chain pass at most (re-read path)
+constexpr int RUN_CAP = REGION_MAX * 256;
 constexpr int TIE_CAP = 1024;
 constexpr uint32_t NCAND_OVERFLOW = 0xffffffffu;
 constexpr int32_t IDX_ALL = 0x7fffffff;
@@ -245,7 +245,6 @@ struct Smem {
         struct { uint32_t cnt[256]; double mass[256]; } h8;                                 // 3 KB
         struct { uint32_t key[SURV_CAP]; int32_t idx[SURV_CAP]; double e[SURV_CAP]; } s;    // 16 KB
         struct { uint64_t k[SURV_CAP]; double e[SURV_CAP]; } so;                           // 16 KB
-        struct { uint32_t cnt[RUN_CAP]; uint32_t rkey[RUN_CAP]; uint32_t rcnt[RUN_CAP]; float rp[RUN_CAP]; } r;
         struct { int32_t idx[TIE_CAP]; } t;
     } u;
     union {
@@ -254,7 +253,10 @@ struct Smem {
     } v;
     double cw[G_MAX];          // per-chunk kept weight
     double etab[ETAB_N];       // 2^(j/64) for dexp
-    Cand cc[CCAP];             // a small-k row's candidates
+    union {
+        Cand cc[CCAP];         // a small-k row's candidates
+        struct { uint32_t cnt[RUN_CAP]; uint32_t rkey[RUN_CAP]; uint32_t rcnt[RUN_CAP]; float rp[RUN_CAP]; } r;  // 16-bit chain runs
+    } w;
     double chs[G_MAX];         // per-chunk rescale to the row max
     double sub_m[256];         // round-local histograms
     uint32_t sub_c[256];
@@ -637,11 +639,20 @@ __device__ __forceinline__ void topp_cut_generic(Smem &sm, const RowCx &c, float
     while (b_hi >= 0 && sm.v.l1.cnt[b_hi] == 0u) --b_hi;
     uint32_t prev_key = 0u;
     bool have_prev = false;
+    double walked = 0.0;  // mass of the L1 bins above b_hi
     while (b_hi >= 0) {
-        int b_lo = b_hi - REGION_BINS + 1;
-        if (b_lo < 0) b_lo = 0;
+        // a region of L1 bins whose mass (float64) reaches past top_p with a
+        // margin for the chain's rounding, at most REGION_MAX bins: one re-read
+        // usually holds the cut; if not, the next region follows
+        int b_lo = b_hi;
+        double reach = walked + sm.v.l1.mass[b_hi];
+        while (b_lo > 0 && b_hi - b_lo + 1 < REGION_MAX && reach < ((double)top_p + 0.02) * S) {
+            --b_lo;
+            reach += sm.v.l1.mass[b_lo];
+        }
+        const int npos = (b_hi - b_lo + 1) * 256;
         __syncthreads();
-        for (int i = threadIdx.x; i < RUN_CAP; i += NT) sm.u.r.cnt[i] = 0u;
+        for (int i = threadIdx.x; i < npos; i += NT) sm.w.r.cnt[i] = 0u;
         uint32_t klo = (uint32_t)b_lo << 24;
         const uint32_t khi = ((uint32_t)b_hi << 24) | 0x00ffffffu;
         if (klo < floor_key) klo = floor_key;
@@ -651,23 +662,22 @@ __device__ __forceinline__ void topp_cut_generic(Smem &sm, const RowCx &c, float
         rescan<DT>(c, xlo, xhi, [&](int64_t, float, uint32_t key) {
             if (key < klo || key > khi) return;
             const uint32_t pos = (uint32_t)(b_hi - (int)(key >> 24)) * 256u + (255u - ((key >> 16) & 255u));
-            atomicAdd(&sm.u.r.cnt[pos], 1u);
+            atomicAdd(&sm.w.r.cnt[pos], 1u);
         });
         __syncthreads();
-        const int npos = (b_hi - b_lo + 1) * 256;
         int nruns_total = 0;
         for (int i0 = 0; i0 < npos; i0 += NT) {
             const int i = i0 + threadIdx.x;
-            const uint32_t cnt = i < npos ? sm.u.r.cnt[i] : 0u;
+            const uint32_t cnt = i < npos ? sm.w.r.cnt[i] : 0u;
             uint32_t tot;
             const uint32_t off = block_excl_scan<uint32_t>(cnt ? 1u : 0u, sm.red, &tot);
             if (cnt) {
                 const uint32_t L1 = (uint32_t)(b_hi - i / 256), b2 = 255u - (uint32_t)(i % 256);
                 const uint32_t key = (L1 << 24) | (b2 << 16);
                 const int r = nruns_total + (int)off;
-                sm.u.r.rkey[r] = key;
-                sm.u.r.rcnt[r] = cnt;
-                sm.u.r.rp[r] = rn_dtype((float)(exp((double)value_of_row_key(key, DT) - md) / S), DT);
+                sm.w.r.rkey[r] = key;
+                sm.w.r.rcnt[r] = cnt;
+                sm.w.r.rp[r] = rn_dtype((float)(exp((double)value_of_row_key(key, DT) - md) / S), DT);
             }
             nruns_total += (int)tot;
         }
@@ -676,15 +686,15 @@ __device__ __forceinline__ void topp_cut_generic(Smem &sm, const RowCx &c, float
             int run_at = -1;
             uint32_t tk = 0;
             float Fw = F;
-            const bool found = chain_walk(sm.u.r.rcnt, sm.u.r.rp, nruns_total, Fw, thr16, DT, &run_at, &tk);
+            const bool found = chain_walk(sm.w.r.rcnt, sm.w.r.rp, nruns_total, Fw, thr16, DT, &run_at, &tk);
             sm.bi[1] = found ? 1 : 0;
             sm.bu[0] = tk;
             sm.bf[0] = Fw;
-            sm.bu[1] = nruns_total > 0 ? sm.u.r.rkey[nruns_total - 1] : 0u;
+            sm.bu[1] = nruns_total > 0 ? sm.w.r.rkey[nruns_total - 1] : 0u;
             if (found) {
-                sm.bu[2] = sm.u.r.rkey[run_at];
-                sm.bu[3] = sm.u.r.rcnt[run_at];
-                sm.bu[4] = run_at > 0 ? sm.u.r.rkey[run_at - 1] : 0u;
+                sm.bu[2] = sm.w.r.rkey[run_at];
+                sm.bu[3] = sm.w.r.rcnt[run_at];
+                sm.bu[4] = run_at > 0 ? sm.w.r.rkey[run_at - 1] : 0u;
                 sm.bi[3] = run_at > 0 ? 1 : 0;
             }
         }
@@ -708,6 +718,7 @@ __device__ __forceinline__ void topp_cut_generic(Smem &sm, const RowCx &c, float
         }
         F = sm.bf[0];
         if (nruns_total > 0) { prev_key = sm.bu[1]; have_prev = true; }
+        for (int b = b_lo; b <= b_hi; ++b) walked += sm.v.l1.mass[b];
         __syncthreads();
         b_hi = b_lo - 1;
         while (b_hi >= 0 && sm.v.l1.cnt[b_hi] == 0u) --b_hi;
@@ -915,7 +926,7 @@ __device__ __forceinline__ bool leader_smallk(Smem &sm, const RowCx &c, const Ro
 #pragma unroll
             for (int u = 0; u < BATCH; ++u) {
                 const uint32_t f = f0 + (uint32_t)(u * NT) + threadIdx.x;
-                if (f < ntot) sm.cc[f] = cv[u];
+                if (f < ntot) sm.w.cc[f] = cv[u];
             }
         }
         __syncthreads();
@@ -935,7 +946,7 @@ __device__ __forceinline__ bool leader_smallk(Smem &sm, const RowCx &c, const Ro
 #pragma unroll
                     for (int u = 0; u < BATCH; ++u) {
                         const uint32_t f = f0 + (uint32_t)(u * NT) + threadIdx.x;
-                        xv[u] = sm.cc[f < ntot ? f : 0u].x;
+                        xv[u] = sm.w.cc[f < ntot ? f : 0u].x;
                     }
                 } else {
                     const Cand *cp[BATCH];
@@ -1014,7 +1025,7 @@ __device__ __forceinline__ bool leader_smallk(Smem &sm, const RowCx &c, const Ro
 #pragma unroll
             for (int u = 0; u < BATCH; ++u) {
                 const uint32_t f = f0 + (uint32_t)(u * NT) + threadIdx.x;
-                cv[u] = sm.cc[f < ntot ? f : 0u];
+                cv[u] = sm.w.cc[f < ntot ? f : 0u];
             }
         } else {
             const Cand *cp[BATCH];
