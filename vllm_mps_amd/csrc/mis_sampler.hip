@@ -41,6 +41,7 @@
 // (fp32 rows) or torch's 16-bit rounding chain (fp16/bf16 rows); the draw is
 // min{i : sum_{j<=i} w_j > u * sum w} over the kept weights w = exp(y - m).
 #include <hip/hip_runtime.h>
+#include <float.h>
 #include <math.h>
 #include <stdint.h>
 
@@ -1397,7 +1398,10 @@ __global__ __launch_bounds__(NT) void k_sample(Args a)
         for (int i = 0; i < EPT; ++i) {
             tmax = fmaxf(tmax, x[i]);
             nan |= x[i] != x[i] ? 1u : 0u;
-            nf += x[i] != -INFINITY ? 1u : 0u;
+        }
+        if (pl.mode == M_SMALLK) {  // the finite count only small-k rows use
+#pragma unroll
+            for (int i = 0; i < EPT; ++i) nf += x[i] != -INFINITY ? 1u : 0u;
         }
         // chunk max, NaN count and finite count in one block reduction
         float xmax;
@@ -1502,16 +1506,19 @@ __global__ __launch_bounds__(NT) void k_sample(Args a)
                 kc = sk;
                 xlo = x_lower<DT>(sk, T);  // every wave finds the same floor: no barrier
             }
+            // the floor as a raw value: x >= xlof <=> key(x) >= xlo for every
+            // finite x (zeros share a key); -inf never passes
+            const float xlof = xlo > key_of_f32(-INFINITY) ? f32_of_key(xlo) : -FLT_MAX;
             uint32_t mine = 0u;
 #pragma unroll
-            for (int i = 0; i < EPT; ++i) mine += (x[i] != -INFINITY && key_of_f32(x[i]) >= xlo) ? 1u : 0u;
+            for (int i = 0; i < EPT; ++i) mine += x[i] >= xlof ? 1u : 0u;
             uint32_t total;
             uint32_t off = block_excl_scan<uint32_t>(mine, sm.red, &total);
             if (total <= (uint32_t)CAND_CAP) {
                 Cand *cand = reinterpret_cast<Cand *>(a.ws + L.cand) + ((size_t)row * G + chunk) * CAND_CAP;
 #pragma unroll
                 for (int i = 0; i < EPT; ++i)
-                    if (x[i] != -INFINITY && key_of_f32(x[i]) >= xlo) {
+                    if (x[i] >= xlof) {
                         cand[off].x = x[i];
                         cand[off].idx = idx_of(i);
                         ++off;
