@@ -163,6 +163,16 @@ def test_topp_f32_refinement_rounds(scale, device):
     _run(f"topp rounds scale={scale}", w, device)
 
 
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_large_vocab_64_per_thread(dtype, device):
+    """V = 2,200,000 needs more than 256 chunks of 8192: the chunk pass runs
+    64 elements per thread (chunks of 16384) and so do the top-p passes."""
+    B, V = 5, 2_200_000
+    w = H.synthetic(dtype, B, V, seed=55, temperature=[0.0, 1.0, 1.0, 0.8, 1.2], top_k=[0, 0, 100, 0, 0],
+                    top_p=[1.0, 0.9, 1.0, 1.0, 0.5] if dtype == "f32" else [1.0, 1.0, 0.9, 1.0, 1.0], scale=2.0)
+    _run(f"large V {dtype}", w, device, debug=False)
+
+
 def test_topp_f32_all_equal(device):
     """Every logit equal: staging and window buffers overflow, the row falls
     back to the re-read path; the keep set is the lowest indices."""
