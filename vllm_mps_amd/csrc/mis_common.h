@@ -165,6 +165,10 @@ MIS_HD void binade_of(float F, double *ulp, double *top)
 MIS_HD float chain_add_n(float F, float p, uint64_t n)
 {
     if (p == 0.0f) return F;
+    if (n <= 8u) {  // short runs: the additions themselves (cheaper than the closed form)
+        for (uint64_t i = 0; i < n; ++i) F = F + p;
+        return F;
+    }
     while (n > 0) {
         if (F == 0.0f) { F = p; n -= 1; continue; }
         double u, top;
