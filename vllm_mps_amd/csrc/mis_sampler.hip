@@ -1103,30 +1103,42 @@ __device__ __forceinline__ bool leader_smallk(Smem &sm, const RowCx &c, const Ro
             }
             __syncthreads();
             block_sort_desc<NT, SURV_CAP>(sm.u.so.k, sm.u.so.e, (int)ns);
+            // runs of equal keys in sorted order, their probabilities and
+            // lengths, computed in parallel (the candidates' cache is free
+            // again); then one thread walks the chain over the runs
+            {
+                uint32_t st[PT];
+#pragma unroll
+                for (int q = 0; q < PT; ++q) {
+                    const int i = threadIdx.x * PT + q;
+                    st[q] = i < (int)ns && (i == 0 || (uint32_t)(sm.u.so.k[i] >> 32) != (uint32_t)(sm.u.so.k[i - 1] >> 32)) ? 1u : 0u;
+                }
+                uint32_t nr;
+                uint32_t r = block_excl_scan<uint32_t>(st[0] + st[1] + st[2] + st[3], sm.red, &nr);
+#pragma unroll
+                for (int q = 0; q < PT; ++q) {
+                    const int i = threadIdx.x * PT + q;
+                    if (st[q]) {
+                        sm.w.r.rkey[r] = (uint32_t)i;  // the run's first sorted position
+                        sm.w.r.rp[r] = rn_dtype((float)(sm.u.so.e[i] / S), DT);
+                        ++r;
+                    }
+                }
+                __syncthreads();
+                for (uint32_t q = threadIdx.x; q < nr; q += NT)
+                    sm.w.r.rcnt[q] = (q + 1 < nr ? sm.w.r.rkey[q + 1] : ns) - sm.w.r.rkey[q];
+                if (threadIdx.x == 0) sm.bu[2] = nr;
+                __syncthreads();
+            }
+            static_assert(PT == 4, "four survivors per thread");
             if (threadIdx.x == 0) {
                 const float thr16 = rn_dtype(pl.top_p, DT);
                 float F = 0.0f;
                 uint32_t r0 = ns;
-                int i = 0;
-                while (i < (int)ns) {
-                    const uint32_t key = (uint32_t)(sm.u.so.k[i] >> 32);
-                    int jn = i + 1;
-                    while (jn < (int)ns && (uint32_t)(sm.u.so.k[jn] >> 32) == key) ++jn;
-                    const float p = rn_dtype((float)(sm.u.so.e[i] / S), DT);
-                    const uint32_t n = (uint32_t)(jn - i);
-                    const float Fend = chain_add_n(F, p, n);
-                    if (chain_E(Fend, p, DT) >= thr16) {
-                        uint32_t lo = 0, hi = n - 1;
-                        while (lo < hi) {
-                            const uint32_t mid = lo + (hi - lo) / 2;
-                            if (chain_E(chain_add_n(F, p, (uint64_t)mid + 1), p, DT) >= thr16) hi = mid; else lo = mid + 1;
-                        }
-                        r0 = (uint32_t)i + lo;
-                        break;
-                    }
-                    F = Fend;
-                    i = jn;
-                }
+                int run_at = -1;
+                uint32_t tk = 0;
+                if (chain_walk(sm.w.r.rcnt, sm.w.r.rp, (int)sm.bu[2], F, thr16, DT, &run_at, &tk))
+                    r0 = sm.w.r.rkey[run_at] + tk;
                 sm.bu[0] = r0;
                 if (r0 > 0) {
                     const uint64_t q = sm.u.so.k[r0 - 1];
