@@ -55,6 +55,8 @@ namespace mis {
 constexpr int K_SMALL = 1024;      // largest k' served by the candidate path
 constexpr int CAND_CAP = 2048;     // candidates one chunk may emit
 constexpr int SURV_CAP = 1024;     // top-k survivors / top-p window held in LDS
+constexpr int K_PROBE = 512;       // fp16/bf16 top-p rows look for their cut among this many largest values
+                                   // first (ties at the last one stay within SURV_CAP)
 constexpr int EPT_DEFAULT = 32;    // elements per thread of the chunk pass (64 when G would exceed G_MAX)
 constexpr int CCAP = 8192;         // small-k candidates of a row cached in LDS (64 KB)
 constexpr int G_MAX = 256;         // chunks per row
@@ -868,9 +870,13 @@ __device__ __forceinline__ int window_resolve(SM &sm, uint32_t n, double above, 
 // overflowed its candidate buffer, when a truncated chunk may hide an element
 // at or above the k'-th value, or when the survivors overflow LDS.
 template <int DT>
+// S_row >= 0: an fp16/bf16 top-p row probing its cut among its kk = K_PROBE
+// largest values: the chain's probabilities divide by the row's S_row, and a
+// cut not reached among them returns false (the generic path takes the row).
 __device__ __forceinline__ bool leader_smallk(Smem &sm, const RowCx &c, const RowPlan &pl, const ChunkSum *cs,
-                                          const Cand *cand, RowOut *ro, const Args &a)
+                                          const Cand *cand, RowOut *ro, const Args &a, double S_row = -1.0)
 {
+    const bool probe = S_row >= 0.0;
     const double md = (double)c.m;
     // candidate counts -> prefix offsets (thread 0, G <= 256); candidate f of
     // the row is candidate f - pre[g] of the chunk g with pre[g] <= f < pre[g+1]
@@ -1061,6 +1067,7 @@ __device__ __forceinline__ bool leader_smallk(Smem &sm, const RowCx &c, const Ro
         double S = 0.0;
         for (uint32_t i = threadIdx.x; i < ns; i += NT) S += sm.u.s.e[i];
         S = block_sum<double>(S, sm.red);
+        if (probe) S = S_row;
         if (DT == F32) {
             // exact masses over the survivors: sorted cut, then back to the
             // (key, idx, e) view the draw reads
@@ -1137,9 +1144,10 @@ __device__ __forceinline__ bool leader_smallk(Smem &sm, const RowCx &c, const Ro
                 uint32_t r0 = ns;
                 int run_at = -1;
                 uint32_t tk = 0;
-                if (chain_walk(sm.w.r.rcnt, sm.w.r.rp, (int)sm.bu[2], F, thr16, DT, &run_at, &tk))
-                    r0 = sm.w.r.rkey[run_at] + tk;
+                const bool found = chain_walk(sm.w.r.rcnt, sm.w.r.rp, (int)sm.bu[2], F, thr16, DT, &run_at, &tk);
+                if (found) r0 = sm.w.r.rkey[run_at] + tk;
                 sm.bu[0] = r0;
+                sm.bi[1] = found ? 1 : 0;
                 if (r0 > 0) {
                     const uint64_t q = sm.u.so.k[r0 - 1];
                     sm.bu[1] = (uint32_t)(q >> 32);
@@ -1148,8 +1156,10 @@ __device__ __forceinline__ bool leader_smallk(Smem &sm, const RowCx &c, const Ro
             }
             __syncthreads();
             const uint32_t r0 = sm.bu[0];
+            const bool found = sm.bi[1] != 0;
             if (r0 > 0) { cut_key = sm.bu[1]; cut_i = sm.bi[0]; }
             __syncthreads();
+            if (probe && !found) return false;  // the cut lies below the K_PROBE largest
             if (r0 == 0) status = MIS_ROW_INVALID;
             for (int q = 0; q < PT; ++q) {               // back to the (key, idx, e) view
                 const int i = threadIdx.x + q * NT;
@@ -1275,6 +1285,18 @@ __device__ __forceinline__ void leader_row(Smem &sm, RowCx &c, const RowPlan &pl
     } else if (pl.mode == M_SMALLK) {
         const Cand *cand = reinterpret_cast<const Cand *>(a.ws + L.cand) + (size_t)row * L.G * CAND_CAP;
         if (!leader_smallk<DT>(sm, c, pl, csr, cand, ro, a)) final_generic<DT>(sm, c, pl, ro, a);
+    } else if (DT != F32 && pl.mode == M_TOPP) {
+        // the cut among the row's K_PROBE largest values first
+        double s = 0.0;
+        for (int g = tid; g < L.G; g += NT) {
+            const float yg = ldp(&csr[g].ymax);
+            s += yg == -INFINITY ? 0.0 : ldp(&csr[g].S) * exp((double)yg - md);
+        }
+        const double S_row = block_sum<double>(s, sm.red);
+        RowPlan pk = pl;
+        pk.kk = (int)(c.V < (int64_t)K_PROBE ? c.V : (int64_t)K_PROBE);
+        const Cand *cand = reinterpret_cast<const Cand *>(a.ws + L.cand) + (size_t)row * L.G * CAND_CAP;
+        if (!leader_smallk<DT>(sm, c, pk, csr, cand, ro, a, S_row)) final_generic<DT>(sm, c, pl, ro, a);
     } else {
         final_generic<DT>(sm, c, pl, ro, a);
     }
@@ -1411,7 +1433,10 @@ __global__ __launch_bounds__(NT) void k_sample(Args a)
             tmax = fmaxf(tmax, x[i]);
             nan |= x[i] != x[i] ? 1u : 0u;
         }
-        if (pl.mode == M_SMALLK) {  // the finite count only small-k rows use
+        // fp16/bf16 top-p rows first try their cut among the row's K_PROBE
+        // largest values: the chunk pass also emits those candidates
+        const bool topp16 = DT != F32 && pl.mode == M_TOPP;
+        if (pl.mode == M_SMALLK || topp16) {  // the finite count only candidate rows use
 #pragma unroll
             for (int i = 0; i < EPT; ++i) nf += x[i] != -INFINITY ? 1u : 0u;
         }
@@ -1482,10 +1507,22 @@ __global__ __launch_bounds__(NT) void k_sample(Args a)
                 if (q == 0) rb->coarse[b] = t;
             }
             if (tid == 0) rb->S = Sc;
-        } else if (live && pl.mode == M_SMALLK) {
+        }
+        if (live && topp16) {
+            // S in float64 from dexp: the row pass's probabilities are
+            // rounded to the dtype, so S must be exact well below its ulp
+            exp_table(sm.etab, tid);
+            __syncthreads();
+            const double ymd = (double)ymax;
+            double s = 0.0;
+#pragma unroll
+            for (int i = 0; i < EPT; ++i) s += dexp((double)scale_r<DT>(x[i], T, rT) - ymd, sm.etab);
+            Sc = block_sum<double>(s, sm.red);
+        }
+        if (live && (pl.mode == M_SMALLK || topp16)) {
             // ---- candidates: every finite x whose scaled key reaches a threshold
             // taken from the per-thread maxima, enough for n_c candidates
-            const uint32_t kk = (uint32_t)pl.kk;
+            const uint32_t kk = topp16 ? (uint32_t)(a.V < (int64_t)K_PROBE ? a.V : (int64_t)K_PROBE) : (uint32_t)pl.kk;
             uint32_t nc = G == 1 ? kk : 2u * ((kk + (uint32_t)G - 1u) / (uint32_t)G) + 32u;
             if (nc > kk) nc = kk;
             uint32_t xlo = 0u;  // raw-key floor of the candidates
