@@ -1507,19 +1507,20 @@ __global__ __launch_bounds__(NT) void k_sample(Args a)
                 if (q == 0) rb->coarse[b] = t;
             }
             if (tid == 0) rb->S = Sc;
-        }
-        if (live && topp16) {
-            // S in float64 from dexp: the row pass's probabilities are
-            // rounded to the dtype, so S must be exact well below its ulp
-            exp_table(sm.etab, tid);
-            __syncthreads();
-            const double ymd = (double)ymax;
-            double s = 0.0;
+        } else if (live && (pl.mode == M_SMALLK || topp16)) {
+            // (one else-if chain: separate branches here cost the fp32 kernel
+            // 70 more VGPRs, half its occupancy)
+            if (topp16) {
+                // S in float64 from dexp: the row pass's probabilities are
+                // rounded to the dtype, so S must be exact well below its ulp
+                exp_table(sm.etab, tid);
+                __syncthreads();
+                const double ymd = (double)ymax;
+                double s = 0.0;
 #pragma unroll
-            for (int i = 0; i < EPT; ++i) s += dexp((double)scale_r<DT>(x[i], T, rT) - ymd, sm.etab);
-            Sc = block_sum<double>(s, sm.red);
-        }
-        if (live && (pl.mode == M_SMALLK || topp16)) {
+                for (int i = 0; i < EPT; ++i) s += dexp((double)scale_r<DT>(x[i], T, rT) - ymd, sm.etab);
+                Sc = block_sum<double>(s, sm.red);
+            }
             // ---- candidates: every finite x whose scaled key reaches a threshold
             // taken from the per-thread maxima, enough for n_c candidates
             const uint32_t kk = topp16 ? (uint32_t)(a.V < (int64_t)K_PROBE ? a.V : (int64_t)K_PROBE) : (uint32_t)pl.kk;
