@@ -194,3 +194,14 @@ def test_repeat_deterministic(device):
         if first is None:
             first = g
         assert np.array_equal(g["ids"], first["ids"]) and np.array_equal(g["status"], first["status"])
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+@pytest.mark.parametrize("V", [4096, 50000])
+def test_topp16_rounding_near_midpoint(dtype, V, device):
+    """fp16/bf16 top-p rows whose largest probability sits within a few 1e-7
+    of a rounding midpoint: the chunk pass's float32-exp S cannot decide that
+    rounding, so the row pass must take S exactly before walking the chain."""
+    offs = [3e-7, -3e-7, 6e-7, -6e-7, 1e-7, -1e-7, 8e-7, -8e-7, 2e-6, -2e-6]
+    w = H.near_midpoint(dtype, V, offs, seed=11 + V)
+    _run(f"topp16 near midpoint V={V}", w, device)

@@ -321,6 +321,19 @@ def test_bf16_top_p_001_closed_form():
         assert r["n_kept"][b] == n
 
 
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+def test_topp16_near_midpoint_closed_form(dtype):
+    """Largest probability 1/S a few 1e-7 above (below) a midpoint M of two
+    neighbouring dtype values b1 < b2, top_p = b2: it rounds up to b2 (down
+    to b1) exactly when the offset is positive, so rank 0 alone reaches
+    top_p (rank 1 is kept as well)."""
+    offs = [3e-7, -3e-7, 1e-7, -1e-7, 8e-7, -8e-7]
+    w = H.near_midpoint(dtype, 4096, offs, seed=3)
+    r = run(w)
+    for b, off in enumerate(offs):
+        assert r["n_kept"][b] == (1 if off > 0 else 2), (b, off)
+
+
 # ------------------------------------------------------------------ golden
 
 def test_workload_digests():

@@ -873,8 +873,13 @@ template <int DT>
 // S_row >= 0: an fp16/bf16 top-p row probing its cut among its kk = K_PROBE
 // largest values: the chain's probabilities divide by the row's S_row, and a
 // cut not reached among them returns false (the generic path takes the row).
+// S_tol > 0: S_row's relative error bound; when a run at or above the cut has
+// a rounded probability that some S within it would round differently, the
+// call sets *ambig and returns false without output (the caller retries with
+// an exact S).
 __device__ __forceinline__ bool leader_smallk(Smem &sm, const RowCx &c, const RowPlan &pl, const ChunkSum *cs,
-                                          const Cand *cand, RowOut *ro, const Args &a, double S_row = -1.0)
+                                          const Cand *cand, RowOut *ro, const Args &a, double S_row = -1.0,
+                                          double S_tol = 0.0, bool *ambig = nullptr)
 {
     const bool probe = S_row >= 0.0;
     const double md = (double)c.m;
@@ -1113,6 +1118,7 @@ __device__ __forceinline__ bool leader_smallk(Smem &sm, const RowCx &c, const Ro
             // runs of equal keys in sorted order, their probabilities and
             // lengths, computed in parallel (the candidates' cache is free
             // again); then one thread walks the chain over the runs
+            uint32_t amb = 0xffffffffu;  // first run whose rounding S's error bound leaves open
             {
                 uint32_t st[PT];
 #pragma unroll
@@ -1127,11 +1133,19 @@ __device__ __forceinline__ bool leader_smallk(Smem &sm, const RowCx &c, const Ro
                     const int i = threadIdx.x * PT + q;
                     if (st[q]) {
                         sm.w.r.rkey[r] = (uint32_t)i;  // the run's first sorted position
-                        sm.w.r.rp[r] = rn_dtype((float)(sm.u.so.e[i] / S), DT);
+                        const double e = sm.u.so.e[i];
+                        const float pr = rn_dtype((float)(e / S), DT);
+                        sm.w.r.rp[r] = pr;
+                        // every rounding step is monotone: equal roundings at
+                        // both ends of the interval fix the value inside it
+                        if (S_tol > 0.0 && (rn_dtype((float)(e / (S * (1.0 + S_tol))), DT) != pr ||
+                                            rn_dtype((float)(e / (S * (1.0 - S_tol))), DT) != pr))
+                            amb = r < amb ? r : amb;
                         ++r;
                     }
                 }
-                __syncthreads();
+                if (S_tol > 0.0) amb = block_min<uint32_t>(amb, sm.red);  // its barriers order the runs
+                else __syncthreads();
                 for (uint32_t q = threadIdx.x; q < nr; q += NT)
                     sm.w.r.rcnt[q] = (q + 1 < nr ? sm.w.r.rkey[q + 1] : ns) - sm.w.r.rkey[q];
                 if (threadIdx.x == 0) sm.bu[2] = nr;
@@ -1148,6 +1162,7 @@ __device__ __forceinline__ bool leader_smallk(Smem &sm, const RowCx &c, const Ro
                 if (found) r0 = sm.w.r.rkey[run_at] + tk;
                 sm.bu[0] = r0;
                 sm.bi[1] = found ? 1 : 0;
+                sm.bi[2] = (found && amb <= (uint32_t)run_at) ? 1 : 0;
                 if (r0 > 0) {
                     const uint64_t q = sm.u.so.k[r0 - 1];
                     sm.bu[1] = (uint32_t)(q >> 32);
@@ -1157,8 +1172,13 @@ __device__ __forceinline__ bool leader_smallk(Smem &sm, const RowCx &c, const Ro
             __syncthreads();
             const uint32_t r0 = sm.bu[0];
             const bool found = sm.bi[1] != 0;
+            const bool open = sm.bi[2] != 0;
             if (r0 > 0) { cut_key = sm.bu[1]; cut_i = sm.bi[0]; }
             __syncthreads();
+            if (open) {  // a rounding above the cut depends on S beyond S_row's accuracy
+                if (ambig) *ambig = true;  // every thread's own flag (the branch is block-uniform)
+                return false;
+            }
             if (probe && !found) return false;  // the cut lies below the K_PROBE largest
             if (r0 == 0) status = MIS_ROW_INVALID;
             for (int q = 0; q < PT; ++q) {               // back to the (key, idx, e) view
@@ -1296,7 +1316,26 @@ __device__ __forceinline__ void leader_row(Smem &sm, RowCx &c, const RowPlan &pl
         RowPlan pk = pl;
         pk.kk = (int)(c.V < (int64_t)K_PROBE ? c.V : (int64_t)K_PROBE);
         const Cand *cand = reinterpret_cast<const Cand *>(a.ws + L.cand) + (size_t)row * L.G * CAND_CAP;
-        if (!leader_smallk<DT>(sm, c, pk, csr, cand, ro, a, S_row)) final_generic<DT>(sm, c, pl, ro, a);
+        // S_row sums wexp weights (relative error <= WEXP_REL_ERR each, all
+        // positive) in float64; twice that bound covers the float64 sums and
+        // the chunk rescales
+        bool ambig = false;
+        if (!leader_smallk<DT>(sm, c, pk, csr, cand, ro, a, S_row, 2.0 * WEXP_REL_ERR, &ambig)) {
+            bool done = false;
+            if (ambig) {
+                // exact S from a re-read of the row (dexp, relative error
+                // below 1e-15), then the probe again
+                exp_table(sm.etab, tid);
+                __syncthreads();
+                double se = 0.0;
+                rescan<DT>(c, 0x007fffffu, 0xff800000u, [&](int64_t, float y, uint32_t) {
+                    if (y != -INFINITY) se += dexp((double)y - md, sm.etab);
+                });
+                const double S_ex = block_sum<double>(se, sm.red);
+                done = leader_smallk<DT>(sm, c, pk, csr, cand, ro, a, S_ex);
+            }
+            if (!done) final_generic<DT>(sm, c, pl, ro, a);
+        }
     } else {
         final_generic<DT>(sm, c, pl, ro, a);
     }
@@ -1511,14 +1550,13 @@ __global__ __launch_bounds__(NT) void k_sample(Args a)
             // (one else-if chain: separate branches here cost the fp32 kernel
             // 70 more VGPRs, half its occupancy)
             if (topp16) {
-                // S in float64 from dexp: the row pass's probabilities are
-                // rounded to the dtype, so S must be exact well below its ulp
-                exp_table(sm.etab, tid);
-                __syncthreads();
-                const double ymd = (double)ymax;
+                // S in float64 over wexp weights (relative error at most
+                // WEXP_REL_ERR): the row pass rounds probabilities to the
+                // dtype and takes an exact S only for a row where one of
+                // them could change within that bound
                 double s = 0.0;
 #pragma unroll
-                for (int i = 0; i < EPT; ++i) s += dexp((double)scale_r<DT>(x[i], T, rT) - ymd, sm.etab);
+                for (int i = 0; i < EPT; ++i) s += (double)wexp(scale_r<DT>(x[i], T, rT), ymax);
                 Sc = block_sum<double>(s, sm.red);
             }
             // ---- candidates: every finite x whose scaled key reaches a threshold
