@@ -455,6 +455,34 @@ template <int DT> __device__ __forceinline__ uint32_t rk_of_xkey(uint32_t xk, fl
 template <int DT> __device__ __forceinline__ uint32_t x_lower(uint32_t target, float T)
 {
     const uint32_t XLO = 0x007fffffu, XHI = 0xff800000u;  // -inf .. +inf
+    const int l0 = lane_id();
+    {
+        // one window of 64 raw keys around a guess first: the boundary lies
+        // within a few ulps of b * T, b the least scaled value that reaches
+        // target (fp32: its value; 16-bit: the midpoint to the next lower
+        // value, where round-to-nearest starts to give target).  The
+        // predicate is monotone, so false at the window's first key and true
+        // at a later one fixes the boundary; otherwise the full search runs.
+        float b;
+        if (DT == F32) {
+            b = f32_of_key(target);
+        } else {
+            // 16-bit row keys are multiples of 2^16: the least one >= target
+            // (0 when none: a NaN guess, which skips the window)
+            const uint32_t t16 = (target & 0xffffu) ? (target | 0xffffu) + 1u : target;
+            const float v = value_of_row_key(t16, DT);
+            const float w = t16 >= 0x10000u ? value_of_row_key(t16 - 0x10000u, DT) : -INFINITY;
+            b = 0.5f * v + 0.5f * w;
+        }
+        const float gx = b * T;
+        if (fabsf(gx) < INFINITY) {  // finite (NaN fails too)
+            const uint32_t gk = key_of_f32(gx);
+            uint32_t base = gk > XLO + 32u ? gk - 32u : XLO;
+            if (base > XHI - 63u) base = XHI - 63u;
+            const uint64_t mask = __ballot(rk_of_xkey<DT>(base + (uint32_t)l0, T) >= target);
+            if (mask != 0ull && (mask & 1ull) == 0ull) return base + (uint32_t)__builtin_ctzll(mask);
+        }
+    }
     if (rk_of_xkey<DT>(XLO, T) >= target) return XLO;
     if (rk_of_xkey<DT>(XHI, T) < target) return XHI + 1u;
     uint64_t lo = XLO, hi = XHI;  // pred(lo) false, pred(hi) true
