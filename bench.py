@@ -11,9 +11,13 @@ Inputs are resident in HBM before timing starts.  The batch (131 MB) fits
 the 256 MB Infinity Cache, so the timed loop rotates through >= 1 GiB of
 distinct copies of it.  Timing uses HIP events on the launch stream:
 * whole region: barrier + synchronize, start event, K steps, end event;
-* per kernel: mis_sample_profiled() records events before the chunk pass,
-  between the two kernels and after the row pass of every step, giving each
-  kernel's mean duration for the roofline entry.
+* per pass: mis_sample_ex() records events before the chunk pass, after it
+  on each stream that runs part of it, and after the row pass of every step.
+  A batch with fp32 top-p rows and other rows splits the chunk pass into two
+  launches on two streams (the top-p rows' on the launch stream, the others'
+  on the side stream); both start after the first event, so the chunk pass
+  takes from it to the later of the two ends.  That window, which reads every
+  row once, is the roofline entry's duration.
 
 The CPU baseline is the literal reference algorithm re-stated with torch CPU
 ops (oracle/faithful.py: one call per row, unstable sort, torch.multinomial),
@@ -62,14 +66,14 @@ def parse():
 
 
 def traffic_from_profile(config: str):
-    """HBM bytes per chunk-pass launch measured by rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE,
+    """HBM bytes per chunk pass (its one or two launches of a step) measured by rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE,
     each scaled by the same counter's reading for a copy of known size), from the committed
     summary profiles/k_sample_<config>_traffic.md; None when there is none."""
     path = os.path.join(ROOT, "profiles", f"k_sample_{config}_traffic.md")
     try:
         with open(path) as f:
             for line in f:
-                if line.startswith("traffic_bytes_per_launch:"):
+                if line.startswith("traffic_bytes_per_chunk_pass:"):
                     return int(float(line.split(":", 1)[1]))
     except OSError:
         pass
@@ -151,7 +155,7 @@ def main():
     torch.cuda.synchronize()
 
     K = args.steps
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(K)]
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(K)]
     for trio in evs:
         for e in trio:
             e.record()
@@ -164,18 +168,22 @@ def main():
     torch.cuda.synchronize()
     total_ms = start.elapsed_time(end)
     step_us = [t[0].elapsed_time(t[2]) * 1e3 for t in evs]
-    k1_us = [t[0].elapsed_time(t[1]) * 1e3 for t in evs]
-    k2_us = [t[1].elapsed_time(t[2]) * 1e3 for t in evs]
+    # the chunk pass: from the first event to the later end of its launches
+    # (two, and the fourth event recorded, exactly for fp32 with both kinds)
+    split = w.dtype == "f32" and kinds == 3
+    k1_us = [(max(t[0].elapsed_time(t[1]), t[0].elapsed_time(t[3])) if split else t[0].elapsed_time(t[1])) * 1e3
+             for t in evs]
+    k2_us = [st - k1 for st, k1 in zip(step_us, k1_us)]  # the rest of the step
     ms_per_step = total_ms / K
     rows_per_s = B * K / (total_ms / 1e3)
     gbs_step = bytes_alg / (ms_per_step / 1e3) / 1e9
     k1_mean, k2_mean = statistics.mean(k1_us), statistics.mean(k2_us)
     bytes_k1 = B * V * esz + 16 * B  # logits + params: the chunk pass's HBM read
-    # the roofline entry is the chunk pass's: the one launch that moves the
-    # algorithmic bytes and the longest single launch.  The row pass is up to
-    # seven shorter launches on two streams whose algorithmic bytes are only the
-    # ids (their re-reads of rows are not algorithmic); its time is reported
-    # beside it.
+    # the roofline entry is the chunk pass's: the pass that moves the
+    # algorithmic bytes (one launch, or two on two streams inside one window)
+    # and the longest.  The row pass is up to seven shorter launches on two
+    # streams whose algorithmic bytes are only the ids (their re-reads of rows
+    # are not algorithmic); its time is reported beside it.
     dom, dom_us, dom_bytes = "k_sample", k1_mean, bytes_k1
     q = statistics.quantiles(step_us, n=10)
     achieved = dom_bytes / (dom_us / 1e6) / 1e9
@@ -205,6 +213,7 @@ def main():
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic_from_profile(args.config) if dom == "k_sample" else None,
                      "algorithmic_bytes_per_launch": dom_bytes, "mean_launch_us": round(dom_us, 2),
+                     "chunk_pass_launches": 2 if split else 1,
                      "row_pass_us": round(k2_mean, 2)},
     }
     if args.copy_calib_mib > 0:

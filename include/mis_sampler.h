@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define MIS_ABI_VERSION 3
+#define MIS_ABI_VERSION 4
 
 /* logits element type */
 enum { MIS_DTYPE_F32 = 0, MIS_DTYPE_F16 = 1, MIS_DTYPE_BF16 = 2 };
@@ -132,10 +132,18 @@ int mis_sample_profiled(const void *logits, int dtype, int64_t B, int64_t V, int
 enum { MIS_KIND_TOPP32 = 1, MIS_KIND_OTHER = 2, MIS_KIND_ALL = 3 };
 
 /*
- * mis_sample() with a row-kind hint and optional events (NULL, or three
- * hipEvent_t recorded as by mis_sample_profiled()).  No counterpart in the
- * reference: its sampler runs on the host, which knows each request's
- * SamplingParams; the engine's batch builder passes what it knows.
+ * mis_sample() with a row-kind hint and optional events: NULL, or four
+ * hipEvent_t handles, events[0..2] as by mis_sample_profiled() and events[3]
+ * after the chunk pass of the rows the side stream serves.  A batch holding
+ * both fp32 top-p rows and other rows splits the chunk pass: the other rows'
+ * half runs on a per-device side stream (default priority), so events[1]
+ * (on `stream`) then closes only the top-p rows' half and events[3] the other
+ * half; both halves start after events[0], and the chunk pass as a whole ends
+ * at the later of the two.  The split happens exactly when dtype is
+ * MIS_DTYPE_F32 and kinds holds both bits; without it events[3] is not
+ * recorded (events[1] closes the whole chunk pass).  No counterpart in the reference: its sampler runs on the host,
+ * which knows each request's SamplingParams; the engine's batch builder
+ * passes what it knows.
  */
 int mis_sample_ex(const void *logits, int dtype, int64_t B, int64_t V, int64_t row_stride,
                   const mis_row_params *params, int64_t *out_ids, int32_t *out_status,

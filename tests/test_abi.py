@@ -46,7 +46,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version_and_strings(lib):
-    assert lib.mis_abi_version() == 3
+    assert lib.mis_abi_version() == 4
     assert lib.mis_strerror(0) == b"ok"
     assert b"workspace" in lib.mis_strerror(2)
     assert lib.mis_last_hip_error() == 0
@@ -79,11 +79,12 @@ def test_argument_validation_without_gpu(lib):
     # profiled entry needs three events
     ev = (vp * 3)(None, None, None)
     assert lib.mis_sample_profiled(fake, 0, 1, 10, 10, fake, fake, None, None, None, fake, 1 << 20, None, ev) == 1
-    # the hinted entry: unknown kind bits and partial event triples are argument errors
+    # the hinted entry: unknown kind bits and partial event sets (four handles) are argument errors
     lib.mis_sample_ex.argtypes = [vp, ctypes.c_int, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, vp, vp, vp, vp, vp,
                                   vp, ctypes.c_size_t, vp, ctypes.c_uint, vp]
     assert lib.mis_sample_ex(fake, 0, 1, 10, 10, fake, fake, None, None, None, fake, 1 << 20, None, 4, None) == 1
-    assert lib.mis_sample_ex(fake, 0, 1, 10, 10, fake, fake, None, None, None, fake, 1 << 20, None, 3, ev) == 1
+    ev4 = (vp * 4)(fake, fake, fake, None)  # the fourth event missing
+    assert lib.mis_sample_ex(fake, 0, 1, 10, 10, fake, fake, None, None, None, fake, 1 << 20, None, 3, ev4) == 1
     assert lib.mis_sample_ex(fake, 0, 0, 10, 10, fake, fake, None, None, None, fake, 1 << 20, None, 3, None) == 0
 
 

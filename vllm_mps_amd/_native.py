@@ -12,7 +12,7 @@ from . import build as _build
 
 DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
 ROW_OK, ROW_BAD_PARAM, ROW_INVALID, ROW_UNSUPPORTED, ROW_INTERNAL = 0, 1, 2, 3, 4
-ABI_VERSION = 3
+ABI_VERSION = 4
 KIND_TOPP32 = 1  # MIS_KIND_TOPP32
 KIND_OTHER = 2   # MIS_KIND_OTHER
 
@@ -77,10 +77,14 @@ def workspace_init(ws_ptr: int, ws_bytes: int, stream: int) -> None:
 
 def sample(logits_ptr: int, dtype: int, B: int, V: int, row_stride: int, params_ptr: int, ids_ptr: int,
            status_ptr: int | None, probs_ptr: int | None, keep_ptr: int | None, ws_ptr: int, ws_bytes: int,
-           stream: int, events: tuple[int, int, int] | None = None, kinds: int | None = None) -> None:
+           stream: int, events: tuple | None = None, kinds: int | None = None) -> None:
+    """events: None, or three handles (mis_sample_profiled), or four with
+    kinds (mis_sample_ex: the fourth closes the side stream's chunk pass)."""
     lib = load()
     if kinds is not None:
-        ev = None if events is None else (ctypes.c_void_p * 3)(*events)
+        if events is not None and len(events) != 4:
+            raise ValueError("mis_sample_ex takes four events")
+        ev = None if events is None else (ctypes.c_void_p * 4)(*events)
         rc = lib.mis_sample_ex(logits_ptr, dtype, B, V, row_stride, params_ptr, ids_ptr, status_ptr, probs_ptr,
                                keep_ptr, ws_ptr, ws_bytes, stream, kinds, ev)
     elif events is None:

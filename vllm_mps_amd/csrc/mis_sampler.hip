@@ -1415,8 +1415,12 @@ __device__ __forceinline__ uint32_t wave_sort_asc(uint32_t v)
 // The chunk pass: one workgroup per (row, chunk).  Loads the chunk into
 // registers and reduces it for the row's mode to the summary the row pass
 // reads.  fp32 top-p rows also bin their mass coarsely for the row pass.
+// k_sample's rows: all, only the fp32 top-p rows, or all but those (the two
+// halves run on two streams so the top-p passes start after their own rows)
+enum : int { K1_ALL = 0, K1_TOPP32 = 1, K1_OTHERS = 2 };
+
 template <int DT, int EPT>
-__global__ __launch_bounds__(NT) void k_sample(Args a)
+__global__ __launch_bounds__(NT) void k_sample(Args a, int part)
 {
     constexpr int VEC = Traits<DT>::VEC, CH = NT * EPT;
     __shared__ ChunkSmem sm;
@@ -1431,6 +1435,7 @@ __global__ __launch_bounds__(NT) void k_sample(Args a)
     mis_row_params P = a.params[row];
     P.temperature = uni(P.temperature); P.top_k = uni(P.top_k); P.top_p = uni(P.top_p); P.uniform = uni(P.uniform);
     const RowPlan pl = plan_row(P, V);
+    if (part != K1_ALL && (part == K1_TOPP32) != (DT == F32 && pl.mode == M_TOPP)) return;  // the other launch's row
     ChunkSum *csr = reinterpret_cast<ChunkSum *>(a.ws + L.chunks) + (size_t)row * G;
     ChunkSum *cs = csr + chunk;
     RoundBuf *rb = reinterpret_cast<RoundBuf *>(a.ws + L.rbuf) + (size_t)row * G + chunk;
@@ -2117,44 +2122,55 @@ static hipError_t side_of_current(Side **out)
 }
 
 template <int DT, int EPT>
-static hipError_t launch_sample(const Args &a, hipStream_t st)
+static hipError_t launch_sample(const Args &a, hipStream_t st, int part)
 {
     const unsigned grid = (unsigned)(a.L.B * a.L.G);
-    hipLaunchKernelGGL((k_sample<DT, EPT>), dim3(grid), dim3(NT), 0, st, a);
+    hipLaunchKernelGGL((k_sample<DT, EPT>), dim3(grid), dim3(NT), 0, st, a, part);
     return hipGetLastError();
 }
 
-// events (optional): [0] before the chunk pass, [1] between the chunk pass
-// and the row pass (k_tp_* + k_final), [2] after the row pass (before the
-// debug emit)
+template <int DT>
+static hipError_t launch_chunks(const Args &a, hipStream_t st, int part)
+{
+    switch (a.L.ept) {
+    case 64: return launch_sample<DT, 64>(a, st, part);
+    case 32: return launch_sample<DT, 32>(a, st, part);
+    default: return launch_sample<DT, 16>(a, st, part);
+    }
+}
+
+// events (optional, nev = 3 or 4): [0] before the chunk pass, [1] after the
+// chunk pass on the caller's stream (with the split, its fp32 top-p rows'),
+// [2] after the row pass (before the debug emit), [3] after the side stream's
+// chunk pass (recorded only with the split: one more marker on the caller's
+// stream would add its own gap to the step)
 template <int DT>
 static hipError_t launch_dt(const Args &a, float *probs, uint32_t *keep, hipStream_t st, unsigned kinds,
-                            void *const *ev)
+                            void *const *ev, int nev)
 {
     hipError_t e;
     if (ev && (e = hipEventRecord((hipEvent_t)ev[0], st)) != hipSuccess) return e;
-    switch (a.L.ept) {
-    case 64: e = launch_sample<DT, 64>(a, st); break;
-    case 32: e = launch_sample<DT, 32>(a, st); break;
-    default: e = launch_sample<DT, 16>(a, st); break;
-    }
-    if (e != hipSuccess) return e;
-    if (ev && (e = hipEventRecord((hipEvent_t)ev[1], st)) != hipSuccess) return e;
     const unsigned B = (unsigned)a.L.B;
-    if (DT == F32 && (kinds & MIS_KIND_TOPP32)) {
-        // fp32 top-p rows: the k_tp_* passes on the caller's stream.  With
-        // other rows present their row pass runs beside them on the side
-        // stream; the rows the passes deferred follow.
-        const bool side = (kinds & MIS_KIND_OTHER) != 0;
-        Side *sd = nullptr;
-        if (side) {
-            if ((e = side_of_current(&sd)) != hipSuccess) return e;
-            if ((e = hipEventRecord(sd->fork, st)) != hipSuccess) return e;
-            if ((e = hipStreamWaitEvent(sd->s, sd->fork, 0)) != hipSuccess) return e;
-            hipLaunchKernelGGL((k_final<DT>), dim3(B), dim3(NT), 0, sd->s, a, (int)FIN_OTHERS);
-            if ((e = hipGetLastError()) != hipSuccess) return e;
-            if ((e = hipEventRecord(sd->join, sd->s)) != hipSuccess) return e;
-        }
+    const bool tp32 = DT == F32 && (kinds & MIS_KIND_TOPP32);
+    // fp32 top-p rows with other rows beside them: the other rows' chunk pass
+    // and row pass run on the side stream, beside the top-p rows' chunk pass
+    // and k_tp_* passes on the caller's stream; the rows the passes deferred
+    // follow once both are done
+    const bool side = tp32 && (kinds & MIS_KIND_OTHER) != 0;
+    Side *sd = nullptr;
+    if (side) {
+        if ((e = side_of_current(&sd)) != hipSuccess) return e;
+        if ((e = hipEventRecord(sd->fork, st)) != hipSuccess) return e;
+        if ((e = hipStreamWaitEvent(sd->s, sd->fork, 0)) != hipSuccess) return e;
+        if ((e = launch_chunks<DT>(a, sd->s, K1_OTHERS)) != hipSuccess) return e;
+        if (ev && nev > 3 && (e = hipEventRecord((hipEvent_t)ev[3], sd->s)) != hipSuccess) return e;
+        hipLaunchKernelGGL((k_final<DT>), dim3(B), dim3(NT), 0, sd->s, a, (int)FIN_OTHERS);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+        if ((e = hipEventRecord(sd->join, sd->s)) != hipSuccess) return e;
+    }
+    if ((e = launch_chunks<DT>(a, st, side ? K1_TOPP32 : K1_ALL)) != hipSuccess) return e;
+    if (ev && (e = hipEventRecord((hipEvent_t)ev[1], st)) != hipSuccess) return e;
+    if (tp32) {
         const unsigned tg = (unsigned)(a.L.B * a.L.G < TP_GRID ? a.L.B * a.L.G : TP_GRID);
         hipLaunchKernelGGL(k_tp_prep, dim3(B), dim3(NT), 0, st, a);
         if (a.L.ept == 64) hipLaunchKernelGGL((k_tp_hist<64>), dim3(tg), dim3(NT), 0, st, a);
@@ -2205,7 +2221,7 @@ int mis_workspace_init(void *workspace, size_t workspace_bytes, void *stream)
 static int sample_impl(const void *logits, int dtype, int64_t B, int64_t V, int64_t row_stride,
                        const mis_row_params *params, int64_t *out_ids, int32_t *out_status, float *out_probs,
                        uint32_t *out_keep, void *workspace, size_t workspace_bytes, void *stream,
-                       unsigned kinds, void *const *events)
+                       unsigned kinds, void *const *events, int nev)
 {
     using namespace mis;
     if (dtype < 0 || dtype > 2 || B < 0 || V <= 0 || row_stride < V) return MIS_ERR_INVALID_ARG;
@@ -2228,9 +2244,9 @@ static int sample_impl(const void *logits, int dtype, int64_t B, int64_t V, int6
     a.out_status = out_status;
     hipStream_t st = (hipStream_t)stream;
     hipError_t e;
-    if (dtype == MIS_DTYPE_F32) e = launch_dt<F32>(a, out_probs, out_keep, st, kinds, events);
-    else if (dtype == MIS_DTYPE_F16) e = launch_dt<F16>(a, out_probs, out_keep, st, kinds, events);
-    else e = launch_dt<BF16>(a, out_probs, out_keep, st, kinds, events);
+    if (dtype == MIS_DTYPE_F32) e = launch_dt<F32>(a, out_probs, out_keep, st, kinds, events, nev);
+    else if (dtype == MIS_DTYPE_F16) e = launch_dt<F16>(a, out_probs, out_keep, st, kinds, events, nev);
+    else e = launch_dt<BF16>(a, out_probs, out_keep, st, kinds, events, nev);
     if (e != hipSuccess) { g_last_hip = (int)e; return MIS_ERR_HIP; }
     return MIS_OK;
 }
@@ -2240,7 +2256,7 @@ int mis_sample(const void *logits, int dtype, int64_t B, int64_t V, int64_t row_
                uint32_t *out_keep, void *workspace, size_t workspace_bytes, void *stream)
 {
     return sample_impl(logits, dtype, B, V, row_stride, params, out_ids, out_status, out_probs, out_keep,
-                       workspace, workspace_bytes, stream, MIS_KIND_ALL, nullptr);
+                       workspace, workspace_bytes, stream, MIS_KIND_ALL, nullptr, 0);
 }
 
 int mis_sample_profiled(const void *logits, int dtype, int64_t B, int64_t V, int64_t row_stride,
@@ -2250,7 +2266,7 @@ int mis_sample_profiled(const void *logits, int dtype, int64_t B, int64_t V, int
 {
     if (!events || !events[0] || !events[1] || !events[2]) return MIS_ERR_INVALID_ARG;
     return sample_impl(logits, dtype, B, V, row_stride, params, out_ids, out_status, out_probs, out_keep,
-                       workspace, workspace_bytes, stream, MIS_KIND_ALL, events);
+                       workspace, workspace_bytes, stream, MIS_KIND_ALL, events, 3);
 }
 
 int mis_sample_ex(const void *logits, int dtype, int64_t B, int64_t V, int64_t row_stride,
@@ -2259,9 +2275,9 @@ int mis_sample_ex(const void *logits, int dtype, int64_t B, int64_t V, int64_t r
                   void *const *events)
 {
     if ((kinds & ~(unsigned)MIS_KIND_ALL) != 0u) return MIS_ERR_INVALID_ARG;
-    if (events && (!events[0] || !events[1] || !events[2])) return MIS_ERR_INVALID_ARG;
+    if (events && (!events[0] || !events[1] || !events[2] || !events[3])) return MIS_ERR_INVALID_ARG;
     return sample_impl(logits, dtype, B, V, row_stride, params, out_ids, out_status, out_probs, out_keep,
-                       workspace, workspace_bytes, stream, kinds, events);
+                       workspace, workspace_bytes, stream, kinds, events, 4);
 }
 
 const char *mis_strerror(int code)

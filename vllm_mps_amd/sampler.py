@@ -126,9 +126,10 @@ class Sampler:
                       status_out: torch.Tensor | None = None, probs_out: torch.Tensor | None = None,
                       keep_out: torch.Tensor | None = None, events=None, kinds: int | None = None) -> torch.Tensor:
         """One launch sequence over ``logits[B, V]`` with a device ``packed``
-        [B, 4] int32 parameter buffer (see ``pack_params``).  ``events``: three
-        recorded ``torch.cuda.Event`` objects to time the chunk pass and the
-        row pass (see ``mis_sample_profiled``).  ``kinds``: the row-kind hint
+        [B, 4] int32 parameter buffer (see ``pack_params``).  ``events``: recorded
+        ``torch.cuda.Event`` objects timing the chunk pass and the row pass:
+        three without ``kinds`` (``mis_sample_profiled``), four with it
+        (``mis_sample_ex``: the fourth closes the side stream's chunk pass).  ``kinds``: the row-kind hint
         (``row_kinds``), None for "any"."""
         if logits.dim() != 2:
             raise ValueError("logits must be [B, V]")
