@@ -1518,7 +1518,7 @@ __global__ __launch_bounds__(NT) void k_sample(Args a, int part)
             for (int i = 0; i < EPT; ++i) s += (double)wexp(scale_r<DT>(x[i], T, rT), ymax);
             Sc = block_sum<double>(s, sm.red);
         } else if (live && topp32) {
-            // round 1: weights and lane-private coarse bins on the global grid
+            // first refinement level: weights and lane-private coarse bins on the global grid
             // floor(y / 2); bins more than CB_N below the chunk's are not kept.
             // Each lane owns one column of the bins, so plain read-modify-write
             // suffices (LDS float atomics serialise)
