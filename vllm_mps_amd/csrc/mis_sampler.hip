@@ -1702,22 +1702,30 @@ __global__ __launch_bounds__(NT) void k_tp_prep(Args a)
     const RoundBuf *rbf = reinterpret_cast<const RoundBuf *>(a.ws + L.rbuf) + (size_t)row * L.G;
     const int G = L.G;
     trace(a.ws, L, row, 2);
+    // this thread's chunk (G <= NT): its S and coarse bins are loaded beside
+    // the chunk maxima row_scales reads, one round trip instead of three
+    static_assert(G_MAX <= NT, "one chunk per thread");
+    const bool hasg = tid < G;
+    const double Sg = hasg ? ldp(&rbf[tid].S) : 0.0;
+    const float ygt = hasg ? ldp(&csr[tid].ymax) : -INFINITY;
+    double cbv[CB_N];
+#pragma unroll
+    for (int lb = 0; lb < CB_N; ++lb) cbv[lb] = hasg ? ldp(&rbf[tid].coarse[lb]) : 0.0;
     uint32_t bad;
     const float m = row_scales(sm, csr, G, &bad);
     trace(a.ws, L, row, 3);
     if (bad != 0u || m == -INFINITY) { if (tid == 0) tr->status = TR_DEFER; return; }
-    double s = 0.0;
-    for (int g = tid; g < G; g += NT) s += ldp(&rbf[g].S) * sm.chs[g];
-    const double S = block_sum<double>(s, sm.red);
+    const double S = block_sum<double>(hasg ? Sg * sm.chs[tid] : 0.0, sm.red);
     const double A = (double)pl.top_p * S;
     const float Ar = coarse_bin(m);
     if (tid < CB_N) sm.v.coarse[tid] = 0.0;
     __syncthreads();
-    for (int g = tid; g < G; g += NT) {
-        const float yg = ldp(&csr[g].ymax);
-        if (yg == -INFINITY) continue;
-        const int off = (int)(Ar - coarse_bin(yg));
-        for (int lb = 0; lb + off < CB_N; ++lb) atomicAdd(&sm.v.coarse[lb + off], ldp(&rbf[g].coarse[lb]) * sm.chs[g]);
+    if (hasg && ygt != -INFINITY) {
+        const int off = (int)(Ar - coarse_bin(ygt));
+        const double sc = sm.chs[tid];
+#pragma unroll
+        for (int lb = 0; lb < CB_N; ++lb)
+            if (lb + off < CB_N) atomicAdd(&sm.v.coarse[lb + off], cbv[lb] * sc);
     }
     __syncthreads();
     if (tid == 0) {
