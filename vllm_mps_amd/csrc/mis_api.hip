@@ -1,0 +1,111 @@
+// mis_api.hip -- the C ABI of include/mis_sampler.h: argument checks, the
+// workspace layout and dispatch to the per-dtype launch sequences.  Host code
+// only; the kernels live in the per-dtype translation units.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "mis_launch.h"
+#include "mis_layout.h"
+#include "mis_sampler.h"
+
+namespace mis {
+static thread_local int g_last_hip = 0;
+}  // namespace mis
+
+extern "C" {
+
+size_t mis_workspace_bytes(int64_t B, int64_t V, int dtype)
+{
+    (void)dtype;
+    if (B <= 0 || V <= 0) return 256;
+    return mis::make_layout(B, V, dtype).total;
+}
+
+int mis_workspace_init(void *workspace, size_t workspace_bytes, void *stream)
+{
+    if (!workspace) return MIS_ERR_INVALID_ARG;
+    if (((uintptr_t)workspace & 255u) != 0 || workspace_bytes < mis::CTL_PREFIX) return MIS_ERR_WORKSPACE;
+    const hipError_t e = hipMemsetAsync(workspace, 0, mis::CTL_PREFIX, (hipStream_t)stream);
+    if (e != hipSuccess) { mis::g_last_hip = (int)e; return MIS_ERR_HIP; }
+    return MIS_OK;
+}
+
+static int sample_impl(const void *logits, int dtype, int64_t B, int64_t V, int64_t row_stride,
+                       const mis_row_params *params, int64_t *out_ids, int32_t *out_status, float *out_probs,
+                       uint32_t *out_keep, void *workspace, size_t workspace_bytes, void *stream,
+                       unsigned kinds, void *const *events, int nev)
+{
+    using namespace mis;
+    if (dtype < 0 || dtype > 2 || B < 0 || V <= 0 || row_stride < V) return MIS_ERR_INVALID_ARG;
+    if (B == 0) return MIS_OK;
+    if (!logits || !params || !out_ids || !workspace) return MIS_ERR_INVALID_ARG;
+    if (V > (int64_t)1 << 30 || B > 0x7fffffff) return MIS_ERR_UNSUPPORTED;
+    const Layout L = make_layout(B, V, dtype);
+    if (L.G > G_MAX || (int64_t)L.B * L.G > 0x7fffffff) return MIS_ERR_UNSUPPORTED;
+    if (workspace_bytes < L.total || ((uintptr_t)workspace & 255u) != 0) return MIS_ERR_WORKSPACE;
+    const int esz = dtype == MIS_DTYPE_F32 ? 4 : 2;
+    Args a;
+    a.logits = (const char *)logits;
+    a.V = V;
+    a.stride_bytes = row_stride * esz;
+    a.vec_ok = (((uintptr_t)logits & 15u) == 0 && (a.stride_bytes & 15) == 0) ? 1 : 0;
+    a.params = params;
+    a.L = L;
+    a.ws = (char *)workspace;
+    a.out_ids = out_ids;
+    a.out_status = out_status;
+    hipStream_t st = (hipStream_t)stream;
+    hipError_t e;
+    if (dtype == MIS_DTYPE_F32) e = launch_f32(a, out_probs, out_keep, st, kinds, events, nev);
+    else if (dtype == MIS_DTYPE_F16) e = launch_f16(a, out_probs, out_keep, st, kinds, events, nev);
+    else e = launch_bf16(a, out_probs, out_keep, st, kinds, events, nev);
+    if (e != hipSuccess) { g_last_hip = (int)e; return MIS_ERR_HIP; }
+    return MIS_OK;
+}
+
+int mis_sample(const void *logits, int dtype, int64_t B, int64_t V, int64_t row_stride,
+               const mis_row_params *params, int64_t *out_ids, int32_t *out_status, float *out_probs,
+               uint32_t *out_keep, void *workspace, size_t workspace_bytes, void *stream)
+{
+    return sample_impl(logits, dtype, B, V, row_stride, params, out_ids, out_status, out_probs, out_keep,
+                       workspace, workspace_bytes, stream, MIS_KIND_ALL, nullptr, 0);
+}
+
+int mis_sample_profiled(const void *logits, int dtype, int64_t B, int64_t V, int64_t row_stride,
+                        const mis_row_params *params, int64_t *out_ids, int32_t *out_status, float *out_probs,
+                        uint32_t *out_keep, void *workspace, size_t workspace_bytes, void *stream,
+                        void *const *events)
+{
+    if (!events || !events[0] || !events[1] || !events[2]) return MIS_ERR_INVALID_ARG;
+    return sample_impl(logits, dtype, B, V, row_stride, params, out_ids, out_status, out_probs, out_keep,
+                       workspace, workspace_bytes, stream, MIS_KIND_ALL, events, 3);
+}
+
+int mis_sample_ex(const void *logits, int dtype, int64_t B, int64_t V, int64_t row_stride,
+                  const mis_row_params *params, int64_t *out_ids, int32_t *out_status, float *out_probs,
+                  uint32_t *out_keep, void *workspace, size_t workspace_bytes, void *stream, unsigned kinds,
+                  void *const *events)
+{
+    if ((kinds & ~(unsigned)MIS_KIND_ALL) != 0u) return MIS_ERR_INVALID_ARG;
+    if (events && (!events[0] || !events[1] || !events[2] || !events[3])) return MIS_ERR_INVALID_ARG;
+    return sample_impl(logits, dtype, B, V, row_stride, params, out_ids, out_status, out_probs, out_keep,
+                       workspace, workspace_bytes, stream, kinds, events, 4);
+}
+
+const char *mis_strerror(int code)
+{
+    switch (code) {
+    case MIS_OK: return "ok";
+    case MIS_ERR_INVALID_ARG: return "invalid argument";
+    case MIS_ERR_WORKSPACE: return "workspace too small or not 256-byte aligned";
+    case MIS_ERR_HIP: return "HIP launch failed";
+    case MIS_ERR_UNSUPPORTED: return "shape not supported (V > 2^30, B > 65535 or too many chunks)";
+    default: return "unknown error";
+    }
+}
+
+int mis_last_hip_error(void) { return mis::g_last_hip; }
+
+int mis_abi_version(void) { return MIS_ABI_VERSION; }
+
+}  // extern "C"

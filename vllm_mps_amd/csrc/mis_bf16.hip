@@ -1,0 +1,13 @@
+// mis_bf16.hip -- the sampler's kernels instantiated for BF16 logits.
+#include "mis_kernels.h"
+#include "mis_launch.h"
+
+namespace mis {
+
+hipError_t launch_bf16(const Args &a, float *probs, uint32_t *keep, hipStream_t st, unsigned kinds,
+                     void *const *ev, int nev)
+{
+    return launch_dt<BF16>(a, probs, keep, st, kinds, ev, nev);
+}
+
+}  // namespace mis

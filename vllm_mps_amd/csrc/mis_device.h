@@ -8,11 +8,9 @@
 #include <stdint.h>
 
 #include "mis_common.h"
+#include "mis_layout.h"
 
 namespace mis {
-
-constexpr int NT = 256;            // threads per workgroup (4 waves of 64)
-constexpr int NWAVE = NT / 64;
 
 // ------------------------------------------------------------------ dtype io
 

@@ -1,0 +1,13 @@
+// mis_f16.hip -- the sampler's kernels instantiated for F16 logits.
+#include "mis_kernels.h"
+#include "mis_launch.h"
+
+namespace mis {
+
+hipError_t launch_f16(const Args &a, float *probs, uint32_t *keep, hipStream_t st, unsigned kinds,
+                     void *const *ev, int nev)
+{
+    return launch_dt<F16>(a, probs, keep, st, kinds, ev, nev);
+}
+
+}  // namespace mis

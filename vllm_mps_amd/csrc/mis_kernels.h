@@ -1,39 +1,34 @@
-// mis_sampler.hip -- MI355X (gfx950) decode-step token sampler behind the C ABI
-// declared in include/mis_sampler.h.
+// mis_kernels.h -- the sampler kernels and their per-dtype launch sequence.
 //
-// One call = one launch of k_sample (plus k_emit when the caller asks for the
-// debug probabilities / keep bitmask).
+// Included by one translation unit per logits dtype (mis_f32.hip,
+// mis_f16.hip, mis_bf16.hip), each of which instantiates launch_dt<DT> for
+// its dtype, so the three device builds compile in parallel.  The C ABI
+// (mis_api.hip) calls them through mis_launch.h.
+#pragma once
+
+// MI355X (gfx950) decode-step token sampler behind the C ABI declared in
+// include/mis_sampler.h.  Stateless: every launch reads only what the same
+// call's earlier launches wrote (stream order); no workgroup waits on
+// another.
 //
-// k_sample: B*G workgroups of 256 threads.  Each workgroup takes a ticket
-// (atomic counter) naming one chunk of one row -- tickets run row-major, so a
-// row's chunks start together -- and loads that chunk into registers with
-// coalesced 16-byte vector reads: the only HBM read of the logits.  The
-// per-element work is register arithmetic only (no LDS atomics on dense
-// data, which serialise on bin conflicts): a max, a divide by the row's
-// temperature through its reciprocal, an f32 exponential with a bounded
-// error.  Each chunk publishes a summary; the last workgroup of a row to
-// arrive finishes the row:
-//   greedy       argmax merge;
-//   temperature  per-chunk weights -> the chunk holding the draw -> that
-//                chunk is re-read for the index;
-//   small top-k  every chunk emits its elements above a threshold chosen from
-//                its per-thread maxima (closed under the ties the scaling
-//                creates); the leader takes the exact k'-th value over the
-//                candidates, checks that no truncated chunk could hide an
-//                element at or above it, then top-p over the survivors and
-//                the draw;
-//   fp32 top-p   the row's workgroups keep their chunks in registers and run
-//                a few rounds with the leader: coarse lane-private mass bins
-//                (conflict-free), then 256-way refinements of the band that
-//                holds the cut, then a collection of the cut's window; masses
-//                carry a proven f32 error bound, and when the decision margin
-//                is inside that bound one more round recomputes them in f64;
-//   otherwise    (k' > 1024, fp16/bf16 top-p, overflows, cuts outside the
-//                coarse range) the leader re-reads the row: radix descent by
-//                mass or count, and the 16-bit rounding chain walked over runs
-//                of equal keys.
-// Every cross-workgroup wait is for row mates that already hold a ticket, so
-// it ends; each is also bounded by a spin limit.
+// k_sample (chunk pass): B*G workgroups of 256 threads, one per (row,
+// chunk).  Each loads its chunk into registers with coalesced 16-byte
+// vector reads -- the only full HBM read of the logits -- and reduces it by
+// the row's mode into a per-(row, chunk) summary:
+//   greedy       argmax of the raw logits;
+//   temperature  chunk max and the sum of weights relative to it;
+//   small top-k  the elements above a floor taken from the per-thread maxima
+//                (closed under the ties the scaling creates) as candidates;
+//   fp32 top-p   float64 sum of exact weights and coarse mass bins;
+//   16-bit top-p the 512 largest values as candidates, float64 sum.
+// k_final (row pass): one workgroup per row merges the summaries: greedy,
+// temperature (chunk holding the draw, then that chunk re-read), small top-k
+// (exact k'-th value over the candidates, top-p over the survivors, draw),
+// the 16-bit top-p probe; the generic path (radix descent over re-reads of
+// the row, the 16-bit rounding chain) serves the rest.
+// k_tp_* (fp32 top-p rows): prep, fine bins, merge, collect and final
+// passes spread each row over the GPU.
+// k_emit: debug probabilities / keep bitmask from each row's cut.
 //
 // Semantics follow model/sampler.py:18-60 per row: greedy argmax (ties ->
 // lowest index) when T == 0; y = dtype(f32(x) / T); top-k keeps y >= k'-th
@@ -48,129 +43,13 @@
 #include <mutex>
 
 #include "mis_device.h"
+#include "mis_layout.h"
 #include "mis_sampler.h"
 
 namespace mis {
-
-constexpr int K_SMALL = 1024;      // largest k' served by the candidate path
-constexpr int CAND_CAP = 2048;     // candidates one chunk may emit
-constexpr int SURV_CAP = 1024;     // top-k survivors / top-p window held in LDS
-constexpr int K_PROBE = 512;       // fp16/bf16 top-p rows look for their cut among this many largest values
-                                   // first (ties at the last one stay within SURV_CAP)
-constexpr int EPT_DEFAULT = 32;    // elements per thread of the chunk pass (64 when G would exceed G_MAX)
-constexpr int CCAP = 8192;         // small-k candidates of a row cached in LDS (64 KB)
-constexpr int G_MAX = 256;         // chunks per row
-constexpr int CB_N = 16;           // coarse top-p bins (lane-private)
-constexpr float CB_SCALE = 0.5f;   // coarse bin = floor(y * CB_SCALE): 2 units of y
-constexpr int REGION_MAX = 16;     // L1 bins per 16-bit chain pass at most (re-read path)
-constexpr int RUN_CAP = REGION_MAX * 256;
-constexpr int TIE_CAP = 1024;
-constexpr uint32_t NCAND_OVERFLOW = 0xffffffffu;
-constexpr int32_t IDX_ALL = 0x7fffffff;
-
-enum : int { M_BAD = 0, M_GREEDY = 1, M_SMALLK = 2, M_LARGEK = 3, M_TOPP = 4, M_TEMP = 5 };
-enum : uint32_t { FLAG_NAN = 1u, FLAG_PINF = 2u };
-
-// ------------------------------------------------------------------ workspace
-
-// The workspace keeps no state between calls: every word a call reads it has
-// written earlier in the same call.
-constexpr size_t CTL_PREFIX = 256;
-
-struct ChunkSum {               // 64 B per (row, chunk)
-    uint32_t xkey;              // argmax key of the raw logits (NaN = 0xffffffff)
-    int32_t xarg;
-    float ymax;                 // max scaled logit of the chunk
-    uint32_t flags;
-    uint32_t ncand;             // small-k candidates written, or NCAND_OVERFLOW
-    uint32_t nfin;              // finite elements of the chunk
-    uint32_t kc;                // small-k: non-candidates have scaled keys < kc
-    uint32_t trunc;             // small-k: some finite element was not emitted
-    double S;                   // sum of weights relative to the chunk max
-    double pad[3];
-};
-
-// per-(row, chunk) coarse mass bins of an fp32 top-p row
-struct RoundBuf {               // 256 B
-    double coarse[CB_N];        // mass per coarse bin (relative to the chunk max)
-    double S;                   // sum of weights relative to the chunk max
-    double pad[15];
-};
-static_assert(sizeof(RoundBuf) == 256, "RoundBuf size");
-
-struct RowOut {                 // 64 B per row, read by k_emit
-    int64_t id;
-    int32_t status;
-    int32_t mode;
-    float m;                    // row max of y
-    uint32_t cut_key;           // kept iff key > cut_key or (key == cut_key and j <= cut_i)
-    int32_t cut_i;
-    int32_t pad;
-    double S;                   // sum of kept weights exp(y - m)
-    double pad2[3];
-};
-
-struct Cand { float x; int32_t idx; };
-struct Elem { uint32_t key; int32_t idx; };
-
-// fp32 top-p passes (k_tp_*): per (row, chunk) fine bins over the row's
-// coarse band, per row the band keys, per-chunk kept masses and survivors
-constexpr int FH = 512;             // fine bins per chunk over the coarse band
-constexpr double FIX_ONE = 1099511627776.0;  // 2^40: fine-bin masses as integers of exp(y - m)
-struct TopChunk {
-    double above;                   // float64 mass of the chunk's elements above the coarse band
-    double pad[31];
-    uint32_t cnt[FH];
-    unsigned long long mass[FH];
-};
-static_assert(sizeof(TopChunk) % 256 == 0, "TopChunk size");
-enum : uint32_t { TR_NONE = 0, TR_ACTIVE = 1, TR_DEFER = 2 };
-struct TopRow {
-    uint32_t status, count;         // TR_*; survivors appended by the collect pass
-    uint32_t klo, khi;              // coarse band (row keys)
-    uint32_t xlo, xhi;              // its raw-key interval
-    int32_t ja, jb;                 // final band: fine bins [ja, jb]
-    uint32_t pad1[2];
-    float m, lo, scf, T;            // row max of y; fine-bin grid y -> (y - lo) * scf; temperature
-    double S, A, fix_err;           // sum of exp(y - m), top_p * S, bound of the fixed-point sums
-    double pad[22];
-    double cw[G_MAX];               // per-chunk kept mass above the final band
-    Elem list[SURV_CAP];            // the final band's elements
-};
-static_assert(sizeof(TopRow) % 256 == 0, "TopRow size");
-
-struct Layout {
-    int64_t B, V;
-    int ept, G;
-    size_t rowout, chunks, rbuf, cand, topc, topr, total;
-};
-
-static inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
-
-// Elements per thread: 16 (chunks of 4096 elements; 16 vector registers of
-// logits per thread keep the chunk pass at six or more waves per SIMD), 64
-// when the row would need more than G_MAX chunks.
-static Layout make_layout(int64_t B, int64_t V, int dtype)
-{
-    Layout L;
-    L.B = B; L.V = V;
-    auto chunks = [&](int ept) { return (V + (int64_t)NT * ept - 1) / ((int64_t)NT * ept); };
-    L.ept = EPT_DEFAULT;
-    if (chunks(L.ept) > G_MAX) L.ept = 64;
-    L.G = (int)chunks(L.ept);
-    const size_t BG = (size_t)B * L.G;
-    size_t off = CTL_PREFIX;
-    L.rowout = off; off = align256(off + sizeof(RowOut) * (size_t)B);
-    L.chunks = off; off = align256(off + sizeof(ChunkSum) * BG);
-    L.rbuf = off;   off = align256(off + sizeof(RoundBuf) * BG);
-    L.cand = off;   off = align256(off + sizeof(Cand) * (size_t)CAND_CAP * BG);
-    // fp32 top-p: per-chunk fine bins and per-row state of the top-p passes
-    const bool f32 = dtype == MIS_DTYPE_F32;
-    L.topc = off;   off = align256(off + (f32 ? sizeof(TopChunk) * BG : 0));
-    L.topr = off;   off = align256(off + (f32 ? sizeof(TopRow) * (size_t)B : 0));
-    L.total = off;
-    return L;
-}
+// everything below is local to the including translation unit: each per-dtype
+// unit holds its own copy of the dtype-independent kernels and helpers
+namespace {
 
 // ------------------------------------------------------------------ phase timestamps
 //
@@ -215,17 +94,6 @@ __device__ __forceinline__ RowPlan plan_row(const mis_row_params &P, int64_t V)
 
 // ------------------------------------------------------------------ context
 
-struct Args {
-    const char *logits;
-    int64_t V;
-    int64_t stride_bytes;
-    int vec_ok;
-    const mis_row_params *params;
-    Layout L;
-    char *ws;
-    int64_t *out_ids;
-    int32_t *out_status;
-};
 
 struct RowCx {                 // what the leader of a row works with
     const char *rowp;
@@ -2099,8 +1967,6 @@ __global__ __launch_bounds__(NT) void k_emit(const char *__restrict__ logits, in
 
 // ------------------------------------------------------------------ host side
 
-static thread_local int g_last_hip = 0;
-
 // Per device: a second stream (default priority) and the two events that
 // fork it from the caller's stream and join it back, made on the first call
 // on that device and kept until the process ends.  Calls that overlap on one
@@ -2142,8 +2008,7 @@ static hipError_t launch_chunks(const Args &a, hipStream_t st, int part)
 {
     switch (a.L.ept) {
     case 64: return launch_sample<DT, 64>(a, st, part);
-    case 32: return launch_sample<DT, 32>(a, st, part);
-    default: return launch_sample<DT, 16>(a, st, part);
+    default: return launch_sample<DT, 32>(a, st, part);
     }
 }
 
@@ -2182,12 +2047,10 @@ static hipError_t launch_dt(const Args &a, float *probs, uint32_t *keep, hipStre
         const unsigned tg = (unsigned)(a.L.B * a.L.G < TP_GRID ? a.L.B * a.L.G : TP_GRID);
         hipLaunchKernelGGL(k_tp_prep, dim3(B), dim3(NT), 0, st, a);
         if (a.L.ept == 64) hipLaunchKernelGGL((k_tp_hist<64>), dim3(tg), dim3(NT), 0, st, a);
-        else if (a.L.ept == 32) hipLaunchKernelGGL((k_tp_hist<32>), dim3(tg), dim3(NT), 0, st, a);
-        else hipLaunchKernelGGL((k_tp_hist<16>), dim3(tg), dim3(NT), 0, st, a);
+        else hipLaunchKernelGGL((k_tp_hist<32>), dim3(tg), dim3(NT), 0, st, a);
         hipLaunchKernelGGL(k_tp_merge, dim3(B), dim3(NT), 0, st, a);
         if (a.L.ept == 64) hipLaunchKernelGGL((k_tp_collect<64>), dim3(tg), dim3(NT), 0, st, a);
-        else if (a.L.ept == 32) hipLaunchKernelGGL((k_tp_collect<32>), dim3(tg), dim3(NT), 0, st, a);
-        else hipLaunchKernelGGL((k_tp_collect<16>), dim3(tg), dim3(NT), 0, st, a);
+        else hipLaunchKernelGGL((k_tp_collect<32>), dim3(tg), dim3(NT), 0, st, a);
         hipLaunchKernelGGL(k_tp_final, dim3(B), dim3(NTF), 0, st, a);
         if ((e = hipGetLastError()) != hipSuccess) return e;
         if (side && (e = hipStreamWaitEvent(st, sd->join, 0)) != hipSuccess) return e;
@@ -2206,102 +2069,5 @@ static hipError_t launch_dt(const Args &a, float *probs, uint32_t *keep, hipStre
     return hipSuccess;
 }
 
+}  // namespace
 }  // namespace mis
-
-extern "C" {
-
-size_t mis_workspace_bytes(int64_t B, int64_t V, int dtype)
-{
-    (void)dtype;
-    if (B <= 0 || V <= 0) return 256;
-    return mis::make_layout(B, V, dtype).total;
-}
-
-int mis_workspace_init(void *workspace, size_t workspace_bytes, void *stream)
-{
-    if (!workspace) return MIS_ERR_INVALID_ARG;
-    if (((uintptr_t)workspace & 255u) != 0 || workspace_bytes < mis::CTL_PREFIX) return MIS_ERR_WORKSPACE;
-    const hipError_t e = hipMemsetAsync(workspace, 0, mis::CTL_PREFIX, (hipStream_t)stream);
-    if (e != hipSuccess) { mis::g_last_hip = (int)e; return MIS_ERR_HIP; }
-    return MIS_OK;
-}
-
-static int sample_impl(const void *logits, int dtype, int64_t B, int64_t V, int64_t row_stride,
-                       const mis_row_params *params, int64_t *out_ids, int32_t *out_status, float *out_probs,
-                       uint32_t *out_keep, void *workspace, size_t workspace_bytes, void *stream,
-                       unsigned kinds, void *const *events, int nev)
-{
-    using namespace mis;
-    if (dtype < 0 || dtype > 2 || B < 0 || V <= 0 || row_stride < V) return MIS_ERR_INVALID_ARG;
-    if (B == 0) return MIS_OK;
-    if (!logits || !params || !out_ids || !workspace) return MIS_ERR_INVALID_ARG;
-    if (V > (int64_t)1 << 30 || B > 0x7fffffff) return MIS_ERR_UNSUPPORTED;
-    const Layout L = make_layout(B, V, dtype);
-    if (L.G > G_MAX || (int64_t)L.B * L.G > 0x7fffffff) return MIS_ERR_UNSUPPORTED;
-    if (workspace_bytes < L.total || ((uintptr_t)workspace & 255u) != 0) return MIS_ERR_WORKSPACE;
-    const int esz = dtype == MIS_DTYPE_F32 ? 4 : 2;
-    Args a;
-    a.logits = (const char *)logits;
-    a.V = V;
-    a.stride_bytes = row_stride * esz;
-    a.vec_ok = (((uintptr_t)logits & 15u) == 0 && (a.stride_bytes & 15) == 0) ? 1 : 0;
-    a.params = params;
-    a.L = L;
-    a.ws = (char *)workspace;
-    a.out_ids = out_ids;
-    a.out_status = out_status;
-    hipStream_t st = (hipStream_t)stream;
-    hipError_t e;
-    if (dtype == MIS_DTYPE_F32) e = launch_dt<F32>(a, out_probs, out_keep, st, kinds, events, nev);
-    else if (dtype == MIS_DTYPE_F16) e = launch_dt<F16>(a, out_probs, out_keep, st, kinds, events, nev);
-    else e = launch_dt<BF16>(a, out_probs, out_keep, st, kinds, events, nev);
-    if (e != hipSuccess) { g_last_hip = (int)e; return MIS_ERR_HIP; }
-    return MIS_OK;
-}
-
-int mis_sample(const void *logits, int dtype, int64_t B, int64_t V, int64_t row_stride,
-               const mis_row_params *params, int64_t *out_ids, int32_t *out_status, float *out_probs,
-               uint32_t *out_keep, void *workspace, size_t workspace_bytes, void *stream)
-{
-    return sample_impl(logits, dtype, B, V, row_stride, params, out_ids, out_status, out_probs, out_keep,
-                       workspace, workspace_bytes, stream, MIS_KIND_ALL, nullptr, 0);
-}
-
-int mis_sample_profiled(const void *logits, int dtype, int64_t B, int64_t V, int64_t row_stride,
-                        const mis_row_params *params, int64_t *out_ids, int32_t *out_status, float *out_probs,
-                        uint32_t *out_keep, void *workspace, size_t workspace_bytes, void *stream,
-                        void *const *events)
-{
-    if (!events || !events[0] || !events[1] || !events[2]) return MIS_ERR_INVALID_ARG;
-    return sample_impl(logits, dtype, B, V, row_stride, params, out_ids, out_status, out_probs, out_keep,
-                       workspace, workspace_bytes, stream, MIS_KIND_ALL, events, 3);
-}
-
-int mis_sample_ex(const void *logits, int dtype, int64_t B, int64_t V, int64_t row_stride,
-                  const mis_row_params *params, int64_t *out_ids, int32_t *out_status, float *out_probs,
-                  uint32_t *out_keep, void *workspace, size_t workspace_bytes, void *stream, unsigned kinds,
-                  void *const *events)
-{
-    if ((kinds & ~(unsigned)MIS_KIND_ALL) != 0u) return MIS_ERR_INVALID_ARG;
-    if (events && (!events[0] || !events[1] || !events[2] || !events[3])) return MIS_ERR_INVALID_ARG;
-    return sample_impl(logits, dtype, B, V, row_stride, params, out_ids, out_status, out_probs, out_keep,
-                       workspace, workspace_bytes, stream, kinds, events, 4);
-}
-
-const char *mis_strerror(int code)
-{
-    switch (code) {
-    case MIS_OK: return "ok";
-    case MIS_ERR_INVALID_ARG: return "invalid argument";
-    case MIS_ERR_WORKSPACE: return "workspace too small or not 256-byte aligned";
-    case MIS_ERR_HIP: return "HIP launch failed";
-    case MIS_ERR_UNSUPPORTED: return "shape not supported (V > 2^30, B > 65535 or too many chunks)";
-    default: return "unknown error";
-    }
-}
-
-int mis_last_hip_error(void) { return mis::g_last_hip; }
-
-int mis_abi_version(void) { return MIS_ABI_VERSION; }
-
-}  // extern "C"

@@ -1,0 +1,21 @@
+// mis_launch.h -- the per-dtype launch sequences, one per translation unit
+// (mis_f32.hip, mis_f16.hip, mis_bf16.hip), called by the C ABI (mis_api.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "mis_layout.h"
+
+namespace mis {
+
+// Launches one sampling step over a.L.B rows on `st` (see launch_dt in
+// mis_kernels.h): ev/nev are the optional profiling events, kinds the
+// row-kind hint.
+hipError_t launch_f32(const Args &a, float *probs, uint32_t *keep, hipStream_t st, unsigned kinds,
+                      void *const *ev, int nev);
+hipError_t launch_f16(const Args &a, float *probs, uint32_t *keep, hipStream_t st, unsigned kinds,
+                      void *const *ev, int nev);
+hipError_t launch_bf16(const Args &a, float *probs, uint32_t *keep, hipStream_t st, unsigned kinds,
+                       void *const *ev, int nev);
+
+}  // namespace mis

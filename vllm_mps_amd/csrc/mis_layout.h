@@ -1,0 +1,148 @@
+// mis_layout.h -- workspace layout, per-call arguments and the limits shared
+// by the kernels (mis_kernels.h) and the host-side C ABI (mis_api.hip).
+#pragma once
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "mis_sampler.h"
+
+namespace mis {
+
+constexpr int NT = 256;            // threads per workgroup (4 waves of 64)
+constexpr int NWAVE = NT / 64;
+
+constexpr int K_SMALL = 1024;      // largest k' served by the candidate path
+constexpr int CAND_CAP = 2048;     // candidates one chunk may emit
+constexpr int SURV_CAP = 1024;     // top-k survivors / top-p window held in LDS
+constexpr int K_PROBE = 512;       // fp16/bf16 top-p rows look for their cut among this many largest values
+                                   // first (ties at the last one stay within SURV_CAP)
+constexpr int EPT_DEFAULT = 32;    // elements per thread of the chunk pass (64 when G would exceed G_MAX)
+constexpr int CCAP = 8192;         // small-k candidates of a row cached in LDS (64 KB)
+constexpr int G_MAX = 256;         // chunks per row
+constexpr int CB_N = 16;           // coarse top-p bins (lane-private)
+constexpr float CB_SCALE = 0.5f;   // coarse bin = floor(y * CB_SCALE): 2 units of y
+constexpr int REGION_MAX = 16;     // L1 bins per 16-bit chain pass at most (re-read path)
+constexpr int RUN_CAP = REGION_MAX * 256;
+constexpr int TIE_CAP = 1024;
+constexpr uint32_t NCAND_OVERFLOW = 0xffffffffu;
+constexpr int32_t IDX_ALL = 0x7fffffff;
+
+enum : int { M_BAD = 0, M_GREEDY = 1, M_SMALLK = 2, M_LARGEK = 3, M_TOPP = 4, M_TEMP = 5 };
+enum : uint32_t { FLAG_NAN = 1u, FLAG_PINF = 2u };
+
+// ------------------------------------------------------------------ workspace
+
+// The workspace keeps no state between calls: every word a call reads it has
+// written earlier in the same call.
+constexpr size_t CTL_PREFIX = 256;
+
+struct ChunkSum {               // 64 B per (row, chunk)
+    uint32_t xkey;              // argmax key of the raw logits (NaN = 0xffffffff)
+    int32_t xarg;
+    float ymax;                 // max scaled logit of the chunk
+    uint32_t flags;
+    uint32_t ncand;             // small-k candidates written, or NCAND_OVERFLOW
+    uint32_t nfin;              // finite elements of the chunk
+    uint32_t kc;                // small-k: non-candidates have scaled keys < kc
+    uint32_t trunc;             // small-k: some finite element was not emitted
+    double S;                   // sum of weights relative to the chunk max
+    double pad[3];
+};
+
+// per-(row, chunk) coarse mass bins of an fp32 top-p row
+struct RoundBuf {               // 256 B
+    double coarse[CB_N];        // mass per coarse bin (relative to the chunk max)
+    double S;                   // sum of weights relative to the chunk max
+    double pad[15];
+};
+static_assert(sizeof(RoundBuf) == 256, "RoundBuf size");
+
+struct RowOut {                 // 64 B per row, read by k_emit
+    int64_t id;
+    int32_t status;
+    int32_t mode;
+    float m;                    // row max of y
+    uint32_t cut_key;           // kept iff key > cut_key or (key == cut_key and j <= cut_i)
+    int32_t cut_i;
+    int32_t pad;
+    double S;                   // sum of kept weights exp(y - m)
+    double pad2[3];
+};
+
+struct Cand { float x; int32_t idx; };
+struct Elem { uint32_t key; int32_t idx; };
+
+// fp32 top-p passes (k_tp_*): per (row, chunk) fine bins over the row's
+// coarse band, per row the band keys, per-chunk kept masses and survivors
+constexpr int FH = 512;             // fine bins per chunk over the coarse band
+constexpr double FIX_ONE = 1099511627776.0;  // 2^40: fine-bin masses as integers of exp(y - m)
+struct TopChunk {
+    double above;                   // float64 mass of the chunk's elements above the coarse band
+    double pad[31];
+    uint32_t cnt[FH];
+    unsigned long long mass[FH];
+};
+static_assert(sizeof(TopChunk) % 256 == 0, "TopChunk size");
+enum : uint32_t { TR_NONE = 0, TR_ACTIVE = 1, TR_DEFER = 2 };
+struct TopRow {
+    uint32_t status, count;         // TR_*; survivors appended by the collect pass
+    uint32_t klo, khi;              // coarse band (row keys)
+    uint32_t xlo, xhi;              // its raw-key interval
+    int32_t ja, jb;                 // final band: fine bins [ja, jb]
+    uint32_t pad1[2];
+    float m, lo, scf, T;            // row max of y; fine-bin grid y -> (y - lo) * scf; temperature
+    double S, A, fix_err;           // sum of exp(y - m), top_p * S, bound of the fixed-point sums
+    double pad[22];
+    double cw[G_MAX];               // per-chunk kept mass above the final band
+    Elem list[SURV_CAP];            // the final band's elements
+};
+static_assert(sizeof(TopRow) % 256 == 0, "TopRow size");
+
+struct Layout {
+    int64_t B, V;
+    int ept, G;
+    size_t rowout, chunks, rbuf, cand, topc, topr, total;
+};
+
+inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+// Elements per thread: 16 (chunks of 4096 elements; 16 vector registers of
+// logits per thread keep the chunk pass at six or more waves per SIMD), 64
+// when the row would need more than G_MAX chunks.
+inline Layout make_layout(int64_t B, int64_t V, int dtype)
+{
+    Layout L;
+    L.B = B; L.V = V;
+    auto chunks = [&](int ept) { return (V + (int64_t)NT * ept - 1) / ((int64_t)NT * ept); };
+    L.ept = EPT_DEFAULT;
+    if (chunks(L.ept) > G_MAX) L.ept = 64;
+    L.G = (int)chunks(L.ept);
+    const size_t BG = (size_t)B * L.G;
+    size_t off = CTL_PREFIX;
+    L.rowout = off; off = align256(off + sizeof(RowOut) * (size_t)B);
+    L.chunks = off; off = align256(off + sizeof(ChunkSum) * BG);
+    L.rbuf = off;   off = align256(off + sizeof(RoundBuf) * BG);
+    L.cand = off;   off = align256(off + sizeof(Cand) * (size_t)CAND_CAP * BG);
+    // fp32 top-p: per-chunk fine bins and per-row state of the top-p passes
+    const bool f32 = dtype == MIS_DTYPE_F32;
+    L.topc = off;   off = align256(off + (f32 ? sizeof(TopChunk) * BG : 0));
+    L.topr = off;   off = align256(off + (f32 ? sizeof(TopRow) * (size_t)B : 0));
+    L.total = off;
+    return L;
+}
+
+
+struct Args {
+    const char *logits;
+    int64_t V;
+    int64_t stride_bytes;
+    int vec_ok;
+    const mis_row_params *params;
+    Layout L;
+    char *ws;
+    int64_t *out_ids;
+    int32_t *out_status;
+};
+
+}  // namespace mis
