@@ -51,10 +51,8 @@ enum {
                                   uniform NaN (core/sequence.py:41-61 raises ValueError) */
     MIS_ROW_INVALID = 2,       /* NaN or +inf scaled logits, or nothing left to sample
                                   (torch.multinomial raises RuntimeError, model/sampler.py:59) */
-    MIS_ROW_UNSUPPORTED = 3,   /* fp16/bf16 logits with a top-k threshold that needs the
-                                  full-row radix descent (1024 < k' < V, or more than 2048
-                                  candidates tied at one chunk's k'-th value): not served
-                                  by this build */
+    MIS_ROW_UNSUPPORTED = 3,   /* reserved: not produced by this build (every row mode is
+                                  served) */
     MIS_ROW_INTERNAL = 4       /* reserved: not produced by this build */
 };
 

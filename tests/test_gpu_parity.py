@@ -99,14 +99,7 @@ def test_neg_inf_and_ties(dtype, device):
     _run("neg inf + ties", w, device)
 
 
-# fp16/bf16 rows whose top-k threshold needs the full-row radix descent
-# (1024 < k' < V, or candidate overflow) faulted the GPU in the single-launch
-# kernel and are switched off (status MIS_ROW_UNSUPPORTED) until the cause is
-# found; their GPU cases stay skipped.
-SKIP16 = pytest.mark.skip(reason="16-bit radix-descent rows switched off (GPU fault, cause not yet found)")
-
-
-@pytest.mark.parametrize("dtype", ["f32", pytest.param("f16", marks=SKIP16), pytest.param("bf16", marks=SKIP16)])
+@pytest.mark.parametrize("dtype", ["f32", "f16", "bf16"])
 def test_large_k_generic_path(dtype, device):
     V = 40000
     w = H.synthetic(dtype, 4, V, seed=31, temperature=[1.0, 0.9, 1.1, 1.0],
@@ -114,13 +107,23 @@ def test_large_k_generic_path(dtype, device):
     _run("large k", w, device)
 
 
-@pytest.mark.parametrize("dtype", ["f32", pytest.param("f16", marks=SKIP16), pytest.param("bf16", marks=SKIP16)])
+@pytest.mark.parametrize("dtype", ["f32", "f16", "bf16"])
 def test_candidate_overflow(dtype, device):
     # every element equal: each chunk's top-k' ties exceed the candidate buffer
     V = 50000
     w = H.synthetic(dtype, 3, V, seed=41, temperature=1.0, top_k=[10, 3, 1000], top_p=[1.0, 0.5, 0.9])
     w.logits[:] = w.logits[:, :1]
     _run("candidate overflow", w, device)
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+def test_topk_ties_past_survivor_list(dtype, device):
+    # N(0, 3^2) rows at T = 0.8: the 1000th / 1024th largest 16-bit value is
+    # tied with enough others that more than 1024 elements survive top-k, so
+    # the small-k path hands the row to the radix descent
+    w = H.synthetic(dtype, 4, 128256, seed=77, temperature=0.8, top_k=[1000, 1024, 1000, 1024],
+                    top_p=[1.0, 1.0, 0.9, 1.0])
+    _run("top-k ties past the survivor list", w, device)
 
 
 @pytest.mark.parametrize("seed", range(6))

@@ -160,7 +160,9 @@ __device__ __forceinline__ bool kept_by_cut(uint32_t key, int64_t j, uint32_t cu
 // recomputed in each pass instead of being kept live for all EPT elements.
 __device__ __forceinline__ float opaque(float v)
 {
+#if defined(__HIP_DEVICE_COMPILE__)
     asm volatile("" : "+v"(v));
+#endif
     return v;
 }
 
@@ -603,11 +605,6 @@ __device__ __forceinline__ void topp_cut_generic(Smem &sm, const RowCx &c, float
 template <int DT>
 __device__ __forceinline__ void final_generic(Smem &sm, const RowCx &c, const RowPlan &pl, RowOut *ro, const Args &a)
 {
-    if (DT != F32 && pl.kk > 0) {
-        // the 16-bit top-k radix descent is switched off in this build
-        write_row(ro, a, c.row, -1, MIS_ROW_UNSUPPORTED, pl.mode, c.m, 0u, 0, 0.0);
-        return;
-    }
     const double md = (double)c.m;
     const uint32_t kneg = row_key(-INFINITY, DT);
     __syncthreads();

@@ -185,7 +185,7 @@ class Sampler:
             if s == _native.ROW_INVALID:
                 raise RuntimeError("invalid probability distribution (NaN/inf logits or nothing left to sample)")
             if s == _native.ROW_UNSUPPORTED:
-                raise NotImplementedError("fp16/bf16 logits with 1024 < top_k < V are not served by this build")
+                raise NotImplementedError("row not served by the sampler library (status 3)")
             if s != _native.ROW_OK:
                 raise _native.MisError(f"sampler row status {s}")
         return ids.tolist()
