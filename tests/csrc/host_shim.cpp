@@ -19,6 +19,21 @@ void shim_dexp_array(const double *d, double *out, int64_t n)
     for (int t = 0; t < mis::ETAB_N; ++t) mis::exp_table(tab, t);
     for (int64_t i = 0; i < n; ++i) out[i] = mis::dexp(d[i], tab);
 }
+float shim_div_rcp(float x, float T) { return mis::div_rcp(x, T, 1.0f / T); }
+// bit patterns [lo, hi) of x (step `stride`): mismatches of div_rcp against
+// IEEE x / T, the first one in *first (NaN quotients compare as NaN)
+uint64_t shim_div_rcp_sweep(float T, uint64_t lo, uint64_t hi, uint64_t stride, uint32_t *first)
+{
+    const float r = 1.0f / T;
+    uint64_t bad = 0;
+    for (uint64_t b = lo; b < hi; b += stride) {
+        const float x = mis::bits_f32((uint32_t)b);
+        const float a = mis::div_rcp(x, T, r), e = x / T;
+        const bool same = (a != a && e != e) || mis::f32_bits(a) == mis::f32_bits(e);
+        if (!same && bad++ == 0) *first = (uint32_t)b;
+    }
+    return bad;
+}
 // naive reference for chain_add_n: one float addition per step
 float shim_chain_naive(float F, float p, uint64_t n)
 {

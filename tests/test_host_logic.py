@@ -20,7 +20,7 @@ F32, F16, BF16 = 0, 1, 2
 @pytest.fixture(scope="module")
 def shim(tmp_path_factory):
     out = str(tmp_path_factory.mktemp("shim") / "host_shim.so")
-    subprocess.run(["g++", "-O2", "-fPIC", "-shared", "-ffp-contract=off", "-o", out,
+    subprocess.run(["g++", "-O2", "-mfma", "-fPIC", "-shared", "-ffp-contract=off", "-o", out,
                     os.path.join(HERE, "csrc", "host_shim.cpp")], check=True)
     L = ctypes.CDLL(out)
     f, u64, i = ctypes.c_float, ctypes.c_uint64, ctypes.c_int
@@ -33,6 +33,9 @@ def shim(tmp_path_factory):
     L.shim_argmax_key.argtypes = [f]; L.shim_argmax_key.restype = ctypes.c_uint32
     L.shim_rn_dtype_array.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, i]
     L.shim_dexp_array.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64]
+    L.shim_div_rcp.argtypes = [f, f]; L.shim_div_rcp.restype = f
+    L.shim_div_rcp_sweep.argtypes = [f, u64, u64, u64, ctypes.POINTER(ctypes.c_uint32)]
+    L.shim_div_rcp_sweep.restype = u64
     return L
 
 
@@ -146,3 +149,35 @@ def test_dexp_relative_error(shim):
     assert np.all(np.abs(out[sub].astype(np.longdouble) - ref[sub]) <= np.longdouble(2.0 ** -1074))
     assert np.all(out[d == 0.0] == 1.0)
     assert np.all(out[d <= -745.0] == 0.0)
+
+
+# temperatures of the configs (C2 0.8, C3's seeded U[0.5, 1.5] draws, the edge
+# tests' extremes) and a few with long reciprocal expansions
+def _config_temperatures():
+    from vllm_mps_amd import workloads as W
+    c3 = W.make_c3().temperature
+    return sorted({0.8, 1.0, 0.7, 1.3, 0.9, 1.1, 1.2, 0.6, 1.4, 0.001, 0.01, 50.0, 7.0, 0.5173, 1.2345678,
+                   1.4999, 0.3, 2.0, *map(float, c3[::16])})
+
+
+def test_div_rcp_exhaustive_binade(shim):
+    """div_rcp (Markstein reciprocal division, run on every element the chunk
+    pass scales) == IEEE x / T bit for bit.  For a fixed T the quotient's
+    rounding depends only on x's significand (a power-of-two factor of x is
+    exact), so every float in [1, 2) covers every normal x whose quotient
+    stays inside div_rcp_safe's range; outside it div_rcp divides."""
+    first = ctypes.c_uint32(0)
+    lo, hi = 0x3F800000, 0x40000000  # [1, 2)
+    for T in _config_temperatures():
+        bad = shim.shim_div_rcp_sweep(ctypes.c_float(T), lo, hi, 1, ctypes.byref(first))
+        assert bad == 0, (T, bad, hex(first.value))
+
+
+def test_div_rcp_every_binade_strided(shim):
+    """Every sign, exponent, subnormal and special value (stride 7 over all
+    2^32 bit patterns) at two temperatures, including the range edges where
+    div_rcp falls back to the division."""
+    first = ctypes.c_uint32(0)
+    for T in (0.8, 1.2345678):
+        bad = shim.shim_div_rcp_sweep(ctypes.c_float(T), 0, 1 << 32, 7, ctypes.byref(first))
+        assert bad == 0, (T, bad, hex(first.value))

@@ -6,9 +6,8 @@ against something that fixes it independently:
 * temperature     torch's own ``x / T`` on f32/f16/bf16 tensors
 * dtype rounding  numpy float16 and torch bfloat16 conversions
 * top-k           np.partition k-th value with ``>=`` and brute force
-* 16-bit top-p    torch's own rounding chain (stable sort, dtype softmax,
-                  cumsum, subtraction, dtype compare) -- the reference's
-                  op sequence, model/sampler.py:46-55
+* 16-bit top-p    torch's own rounding chain, every row accounted for
+                  (tests/test_oracle_torch.py)
 * fp32 top-p      torch float64 softmax/cumsum; exact Decimal arithmetic on
                   tiny rows
 * draw            searchsorted on a float64 CDF; chi-square frequencies
@@ -27,7 +26,6 @@ import numpy as np
 import pytest
 import torch
 
-from oracle import faithful
 from oracle import oracle as O
 from tests import harness as H
 from vllm_mps_amd import workloads as W
@@ -123,47 +121,7 @@ def test_topk_brute_force_tiny():
 
 
 # --------------------------------------------------------- 16-bit top-p chain
-
-def torch_chain_keep(t: torch.Tensor, T: float, k: int, p: float):
-    """The reference op sequence (contract mode: stable sort) on a 16-bit row;
-    returns the keep mask and torch's sorted probabilities."""
-    _, probs = faithful.row_sample(t, T, k, p, uniform=0.5, literal=False, return_probs=True)
-    return (probs > 0).numpy()
-
-
-@pytest.mark.parametrize("dtype", ["f16", "bf16"])
-def test_chain16_matches_torch(dtype):
-    """Oracle's 16-bit top-p == torch's own chain whenever torch's dtype
-    softmax equals RN16(RN32(exact)) on the row (it differs only on
-    near-midpoint elements, where torch's float arithmetic decides)."""
-    rng = np.random.default_rng(7)
-    cases, agree_p = 0, 0
-    for trial in range(40):
-        V = int(rng.choice([50, 1000, 32000, 128256]))
-        T = float(rng.choice([0.7, 1.0, 1.3]))
-        k = int(rng.choice([0, 0, 50, 1000]))
-        p = float(rng.choice([0.9, 0.95, 0.5, 0.01, 0.99]))
-        w = H.synthetic(dtype, 1, V, seed=100 + trial, temperature=T, top_k=k, top_p=p,
-                        scale=float(rng.choice([1.0, 2.5, 3.0])))
-        r = run(w)
-        t = torch_tensor(w.logits, dtype)[0]
-        keep_t = torch_chain_keep(t, T, k, p)
-        # does torch's dtype softmax of the (top-k filtered) sorted row equal RN16(RN32(exact))?
-        z = t / T
-        if k > 0:
-            kth = torch.topk(z, min(k, V)).values[-1]
-            z = torch.where(z < kth, torch.full_like(z, float("-inf")), z)
-        s = torch.sort(z, descending=True, stable=True).values
-        pt = torch.softmax(s, -1).float().numpy()
-        sd = s.double().numpy()
-        e = np.exp(sd - sd.max())
-        pe = O.round_to((e / e.sum()).astype(np.float32), dtype)
-        cases += 1
-        if np.array_equal(pt, pe):
-            agree_p += 1
-            assert np.array_equal(keep_t, r["keep"][0]), (V, T, k, p)
-    print(f"chain16 {dtype}: masks compared on {agree_p} of {cases} rows")
-    assert agree_p >= cases * 0.6, (agree_p, cases)
+# (pinned row by row against torch's own chain in tests/test_oracle_torch.py)
 
 
 # ------------------------------------------------------------ fp32 top-p

@@ -130,6 +130,35 @@ MIS_HD float value_of_row_key(uint32_t k, int dt)
 // (torch.argmax returns the first NaN).
 MIS_HD uint32_t argmax_key(float x) { return (x != x) ? 0xffffffffu : key_of_f32(x); }
 
+// ---------------------------------------------------------- temperature division
+//
+// y = RN(x / T) from the row's reciprocal r = RN(1/T): q0 = RN(x * r) lies
+// within 1.5 ulp of x / T, every residual x - q * T is then exact in one FMA,
+// and two Newton corrections q + (x - q * T) * r give RN(x / T) (Markstein's
+// theorem: the second correction starts from a faithful quotient).
+// div_rcp_safe() names the inputs this holds for: quotients away from
+// overflow, and x and quotients away from the range where a residual could
+// underflow.  Elsewhere the callers divide.  tests/test_host_logic.py checks
+// the pair bit for bit against IEEE x / T, exhaustively over every float x
+// for one temperature and on samples for the configs' temperatures.
+MIS_HD bool div_rcp_safe(float x, float q0)
+{
+    const float aq = fabsf(q0);
+    return aq < 0x1p127f && aq >= 0x1p-100f && fabsf(x) >= 0x1p-100f;
+}
+MIS_HD float div_rcp_core(float x, float T, float r, float q0)
+{
+    const float e0 = fmaf(-q0, T, x);
+    const float q1 = fmaf(e0, r, q0);
+    const float e1 = fmaf(-q1, T, x);
+    return fmaf(e1, r, q1);
+}
+MIS_HD float div_rcp(float x, float T, float r)
+{
+    const float q0 = x * r;
+    return div_rcp_safe(x, q0) ? div_rcp_core(x, T, r, q0) : x / T;
+}
+
 // ---------------------------------------------------------- 16-bit top-p chain
 //
 // torch's top-p on fp16/bf16 tensors (model/sampler.py:48-51) evaluates, in

@@ -57,23 +57,8 @@ template <int DT> __device__ __forceinline__ float scale_y(float x, float T)
     return DT == F32 ? q : rn_dtype(q, DT);
 }
 
-// The same quotient through the row's reciprocal r = RN(1/T): q0 = RN(x*r)
-// lies within 1.5 ulp of x/T, every residual x - q*T is then exact in one
-// FMA, and two Newton corrections q + (x - q*T)*r give RN(x/T) (Markstein's
-// theorem: the second correction starts from a faithful quotient).  Quotients
-// near overflow, tiny x or quotients (whose residuals would underflow) and
-// infinite x take the generic division.  Checked bit for bit against x / T over every float x for a set
-// of temperatures (tests/test_host_logic.py samples the same property).
-__device__ __forceinline__ float div_rcp(float x, float T, float r)
-{
-    const float q0 = x * r;
-    const float aq = fabsf(q0);
-    if (!(aq < 0x1p127f) || aq < 0x1p-100f || fabsf(x) < 0x1p-100f) return x / T;
-    const float e0 = fmaf(-q0, T, x);
-    const float q1 = fmaf(e0, r, q0);
-    const float e1 = fmaf(-q1, T, x);
-    return fmaf(e1, r, q1);
-}
+// The same quotient through the row's reciprocal r = RN(1/T): div_rcp()
+// (mis_common.h), the generic division where it does not apply.
 template <int DT> __device__ __forceinline__ float scale_r(float x, float T, float r)
 {
     const float q = div_rcp(x, T, r);
@@ -91,12 +76,9 @@ template <int DT, int N> __device__ __forceinline__ void scale_all(float (&x)[N]
     for (int i = 0; i < N; ++i) {
         const float xi = x[i];
         const float q0 = xi * r;
-        const float aq = fabsf(q0);
-        const bool sl = !(aq < 0x1p127f) || aq < 0x1p-100f || fabsf(xi) < 0x1p-100f;
-        const float e0 = fmaf(-q0, T, xi);
-        const float q1 = fmaf(e0, r, q0);
-        const float e1 = fmaf(-q1, T, xi);
-        x[i] = sl ? xi : fmaf(e1, r, q1);
+        const bool sl = !div_rcp_safe(xi, q0);
+        const float q = div_rcp_core(xi, T, r, q0);
+        x[i] = sl ? xi : q;
         slow |= sl ? (1ull << i) : 0ull;
     }
     if (__ballot(slow != 0ull) != 0ull) {
