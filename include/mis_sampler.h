@@ -47,10 +47,11 @@ enum {
 /* per-row status written to out_status */
 enum {
     MIS_ROW_OK = 0,
-    MIS_ROW_BAD_PARAM = 1,     /* temperature < 0 or NaN, top_k < 0, top_p <= 0 or NaN,
-                                  uniform NaN (core/sequence.py:41-61 raises ValueError) */
-    MIS_ROW_INVALID = 2,       /* NaN or +inf scaled logits, or nothing left to sample
-                                  (torch.multinomial raises RuntimeError, model/sampler.py:59) */
+    MIS_ROW_BAD_PARAM = 1,     /* temperature < 0, top_k < 0, top_p <= 0 or NaN, uniform NaN
+                                  (core/sequence.py:41-61 raises ValueError) */
+    MIS_ROW_INVALID = 2,       /* temperature NaN, NaN or +inf scaled logits, or nothing left
+                                  to sample (torch.multinomial raises RuntimeError,
+                                  model/sampler.py:59) */
     MIS_ROW_UNSUPPORTED = 3,   /* reserved: not produced by this build (every row mode is
                                   served) */
     MIS_ROW_INTERNAL = 4       /* reserved: not produced by this build */

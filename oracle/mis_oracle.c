@@ -34,8 +34,8 @@
  *                                  w_j = exp(z_j - m); clamped to the last kept
  *                                  index.
  *
- * Row status: 0 ok, 1 bad parameter (T < 0 or NaN, top_k < 0, top_p <= 0 or
- * NaN), 2 invalid distribution (NaN or +inf scaled logits, or nothing kept;
+ * Row status: 0 ok, 1 bad parameter (T < 0, top_k < 0, top_p <= 0 or NaN),
+ * 2 invalid distribution (T NaN, NaN or +inf scaled logits, or nothing kept;
  * torch.multinomial raises on these).  ids = -1 for rows with status != 0.
  *
  * Debug outputs: probs[j] = RN_dtype(RN32(softmax over kept)) as float, 0 for
@@ -172,7 +172,10 @@ static void row_sample(int dt, int64_t V, const void *row, orc_params P,
     if (keep) memset(keep, 0, (size_t)V);
 
     float T = P.temperature;
-    if (!(T >= 0.0f) || P.top_k < 0 || !(P.top_p > 0.0f)) { R->status = ORC_BAD_PARAM; return; }
+    if (T < 0.0f || P.top_k < 0 || !(P.top_p > 0.0f)) { R->status = ORC_BAD_PARAM; return; }
+    /* T = NaN passes SamplingParams' check (core/sequence.py:43: NaN < 0 is
+       false); logits / NaN is NaN and torch.multinomial raises (:59) */
+    if (T != T) { R->status = ORC_INVALID; return; }
 
     if (T == 0.0f) { /* greedy, sampler.py:33-34 */
         int64_t best = 0;

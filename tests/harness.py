@@ -12,7 +12,8 @@ def params_of(w: W.Workload) -> np.ndarray:
     return O.make_params(w.temperature, w.top_k, w.top_p, w.uniform)
 
 
-def run_gpu(w: W.Workload, device, debug: bool = True, stride_pad: int = 0, sampler=None, kinds=None) -> dict:
+def run_gpu(w: W.Workload, device, debug: bool = True, stride_pad: int = 0, sampler=None, kinds=None,
+            probs: bool = True) -> dict:
     import torch
     from vllm_mps_amd.sampler import Sampler, pack_params
 
@@ -25,14 +26,15 @@ def run_gpu(w: W.Workload, device, debug: bool = True, stride_pad: int = 0, samp
     packed = pack_params(torch.from_numpy(w.temperature).to(device), torch.from_numpy(w.top_k).to(device),
                          torch.from_numpy(w.top_p).to(device), torch.from_numpy(w.uniform).to(device))
     status = torch.full((B,), -7, dtype=torch.int32, device=device)
-    probs = torch.full((B, V), -1.0, dtype=torch.float32, device=device) if debug else None
+    pr = torch.full((B, V), -1.0, dtype=torch.float32, device=device) if debug and probs else None
     keep = torch.zeros((B, (V + 31) // 32), dtype=torch.int32, device=device) if debug else None
     s = Sampler() if sampler is None else sampler
-    ids = s.sample_packed(t, packed, status_out=status, probs_out=probs, keep_out=keep, kinds=kinds)
+    ids = s.sample_packed(t, packed, status_out=status, probs_out=pr, keep_out=keep, kinds=kinds)
     torch.cuda.synchronize(device)
     out = dict(ids=ids.cpu().numpy(), status=status.cpu().numpy())
-    if debug:
-        out["probs"] = probs.cpu().numpy()
+    if pr is not None:
+        out["probs"] = pr.cpu().numpy()
+    if keep is not None:
         out["keep"] = C.unpack_keep(keep.cpu().numpy(), V)
     return out
 

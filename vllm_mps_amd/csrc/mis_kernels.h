@@ -78,8 +78,10 @@ __device__ __forceinline__ RowPlan plan_row(const mis_row_params &P, int64_t V)
 {
     RowPlan r;
     r.T = P.temperature; r.top_p = P.top_p; r.u = P.uniform; r.kk = 0; r.topp = 0;
-    const bool bad = !(P.temperature >= 0.0f) || P.top_k < 0 || !(P.top_p > 0.0f) || !(P.uniform == P.uniform);
+    const bool bad = P.temperature < 0.0f || P.top_k < 0 || !(P.top_p > 0.0f) || !(P.uniform == P.uniform);
     if (bad) { r.mode = M_BAD; return r; }
+    // x / NaN is NaN everywhere: the reference's multinomial rejects the row
+    if (P.temperature != P.temperature) { r.mode = M_INVAL; return r; }
     if (P.temperature == 0.0f) { r.mode = M_GREEDY; return r; }
     int64_t kk = P.top_k > 0 ? ((int64_t)P.top_k < V ? (int64_t)P.top_k : V) : 0;
     if (kk >= V) kk = 0;  // k' = V keeps every element
@@ -1113,8 +1115,8 @@ __device__ __forceinline__ void leader_row(Smem &sm, RowCx &c, const RowPlan &pl
 {
     const int tid = threadIdx.x, row = c.row;
     const Layout &L = a.L;
-    if (pl.mode == M_BAD) {
-        write_row(ro, a, row, -1, MIS_ROW_BAD_PARAM, pl.mode, 0.0f, 0u, 0, 0.0);
+    if (pl.mode == M_BAD || pl.mode == M_INVAL) {
+        write_row(ro, a, row, -1, pl.mode == M_BAD ? MIS_ROW_BAD_PARAM : MIS_ROW_INVALID, pl.mode, 0.0f, 0u, 0, 0.0);
         return;
     }
     uint32_t k2 = 0u;
@@ -1333,7 +1335,7 @@ __global__ __launch_bounds__(NT) void k_sample(Args a, int part)
             }
             cs->xkey = bk; cs->xarg = bi;
         }
-    } else if (pl.mode != M_BAD) {
+    } else if (pl.mode != M_BAD && pl.mode != M_INVAL) {
         // ---- chunk max and flags
         float tmax = -INFINITY;
         uint32_t nan = 0u, nf = 0u;

@@ -28,7 +28,7 @@ constexpr int TIE_CAP = 1024;
 constexpr uint32_t NCAND_OVERFLOW = 0xffffffffu;
 constexpr int32_t IDX_ALL = 0x7fffffff;
 
-enum : int { M_BAD = 0, M_GREEDY = 1, M_SMALLK = 2, M_LARGEK = 3, M_TOPP = 4, M_TEMP = 5 };
+enum : int { M_BAD = 0, M_GREEDY = 1, M_SMALLK = 2, M_LARGEK = 3, M_TOPP = 4, M_TEMP = 5, M_INVAL = 6 };
 enum : uint32_t { FLAG_NAN = 1u, FLAG_PINF = 2u };
 
 // ------------------------------------------------------------------ workspace

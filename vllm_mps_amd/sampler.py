@@ -59,7 +59,9 @@ def host_row_params(params: Sequence[SamplingParams], dtype: torch.dtype) -> np.
         t = float(sp.temperature)
         t32 = np.float32(t)
         if t > 0.0 and t32 == 0.0:
-            t32 = np.float32(np.nan)  # divides by f32(T) = 0 in torch: invalid distribution
+            # torch divides by f32(T) = 0: inf / NaN logits, and multinomial
+            # raises; NaN selects that row status (invalid distribution)
+            t32 = np.float32(np.nan)
         f[i, 0] = t32
         out[i, 1] = int(min(max(int(sp.top_k), 0), 2**31 - 1)) if sp.top_k >= 0 else int(sp.top_k)
         p = float(sp.top_p)
@@ -172,12 +174,18 @@ class Sampler:
         if uniforms is None:
             uniforms = torch.rand(B, device=dev, dtype=torch.float32, generator=self.generator)
         packed = torch.empty((B, 4), dtype=torch.int32, device=dev)
-        packed[:, :3].copy_(host, non_blocking=False)
+        # staged through pinned host memory: the copy is queued on the stream
+        # and the host does not wait for the device
+        packed[:, :3].copy_(host.pin_memory(), non_blocking=True)
         packed[:, 3].copy_(uniforms.to(device=dev, dtype=torch.float32).view(torch.int32))
         return self.sample_packed(logits, packed, **buffers)
 
     # -- reference call surface -------------------------------------------
     def _checked(self, ids: torch.Tensor, status: torch.Tensor) -> list[int]:
+        """Host ints, raising as the reference does for a row it rejects:
+        ValueError for invalid parameters (core/sequence.py:41-61),
+        RuntimeError for an invalid distribution (torch.multinomial,
+        model/sampler.py:59)."""
         st = status.tolist()
         for s in st:
             if s == _native.ROW_BAD_PARAM:
