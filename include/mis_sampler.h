@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define MIS_ABI_VERSION 4
+#define MIS_ABI_VERSION 5
 
 /* logits element type */
 enum { MIS_DTYPE_F32 = 0, MIS_DTYPE_F16 = 1, MIS_DTYPE_BF16 = 2 };
@@ -121,14 +121,17 @@ int mis_sample_profiled(const void *logits, int dtype, int64_t B, int64_t V, int
 
 /*
  * Row kinds a batch holds, for mis_sample_ex(): a performance hint only.
- *   MIS_KIND_TOPP32  fp32 logits, 0 < temperature, top_k off (0 or >= V),
- *                    top_p < 1 (the rows the top-p passes serve)
- *   MIS_KIND_OTHER   every other row
+ *   MIS_KIND_TOPP32   fp32 logits, 0 < temperature, top_k off (0 or >= V),
+ *                     top_p < 1 (the rows the top-p passes serve)
+ *   MIS_KIND_OTHER    every other row
+ *   MIS_KIND_GENERIC  among the others, rows that take the generic row pass:
+ *                     0 < temperature and either top_k > 1024 (and < V) or
+ *                     fp16/bf16 logits with top_k off and top_p < 1
  * A clear bit lets the library skip the launches only that kind needs; the
  * results are the same for any `kinds` (rows of a kind whose bit is clear
  * take the generic path), so a wrong hint costs time, never correctness.
  */
-enum { MIS_KIND_TOPP32 = 1, MIS_KIND_OTHER = 2, MIS_KIND_ALL = 3 };
+enum { MIS_KIND_TOPP32 = 1, MIS_KIND_OTHER = 2, MIS_KIND_GENERIC = 4, MIS_KIND_ALL = 7 };
 
 /*
  * mis_sample() with a row-kind hint and optional events: NULL, or four

@@ -18,6 +18,7 @@ ROOT = os.path.dirname(os.path.dirname(HERE))
 CSRC = os.path.join(ROOT, "vllm_mps_amd", "csrc")
 OUT_DIR = os.path.join(HERE, "_build")
 EXE = os.path.join(OUT_DIR, "emu_driver")
+EXE_TRACE = os.path.join(OUT_DIR, "emu_driver_trace")
 UNITS = ["mis_api.hip", "mis_f32.hip", "mis_f16.hip", "mis_bf16.hip"]
 
 
@@ -37,26 +38,28 @@ def sources():
     return [os.path.join(CSRC, u) for u in UNITS] + [os.path.join(HERE, "emu.cpp")]
 
 
-def up_to_date() -> bool:
-    if not os.path.exists(EXE):
+def up_to_date(exe: str = EXE) -> bool:
+    if not os.path.exists(exe):
         return False
-    t = os.path.getmtime(EXE)
+    t = os.path.getmtime(exe)
     deps = sources() + [os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".h")]
     deps += [os.path.join(HERE, "include", "hip", "hip_runtime.h"), os.path.join(ROOT, "include", "mis_sampler.h")]
     return all(os.path.getmtime(d) <= t for d in deps)
 
 
-def build(verbose: bool = False, force: bool = False) -> str:
-    if not force and up_to_date():
-        return EXE
+def build(verbose: bool = False, force: bool = False, trace: bool = False) -> str:
+    """trace=True: the kernels' MIS_TRACE phase table as well (emu_driver_trace)."""
+    exe = EXE_TRACE if trace else EXE
+    if not force and up_to_date(exe):
+        return exe
     os.makedirs(OUT_DIR, exist_ok=True)
     cc = clangxx()
     inc = ["-I", os.path.join(HERE, "include"), "-I", os.path.join(ROOT, "include"), "-I", CSRC]
     objs, procs = [], []
     for src in sources():
-        obj = os.path.join(OUT_DIR, os.path.basename(src) + ".o")
+        obj = os.path.join(OUT_DIR, os.path.basename(src) + (".trace.o" if trace else ".o"))
         objs.append(obj)
-        cmd = [cc, *FLAGS, *inc, "-x", "c++", "-c", "-o", obj, src]
+        cmd = [cc, *FLAGS, *(["-DMIS_TRACE"] if trace else []), *inc, "-x", "c++", "-c", "-o", obj, src]
         if verbose:
             print(" ".join(cmd), flush=True)
         procs.append(subprocess.Popen(cmd, stderr=subprocess.PIPE, text=True))
@@ -68,10 +71,10 @@ def build(verbose: bool = False, force: bool = False) -> str:
     if errs:
         sys.stderr.write("\n".join(errs))
         raise RuntimeError("emulator build failed")
-    tmp = EXE + ".tmp"
+    tmp = exe + ".tmp"
     subprocess.run([cc, *FLAGS, "-o", tmp, *objs], check=True)
-    os.replace(tmp, EXE)
-    return EXE
+    os.replace(tmp, exe)
+    return exe
 
 
 if __name__ == "__main__":

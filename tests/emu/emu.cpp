@@ -235,6 +235,12 @@ void run_block()
 
 }  // namespace
 
+uint64_t clock_tick()
+{
+    static uint64_t t = 0;
+    return ++t;
+}
+
 const dim3 &thread_idx() { return g_blk.cur ? g_blk.cur->tid : g_zero; }
 const dim3 &block_idx() { return g_blk.bidx; }
 const dim3 &block_dim() { return g_blk.bdim; }
@@ -335,8 +341,12 @@ int main(int argc, char **argv)
     }
     fclose(f);
     const size_t ws_bytes = mis_workspace_bytes(B, V, dtype);
-    void *ws = aligned_alloc(256, (ws_bytes + 255) & ~(size_t)255);
+    // a MIS_TRACE build writes a [B][32] u64 timestamp table past the workspace
+    const char *trace_out = getenv("EMU_TRACE_OUT");
+    const size_t tr_bytes = trace_out ? (size_t)B * 32 * 8 : 0;
+    void *ws = aligned_alloc(256, (ws_bytes + tr_bytes + 255) & ~(size_t)255);
     memset(ws, 0xa5, ws_bytes);  // nothing may depend on the workspace's prior contents
+    if (tr_bytes) memset((char *)ws + ws_bytes, 0, tr_bytes);
     int64_t *ids = (int64_t *)malloc((size_t)B * 8);
     int32_t *status = (int32_t *)malloc((size_t)B * 4);
     const int64_t W = (V + 31) / 32;
@@ -352,6 +362,10 @@ int main(int argc, char **argv)
     fwrite(status, 4, (size_t)B, o);
     if (want) { fwrite(probs, 4, (size_t)(B * V), o); fwrite(keep, 4, (size_t)(B * W), o); }
     fclose(o);
+    if (trace_out) {
+        FILE *t = fopen(trace_out, "wb");
+        if (t) { fwrite((char *)ws + ws_bytes, 1, tr_bytes, t); fclose(t); }
+    }
     free(logits); free(params); free(ws); free(ids); free(status); free(probs); free(keep);
     return 0;
 }

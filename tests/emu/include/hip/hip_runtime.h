@@ -90,6 +90,11 @@ template <class T> inline T emu_first(T v, const char *site)
 #define __ballot(p) emu::wave_op(emu::OP_BALLOT, (uint64_t)((p) ? 1 : 0), 0, 64, EMU_SITE)
 #define __builtin_amdgcn_readfirstlane(v) emu_first((v), EMU_SITE)
 #define __builtin_amdgcn_exp2f(f) exp2f(f)
+// phase timestamps of a MIS_TRACE build: a global counter stands in for the
+// real-time clock, a plain store for the device-scope store
+namespace emu { uint64_t clock_tick(); }
+#define __builtin_amdgcn_s_memrealtime() emu::clock_tick()
+#define __hip_atomic_store(p, v, order, scope) (*(p) = (v))
 
 // HIP's device integer min / max
 template <class T> inline T min(T a, T b) { return b < a ? b : a; }

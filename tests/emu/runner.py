@@ -21,8 +21,10 @@ DTYPE_CODE = {"f32": 0, "f16": 1, "bf16": 2}
 MAGIC = 0x4D495345
 
 
-def run(w: W.Workload, debug: bool = True, kinds: int = 3, timeout: float = 600.0) -> dict:
-    exe = build_emu.build()
+def run(w: W.Workload, debug: bool = True, kinds: int = 7, timeout: float = 600.0, trace: bool = False) -> dict:
+    """trace=True: also returns the MIS_TRACE phase table (``trace`` [B, 32],
+    a logical clock: nonzero where a row passed that phase)."""
+    exe = build_emu.build(trace=trace)
     B, V = w.shape
     params = np.zeros((B, 4), dtype=np.int32)
     params.view(np.float32)[:, 0] = w.temperature
@@ -38,14 +40,20 @@ def run(w: W.Workload, debug: bool = True, kinds: int = 3, timeout: float = 600.
             f.write(logits.tobytes())
             f.write(params.tobytes())
         env = dict(os.environ, ASAN_OPTIONS="detect_leaks=0:abort_on_error=1:detect_stack_use_after_return=0")
+        ctr = os.path.join(td, "trace.bin")
+        if trace:
+            env["EMU_TRACE_OUT"] = ctr
         res = subprocess.run([exe, cin, cout], capture_output=True, text=True, timeout=timeout, env=env)
         if res.returncode != 0:
             raise RuntimeError(f"emulator failed ({res.returncode}):\n{res.stderr[-4000:]}")
         raw = open(cout, "rb").read()
+        tr = np.fromfile(ctr, dtype=np.uint64).reshape(B, 32) if trace else None
     off = 0
     ids = np.frombuffer(raw, np.int64, B, off); off += 8 * B
     status = np.frombuffer(raw, np.int32, B, off); off += 4 * B
     out = dict(ids=ids.copy(), status=status.copy())
+    if tr is not None:
+        out["trace"] = tr
     if debug:
         probs = np.frombuffer(raw, np.float32, B * V, off).reshape(B, V); off += 4 * B * V
         Wd = (V + 31) // 32

@@ -24,7 +24,7 @@ def _emu(w, **kw):
     return runner.run(w, **kw)
 
 
-def _check(name, w, kinds=3):
+def _check(name, w, kinds=7):
     print(f"[emu] {name} dtype={w.dtype} shape={w.shape}", flush=True)
     g = _emu(w, kinds=kinds)
     rep = C.compare(w.dtype, H.params_of(w), g, H.run_oracle(w))
@@ -70,6 +70,9 @@ def test_emu_mixed_modes(dtype):
     p = [1.0, 1.0, 1.0, 0.8, 0.5, 0.9, 0.7, 0.95]
     w = H.synthetic(dtype, len(T), V, seed=3, temperature=T, top_k=k, top_p=p, ninf_frac=0.1, dup_max=True)
     _check("mixed", w)
+    # hints that leave kinds out: the same results through the fallback phases
+    for kinds in (3, 2, 1):
+        _check(f"mixed kinds={kinds}", w, kinds=kinds)
 
 
 def test_emu_config_c2():

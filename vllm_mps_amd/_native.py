@@ -12,9 +12,11 @@ from . import build as _build
 
 DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
 ROW_OK, ROW_BAD_PARAM, ROW_INVALID, ROW_UNSUPPORTED, ROW_INTERNAL = 0, 1, 2, 3, 4
-ABI_VERSION = 4
+ABI_VERSION = 5
 KIND_TOPP32 = 1  # MIS_KIND_TOPP32
 KIND_OTHER = 2   # MIS_KIND_OTHER
+KIND_GENERIC = 4  # MIS_KIND_GENERIC
+KIND_ALL = 7     # MIS_KIND_ALL
 
 EXPORTED = ("mis_workspace_bytes", "mis_workspace_init", "mis_sample", "mis_sample_profiled", "mis_sample_ex", "mis_strerror", "mis_last_hip_error",
             "mis_abi_version")

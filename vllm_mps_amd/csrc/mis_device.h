@@ -293,6 +293,35 @@ __device__ __forceinline__ int wave_find_desc(const T *h, int nbins, T target, T
     return bsel;
 }
 
+// Descending search over a count histogram in LDS by the whole block (NTH
+// threads, nbins a multiple of NTH, at most 4 bins per thread): the bin b
+// where the count from the top reaches `target` (which must be at most the
+// total); *above = the count strictly above b.  slot: two LDS words.
+template <int NTH>
+__device__ __forceinline__ int block_find_desc(const uint32_t *h, int nbins, uint32_t target, uint32_t *above, Red &rr,
+                                               uint32_t *slot)
+{
+    const int per = nbins / NTH, t = threadIdx.x;
+    uint32_t v[4] = {0u, 0u, 0u, 0u}, s = 0u;
+    for (int q = 0; q < per && q < 4; ++q) { v[q] = h[nbins - 1 - (t * per + q)]; s += v[q]; }
+    uint32_t tot;
+    const uint32_t ex = block_excl_scan<uint32_t, NTH / 64>(s, rr, &tot);
+    if (t == 0) { slot[0] = 0u; slot[1] = tot; }
+    __syncthreads();
+    if (ex < target && ex + s >= target) {
+        uint32_t run = ex;
+        for (int q = 0; q < per && q < 4; ++q) {
+            if (run + v[q] >= target) { slot[0] = (uint32_t)(nbins - 1 - (t * per + q)); slot[1] = run; break; }
+            run += v[q];
+        }
+    }
+    __syncthreads();
+    const int b = (int)slot[0];
+    *above = slot[1];
+    __syncthreads();
+    return b;
+}
+
 // Ascending search over n <= 64*per values in LDS, run by one whole wave:
 // the first index i whose inclusive prefix sum exceeds `target` (indices with
 // zero value never qualify); *before = sum of the values before i.  When

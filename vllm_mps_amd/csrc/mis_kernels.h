@@ -147,7 +147,7 @@ struct Smem {
 // LDS of the chunk pass: only what its per-mode reductions need (17 KB), so
 // that more of its workgroups fit on a CU
 struct ChunkSmem {
-    float lp[CB_N][NT];        // lane-private coarse bins (fp32 top-p)
+    double wb[NWAVE][CB_N];    // per-wave coarse bins (fp32 top-p)
     double etab[ETAB_N];       // 2^(j/64) for dexp
     Red red;
     uint32_t bu[8];
@@ -313,16 +313,17 @@ __device__ __forceinline__ void pick_chunk(SM &sm, int G, float u, int *g_out, d
 
 // First index (ascending) of an LDS element list at which the running weight
 // exceeds `target`: radix over index space, 256 buckets per level.
-__device__ __forceinline__ int64_t draw_in_list(Smem &sm, const int32_t *idx, const double *e, int n, int64_t V, double target)
+template <int NTH = NT, class SM>
+__device__ __forceinline__ int64_t draw_in_list(SM &sm, const int32_t *idx, const double *e, int n, int64_t V, double target)
 {
     int64_t lo = 0, hi = V;
     double acc = 0.0;
     while (hi - lo > 1) {
         const int64_t width = (hi - lo + 255) / 256;
         __syncthreads();
-        for (int i = threadIdx.x; i < 256; i += NT) sm.sub_m[i] = 0.0;
+        for (int i = threadIdx.x; i < 256; i += NTH) sm.sub_m[i] = 0.0;
         __syncthreads();
-        for (int i = threadIdx.x; i < n; i += NT) {
+        for (int i = threadIdx.x; i < n; i += NTH) {
             const int64_t j = idx[i];
             if (j >= lo && j < hi && e[i] > 0.0) atomicAdd(&sm.sub_m[(j - lo) / width], e[i]);
         }
@@ -1170,8 +1171,7 @@ __device__ __forceinline__ void leader_row(Smem &sm, RowCx &c, const RowPlan &pl
         }
         write_row(ro, a, row, id, id >= 0 ? MIS_ROW_OK : MIS_ROW_INVALID, pl.mode, m, row_key(-INFINITY, DT), -1, SK);
     } else if (pl.mode == M_SMALLK) {
-        const Cand *cand = reinterpret_cast<const Cand *>(a.ws + L.cand) + (size_t)row * L.G * CAND_CAP;
-        if (!leader_smallk<DT>(sm, c, pl, csr, cand, ro, a)) final_generic<DT>(sm, c, pl, ro, a);
+        final_generic<DT>(sm, c, pl, ro, a);  // the rows k_rowpass deferred (or no row pass ran)
     } else if (DT != F32 && pl.mode == M_TOPP) {
         // the cut among the row's K_PROBE largest values first
         double s = 0.0;
@@ -1295,14 +1295,23 @@ __global__ __launch_bounds__(NT) void k_sample(Args a, int part)
     const int tid = threadIdx.x;
     const int G = L.G;
     const uint32_t task = blockIdx.x;  // a row's chunks have consecutive indices
-    const int row = (int)(task / (uint32_t)G), chunk = (int)(task % (uint32_t)G);
+    const int chunk = (int)(task % (uint32_t)G);
+    int row = (int)(task / (uint32_t)G);
+    if (part != K1_ALL) {
+        // the split halves take their rows from the launch order k_rows wrote
+        // (fp32 top-p rows first), so a half's working workgroups lead its grid
+        const int32_t *perm = reinterpret_cast<const int32_t *>(a.ws + L.perm);
+        const int ntp = uni(ldp(&perm[L.B]));
+        const int r = part == K1_TOPP32 ? row : ntp + row;
+        if ((part == K1_TOPP32 && row >= ntp) || r >= (int)L.B) return;
+        row = uni(ldp(&perm[r]));
+    }
     const int64_t V = a.V;
     const int64_t base = (int64_t)chunk * CH;
     const char *rowp = a.logits + (int64_t)row * a.stride_bytes;
     mis_row_params P = a.params[row];
     P.temperature = uni(P.temperature); P.top_k = uni(P.top_k); P.top_p = uni(P.top_p); P.uniform = uni(P.uniform);
     const RowPlan pl = plan_row(P, V);
-    if (part != K1_ALL && (part == K1_TOPP32) != (DT == F32 && pl.mode == M_TOPP)) return;  // the other launch's row
     ChunkSum *csr = reinterpret_cast<ChunkSum *>(a.ws + L.chunks) + (size_t)row * G;
     ChunkSum *cs = csr + chunk;
     RoundBuf *rb = reinterpret_cast<RoundBuf *>(a.ws + L.rbuf) + (size_t)row * G + chunk;
@@ -1385,39 +1394,30 @@ __global__ __launch_bounds__(NT) void k_sample(Args a, int part)
             for (int i = 0; i < EPT; ++i) s += (double)wexp(scale_r<DT>(x[i], T, rT), ymax);
             Sc = block_sum<double>(s, sm.red);
         } else if (live && topp32) {
-            // first refinement level: weights and lane-private coarse bins on the global grid
-            // floor(y / 2); bins more than CB_N below the chunk's are not kept.
-            // Each lane owns one column of the bins, so plain read-modify-write
-            // suffices (LDS float atomics serialise)
-            // S in float64 from dexp (relative error below 1e-15), so the row
-            // pass can decide the cut against exact masses
+            // weights exp(y - ymax) in float64 (dexp: relative error below
+            // 1e-15), their sum and coarse bins floor(4y) on the absolute
+            // grid, the CB_N bins at and below the chunk max's, summed per
+            // wave with LDS float64 atomics: exact enough that the masses
+            // above the row's cut band come from these bins alone
             const float Ac = coarse_bin(ymax);
             exp_table(sm.etab, tid);
-#pragma unroll
-            for (int b = 0; b < CB_N; ++b) sm.lp[b][tid] = 0.0f;
+            for (int b = tid; b < NWAVE * CB_N; b += NT) (&sm.wb[0][0])[b] = 0.0;
             __syncthreads();
             const double ymd = (double)ymax;
             double s = 0.0;
+            double *wb = sm.wb[wave_id()];
             scale_all<DT, EPT>(x, T, rT);  // x now holds y
 #pragma unroll
             for (int i = 0; i < EPT; ++i) {
                 const float y = x[i];
                 const double e = dexp((double)y - ymd, sm.etab);
                 s += e;
-                const float cb = Ac - coarse_bin(y);
-                if (cb < (float)CB_N) { const int cbi = (int)cb; sm.lp[cbi][tid] += (float)e; }  // lane-private: no atomic
+                const float cb = Ac - coarse_bin(y);  // +inf for y = -inf
+                if (cb < (float)CB_N) atomicAdd(&wb[(int)cb], e);
             }
             Sc = block_sum<double>(s, sm.red);  // its barriers also order the bins
-            {
-                const int b = tid >> 4, q = tid & 15;
-                double t = 0.0;
-#pragma unroll
-                for (int l = 0; l < 16; ++l) t += (double)sm.lp[b][q * 16 + l];
-#pragma unroll
-                for (int o = 8; o > 0; o >>= 1) t += __shfl_xor(t, o, 64);
-                if (q == 0) rb->coarse[b] = t;
-            }
-            if (tid == 0) rb->S = Sc;
+            if (tid < CB_N) rb->coarse[tid] = sm.wb[0][tid] + sm.wb[1][tid] + sm.wb[2][tid] + sm.wb[3][tid];
+            if (tid == 0) { rb->S = Sc; rb->top = Ac; }
         } else if (live && (pl.mode == M_SMALLK || topp16)) {
             // (one else-if chain: separate branches here cost the fp32 kernel
             // 70 more VGPRs, half its occupancy)
@@ -1499,42 +1499,44 @@ __global__ __launch_bounds__(NT) void k_sample(Args a, int part)
 
 // ------------------------------------------------------------------ the row pass
 
-// ------------------------------------------------------------------ fp32 top-p rows
+// ------------------------------------------------------------------ greedy, temperature, small top-k rows (k_rowpass)
 //
-// Five launches spread an fp32 top-p row over the whole GPU (the chunk pass's
-// float64 S and coarse bins come first):
-//   k_tp_prep    one workgroup per row: row max, S, A = top_p * S, the coarse
-//                band of keys whose cumulative mass can reach A (margin 1e-5 S
-//                over the float32 bin sums) and its raw-value interval;
-//   k_tp_hist    one workgroup per (row, chunk), grid-stride: re-reads the
-//                chunk (Infinity Cache); elements above the band add their
-//                float64 weight (dexp) to the chunk's above-mass, band
-//                elements go to FH linear fine bins (count, weight in 2^-40
-//                units of the row max's weight);
-//   k_tp_merge   one workgroup per row: merges the fine bins and finds the
-//                bins whose cumulative mass can hold the cut (exact to the
-//                fixed-point bound): the final band;
-//   k_tp_collect one workgroup per (row, chunk), grid-stride: the chunk's
-//                kept mass above the final band, and the band's elements
-//                appended to the row's survivor list;
-//   k_tp_final   one workgroup per row: the survivors' float64 weights, their
-//                sorted cut (window_resolve) with its decision margin checked
-//                against the error bound, then the draw.
-// A row where a step does not apply is left to the row pass's generic path
-// (RowOut status ROW_DEFER).
+// One workgroup of NTS threads per row, from the chunk summaries:
+//   greedy       the argmax merge;
+//   temperature  the chunk holding u * S, then that chunk re-read;
+//   bad rows     their status;
+//   small top-k  (0 < k' <= K_SMALL)
+//     1. the candidate counts and prefix;
+//     2. the candidates gathered into LDS, one wave per chunk;
+//     3. the k'-th largest raw value by a three-level radix select over the
+//        candidates' keys (11 / 11 / 10 bits, LDS histograms);
+//     4. the survivors: scaled value >= scale(k'-th value), every tie kept,
+//        with float64 weights exp(y - m) (dexp);
+//     5. top-p over the survivors in the stable descending order: exact
+//        masses (fp32) or torch's 16-bit rounding chain;
+//     6. the inverse-CDF draw over the kept survivors in vocabulary order.
+// A small-k row it cannot finish here (a chunk's candidates overflowed or
+// were truncated above the threshold, more candidates than the LDS cache,
+// more survivors than SURV_CAP) gets RowOut status ROW_DEFER; k_final's
+// generic path then re-reads it.
 
+constexpr int NTS = 1024;           // threads of k_rowpass (16 waves)
 constexpr int ROW_DEFER = 16;       // RowOut status: k_final's generic path finishes the row
 
-// LDS of the top-p per-row kernels: only what their steps use (the row
-// pass's Smem also caches small-k candidates)
-struct TopRowSmem {
+struct SmallkSmem {
+    Cand cc[CCAP];                  // the row's candidates
     union {
         struct { uint32_t key[SURV_CAP]; int32_t idx[SURV_CAP]; double e[SURV_CAP]; } s;
         struct { uint64_t k[SURV_CAP]; double e[SURV_CAP]; } so;
     } u;
-    union { double coarse[CB_N]; } v;
-    double cw[G_MAX];
-    double chs[G_MAX];
+    struct { uint32_t key[SURV_CAP]; int32_t idx[SURV_CAP]; double e[SURV_CAP]; } sv;  // the survivors
+    uint32_t h[2048];               // radix-select histogram; fp32 top-p: bin counts
+    double hm[1024];                // fp32 top-p: bin masses
+    uint32_t rkey[SURV_CAP], rcnt[SURV_CAP];  // 16-bit chain: runs (first sorted position, length)
+    float rp[SURV_CAP];             //                         and their dtype probabilities
+    uint32_t pre[G_MAX + 1];        // candidate prefix per chunk
+    double sub_m[256];              // the draw's index-radix buckets
+    double cw[G_MAX], chs[G_MAX];   // temperature rows: per-chunk weight and rescale
     double etab[ETAB_N];
     Red red;
     uint32_t bu[8];
@@ -1542,7 +1544,341 @@ struct TopRowSmem {
     double bd[8];
     unsigned long long bq[2];
 };
-constexpr int TP_GRID = 2048;       // workgroups of the grid-stride passes
+
+template <int DT>
+__global__ __launch_bounds__(NTS) void k_rowpass(Args a)
+{
+    __shared__ SmallkSmem sm;
+    constexpr int NW = NTS / 64;
+    const Layout &L = a.L;
+    const int row = blockIdx.x, tid = threadIdx.x, G = L.G;
+    mis_row_params P = a.params[row];
+    P.temperature = uni(P.temperature); P.top_k = uni(P.top_k); P.top_p = uni(P.top_p); P.uniform = uni(P.uniform);
+    const RowPlan pl = plan_row(P, a.V);
+    RowOut *ro = reinterpret_cast<RowOut *>(a.ws + L.rowout) + row;
+    if (pl.mode == M_BAD || pl.mode == M_INVAL) {
+        write_row(ro, a, row, -1, pl.mode == M_BAD ? MIS_ROW_BAD_PARAM : MIS_ROW_INVALID, pl.mode, 0.0f, 0u, 0, 0.0);
+        return;
+    }
+    if (pl.mode != M_SMALLK && pl.mode != M_GREEDY && pl.mode != M_TEMP) return;
+    const ChunkSum *cs = reinterpret_cast<const ChunkSum *>(a.ws + L.chunks) + (size_t)row * G;
+    static_assert(G_MAX <= NTS, "one chunk per thread");
+    if (pl.mode == M_GREEDY) {
+        // argmax merge: key descending, index ascending
+        uint32_t k2 = 0u;
+        int32_t i2 = IDX_ALL;
+        if (tid < G) { k2 = ldp(&cs[tid].xkey); i2 = ldp(&cs[tid].xarg); }
+        wave_argmax(k2, i2);
+        if (lane_id() == 0) { sm.red.u[wave_id()] = k2; sm.red.l[wave_id()] = i2; }
+        __syncthreads();
+        if (tid == 0) {
+            for (int w = 1; w < NW; ++w) {
+                const uint32_t kk = sm.red.u[w];
+                const int32_t ii = (int32_t)sm.red.l[w];
+                if (kk > k2 || (kk == k2 && ii < i2)) { k2 = kk; i2 = ii; }
+            }
+            write_row(ro, a, row, i2, MIS_ROW_OK, pl.mode, 0.0f, 0u, i2, 1.0);
+        }
+        return;
+    }
+    if (pl.mode == M_TEMP) {
+        // chunk weights are exp(y - ymax_c): rescale to the row max m, pick
+        // the chunk holding u * S, re-read it for the index
+        uint32_t flg = 0u;
+        float yg = -INFINITY;
+        double Sg = 0.0;
+        if (tid < G) { flg = ldp(&cs[tid].flags) != 0u ? 1u : 0u; yg = ldp(&cs[tid].ymax); Sg = ldp(&cs[tid].S); }
+        const float m = block_max<float, NW>(yg, sm.red);
+        flg = block_sum<uint32_t, NW>(flg, sm.red);
+        if (flg != 0u || m == -INFINITY) {
+            write_row(ro, a, row, -1, MIS_ROW_INVALID, pl.mode, m, 0u, 0, 0.0);
+            return;
+        }
+        if (tid < G) {
+            const double ch = yg == -INFINITY ? 0.0 : exp((double)yg - (double)m);
+            sm.chs[tid] = ch;
+            sm.cw[tid] = Sg * ch;
+        }
+        int gsel;
+        double resid, SK;
+        pick_chunk(sm, G, pl.u, &gsel, &resid, &SK);  // (its barriers publish cw)
+        int64_t id = -1;
+        if (gsel >= 0) {
+            RowCx c;
+            c.rowp = a.logits + (int64_t)row * a.stride_bytes;
+            c.V = a.V; c.vec_ok = a.vec_ok; c.G = G; c.CH = (int64_t)NT * L.ept; c.row = row; c.T = pl.T; c.m = m;
+            const float yc = ldp(&cs[gsel].ymax), T = pl.T;
+            // the chunk pass's weights, recomputed the same way
+            id = draw_in_chunk<DT, NTS>(sm, c, gsel, resid / sm.chs[gsel], [&](float xv, int64_t) -> double {
+                return (double)wexp(scale_y<DT>(xv, T), yc);
+            });
+        }
+        write_row(ro, a, row, id, id >= 0 ? MIS_ROW_OK : MIS_ROW_INVALID, pl.mode, m, row_key(-INFINITY, DT), -1, SK);
+        return;
+    }
+    const Cand *cand = reinterpret_cast<const Cand *>(a.ws + L.cand) + (size_t)row * G * CAND_CAP;
+    trace(a.ws, L, row, 17);
+    exp_table(sm.etab, tid);
+    // 1. summaries
+    uint32_t nc = 0u, ovf = 0u, ntr = 0u, nfin = 0u, flg = 0u;
+    float ymx = -INFINITY;
+    if (tid < G) {
+        const uint32_t n = ldp(&cs[tid].ncand);
+        ovf = n == NCAND_OVERFLOW ? 1u : 0u;
+        nc = n <= (uint32_t)CAND_CAP ? n : 0u;
+        ntr = ldp(&cs[tid].trunc) != 0u ? 1u : 0u;
+        nfin = ldp(&cs[tid].nfin);
+        flg = ldp(&cs[tid].flags) != 0u ? 1u : 0u;
+        ymx = ldp(&cs[tid].ymax);
+    }
+    uint32_t ntot;
+    const uint32_t off = block_excl_scan<uint32_t, NW>(nc, sm.red, &ntot);
+    if (tid < G) sm.pre[tid] = off;
+    const float m = block_max<float, NW>(ymx, sm.red);
+    ovf = block_sum<uint32_t, NW>(ovf, sm.red);
+    ntr = block_sum<uint32_t, NW>(ntr, sm.red);
+    nfin = block_sum<uint32_t, NW>(nfin, sm.red);
+    flg = block_sum<uint32_t, NW>(flg, sm.red);  // (its barriers publish pre)
+    if (flg != 0u || m == -INFINITY) {  // NaN / +inf scaled logits, or nothing finite
+        write_row(ro, a, row, -1, MIS_ROW_INVALID, pl.mode, m, 0u, 0, 0.0);
+        return;
+    }
+    const double md = (double)m;
+    // fewer finite elements than k': the k'-th value is -inf and every finite
+    // element survives, which the candidates hold only if no chunk truncated
+    const bool all_fin = nfin <= (uint32_t)pl.kk;
+    if (ovf != 0u || ntot > (uint32_t)CCAP || (all_fin && ntr != 0u) || (!all_fin && ntot < (uint32_t)pl.kk)) {
+        if (tid == 0) ro->status = ROW_DEFER;
+        return;
+    }
+    // 2. candidates into LDS, one wave per chunk, eight loads in flight
+    for (int g = wave_id(); g < G; g += NW) {
+        const uint32_t n = g + 1 < G ? sm.pre[g + 1] - sm.pre[g] : ntot - sm.pre[g];
+        const Cand *cg = cand + (size_t)g * CAND_CAP;
+        Cand *dst = sm.cc + sm.pre[g];
+        for (uint32_t i0 = 0; i0 < n; i0 += 8 * 64) {
+            Cand v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const uint32_t i = i0 + (uint32_t)(u * 64 + lane_id());
+                v[u] = i < n ? ldp_cand(&cg[i]) : Cand{0.0f, 0};
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const uint32_t i = i0 + (uint32_t)(u * 64 + lane_id());
+                if (i < n) dst[i] = v[u];
+            }
+        }
+    }
+    __syncthreads();
+    trace(a.ws, L, row, 21);
+    // 3. k'-th largest raw key: three radix levels over the candidates
+    uint32_t xk = 0u;
+    if (!all_fin) {
+        uint32_t prefix = 0u, rem = (uint32_t)pl.kk;
+        const int sh[3] = {21, 10, 0};
+        const int nb[3] = {2048, 2048, 1024};
+#pragma unroll
+        for (int lev = 0; lev < 3; ++lev) {
+            const uint32_t hmask = lev == 0 ? 0u : ~((1u << (sh[lev] + (lev == 2 ? 10 : 11))) - 1u);
+            for (int i = tid; i < 2048; i += NTS) sm.h[i] = 0u;
+            __syncthreads();
+            for (uint32_t f = tid; f < ntot; f += NTS) {
+                const uint32_t k = key_of_f32(sm.cc[f].x);
+                if ((k & hmask) == (prefix & hmask)) atomicAdd(&sm.h[(k >> sh[lev]) & (uint32_t)(nb[lev] - 1)], 1u);
+            }
+            __syncthreads();
+            uint32_t above;
+            const int d = block_find_desc<NTS>(sm.h, nb[lev], rem, &above, sm.red, &sm.bu[0]);
+            rem -= above;
+            prefix |= (uint32_t)d << sh[lev];
+        }
+        xk = prefix;
+    }
+    trace(a.ws, L, row, 18);
+    // 4. survivors: scaled value >= scale(k'-th raw value); the ties the
+    // scaling creates are kept, as the reference keeps them
+    const uint32_t thr_key = xk ? row_key(scale_y<DT>(f32_of_key(xk), pl.T), DT) : 0u;
+    if (ntr != 0u) {
+        // a truncated chunk left out only elements with scaled keys below its
+        // kc; they cannot reach the threshold if kc <= thr_key
+        uint32_t hide = 0u;
+        if (tid < G) hide = (ldp(&cs[tid].trunc) != 0u && ldp(&cs[tid].kc) > thr_key) ? 1u : 0u;
+        hide = block_sum<uint32_t, NW>(hide, sm.red);
+        if (hide != 0u) {
+            if (tid == 0) ro->status = ROW_DEFER;
+            return;
+        }
+    }
+    if (tid == 0) sm.bu[3] = 0u;
+    __syncthreads();
+    const float T = pl.T, rT = 1.0f / pl.T;
+    for (uint32_t f0 = 0; f0 < ntot; f0 += NTS) {
+        const uint32_t f = f0 + tid;
+        float y = 0.0f;
+        uint32_t k = 0u;
+        bool in = false;
+        if (f < ntot) {
+            y = scale_r<DT>(sm.cc[f].x, T, rT);
+            k = row_key(y, DT);
+            in = y != -INFINITY && k >= thr_key;
+        }
+        const uint32_t p = wave_append(in, &sm.bu[3]);
+        if (in && p < (uint32_t)SURV_CAP) {
+            sm.sv.key[p] = k;
+            sm.sv.idx[p] = sm.cc[f].idx;
+            sm.sv.e[p] = dexp((double)y - md, sm.etab);
+        }
+    }
+    __syncthreads();
+    const uint32_t ns = sm.bu[3];
+    trace(a.ws, L, row, 19);
+    if (ns > (uint32_t)SURV_CAP || ns == 0u) {
+        if (tid == 0) ro->status = ROW_DEFER;
+        return;
+    }
+    // 5. top-p over the survivors
+    uint32_t cut_key = thr_key;
+    int32_t cut_i = IDX_ALL;
+    if (pl.topp) {
+        double S = 0.0;
+        for (uint32_t i = tid; i < ns; i += NTS) S += sm.sv.e[i];
+        S = block_sum<double, NW>(S, sm.red);
+        const double A = (double)pl.top_p * S;
+        constexpr int PT = SURV_CAP / NTS;
+        static_assert(PT == 1, "one survivor per thread");
+        const int i = tid;
+        if (DT == F32) {
+            // exact masses: 1024 linear bins over the survivors' values locate
+            // the bin(s) whose cumulative mass (descending) can reach A; only
+            // their elements are sorted for the cut
+            const bool have = i < (int)ns;
+            const float yv = have ? f32_of_key(sm.sv.key[i]) : 0.0f;
+            const float ylo = block_min<float, NW>(have ? yv : INFINITY, sm.red);
+            const float yhi = block_max<float, NW>(have ? yv : -INFINITY, sm.red);
+            const float inv = yhi > ylo ? 1023.0f / (yhi - ylo) : 0.0f;
+            sm.h[i] = 0u;
+            sm.hm[i] = 0.0;
+            __syncthreads();
+            int bin = 0;
+            if (have) {
+                bin = (int)fminf(fmaxf((yv - ylo) * inv, 0.0f), 1023.0f);
+                atomicAdd(&sm.h[bin], 1u);
+                atomicAdd(&sm.hm[bin], sm.sv.e[i]);
+            }
+            __syncthreads();
+            // bins in descending order: thread t holds bin 1023 - t
+            const double v = sm.hm[1023 - i];
+            double tot;
+            const double ex = block_excl_scan<double, NW>(v, sm.red, &tot);
+            const double delta = 1e-12 * S;
+            const bool inb = sm.h[1023 - i] > 0u && ex + v >= A - delta && ex <= A + delta;
+            if (tid == 0) { sm.bi[0] = 1 << 20; sm.bi[1] = -1; }
+            __syncthreads();
+            if (inb) { atomicMin(&sm.bi[0], i); atomicMax(&sm.bi[1], i); }  // descending positions
+            __syncthreads();
+            const int pa = sm.bi[0], pb = sm.bi[1];
+            if (inb && i == pa) sm.bd[0] = ex;
+            if (tid == 0) sm.bu[4] = 0u;
+            __syncthreads();
+            bool ok = pa <= pb;
+            if (ok) {
+                const double above = sm.bd[0];
+                // the window: survivors in bins [1023 - pb, 1023 - pa]
+                const int blo = 1023 - pb, bhi = 1023 - pa;
+                const bool w = have && bin >= blo && bin <= bhi;
+                const uint32_t q = wave_append(w, &sm.bu[4]);
+                if (w) { sm.u.s.key[q] = sm.sv.key[i]; sm.u.s.idx[q] = sm.sv.idx[i]; sm.u.s.e[q] = sm.sv.e[i]; }
+                __syncthreads();
+                const uint32_t nw = sm.bu[4];
+                double ql, wl;
+                const int rl = window_resolve<NTS>(sm, nw, above, A, &cut_key, &cut_i, &ql, &wl);
+                ok = rl >= 0;
+            }
+            if (!ok) {  // the cut not inside the window (sums within rounding of A)
+                if (tid == 0) ro->status = ROW_DEFER;
+                return;
+            }
+        } else {
+            // 16-bit rounding chain in the stable descending order: sort, runs
+            // of equal keys with their probabilities in parallel, then one
+            // thread walks the chain over the runs
+            const uint64_t kt = i < (int)ns ? (((uint64_t)sm.sv.key[i] << 32) | (uint64_t)(0xffffffffu - (uint32_t)sm.sv.idx[i])) : 0ull;
+            const double et = i < (int)ns ? sm.sv.e[i] : 0.0;
+            sm.u.so.k[i] = kt;
+            sm.u.so.e[i] = et;
+            __syncthreads();
+            block_sort_desc<NTS, SURV_CAP>(sm.u.so.k, sm.u.so.e, (int)ns);
+            const uint32_t st = i < (int)ns && (i == 0 || (uint32_t)(sm.u.so.k[i] >> 32) != (uint32_t)(sm.u.so.k[i - 1] >> 32)) ? 1u : 0u;
+            uint32_t nr;
+            const uint32_t r = block_excl_scan<uint32_t, NW>(st, sm.red, &nr);
+            if (st) {
+                sm.rkey[r] = (uint32_t)i;  // the run's first sorted position
+                sm.rp[r] = rn_dtype((float)(sm.u.so.e[i] / S), DT);
+            }
+            __syncthreads();
+            if ((uint32_t)i < nr) sm.rcnt[i] = ((uint32_t)i + 1 < nr ? sm.rkey[i + 1] : ns) - sm.rkey[i];
+            __syncthreads();
+            if (tid == 0) {
+                const float thr16 = rn_dtype(pl.top_p, DT);
+                float F = 0.0f;
+                int run_at = -1;
+                uint32_t tk = 0;
+                const bool found = chain_walk(sm.rcnt, sm.rp, (int)nr, F, thr16, DT, &run_at, &tk);
+                const uint32_t r0 = found ? sm.rkey[run_at] + tk : ns;  // kept: sorted positions < r0
+                sm.bu[0] = r0;
+                if (r0 > 0) {
+                    const uint64_t q = sm.u.so.k[r0 - 1];
+                    sm.bu[1] = (uint32_t)(q >> 32);
+                    sm.bi[0] = (int32_t)(0xffffffffu - (uint32_t)q);
+                }
+            }
+            __syncthreads();
+            if (sm.bu[0] == 0u) {  // nothing kept: not a distribution
+                write_row(ro, a, row, -1, MIS_ROW_INVALID, pl.mode, m, 0u, 0, 0.0);
+                return;
+            }
+            cut_key = sm.bu[1];
+            cut_i = sm.bi[0];
+            __syncthreads();
+        }
+    }
+    trace(a.ws, L, row, 20);
+    // 6. the draw over the kept survivors in vocabulary order
+    double SK = 0.0;
+    for (uint32_t i = tid; i < ns; i += NTS) {
+        if (!kept_by_cut(sm.sv.key[i], sm.sv.idx[i], cut_key, cut_i)) sm.sv.e[i] = 0.0;
+        SK += sm.sv.e[i];
+    }
+    SK = block_sum<double, NW>(SK, sm.red);
+    const int64_t id = draw_in_list<NTS>(sm, sm.sv.idx, sm.sv.e, (int)ns, a.V, (double)pl.u * SK);
+    write_row(ro, a, row, id, id >= 0 ? MIS_ROW_OK : MIS_ROW_INVALID, pl.mode, m, cut_key, cut_i, SK);
+    trace(a.ws, L, row, 22);
+}
+
+// ------------------------------------------------------------------ fp32 top-p rows
+//
+// Two launches after the chunk pass spread an fp32 top-p row over the GPU:
+//   k_tp_hist   one workgroup per (row, chunk).  Every workgroup of a row
+//               merges the row's coarse bins from the chunk pass (float64,
+//               exact to rounding) into the row max, S, A = top_p * S and the
+//               coarse band whose cumulative mass can reach A; the mass above
+//               the band follows from the bins.  It then re-reads its chunk
+//               (Infinity Cache) and puts the band's elements into FH linear
+//               fine bins (count, float64 mass) and a stash (raw value,
+//               index): all of them when they fit, otherwise those in a
+//               window of fine bins around the cut as the chunk itself
+//               estimates it (a chunk is a random sample of its row).
+//   k_tp_final  one workgroup per row: merges the fine bins into the final
+//               band (the bins whose cumulative mass can hold the cut), takes
+//               that band's elements from the stashes (checking that every
+//               chunk's window covers it), sorts them into the exact cut with
+//               its decision margin checked against the error bound, then
+//               draws.
+// A row where a step does not apply is left to the row pass's generic path
+// (RowOut status ROW_DEFER).
+
+static_assert(NWAVE == 4, "four waves per chunk-pass workgroup");
 
 __device__ __forceinline__ TopRow *top_row(const Args &a, int row)
 {
@@ -1552,71 +1888,168 @@ __device__ __forceinline__ TopChunk *top_chunk(const Args &a, int row, int g)
 {
     return reinterpret_cast<TopChunk *>(a.ws + a.L.topc) + (size_t)row * a.L.G + g;
 }
+__device__ __forceinline__ Cand *top_stash(const Args &a, int row, int g)
+{
+    return reinterpret_cast<Cand *>(a.ws + a.L.stash) + ((size_t)row * a.L.G + g) * STASH_CAP;
+}
 __device__ __forceinline__ int fine_bin(float y, float lo, float scf)
 {
     return (int)fminf(fmaxf(floorf((y - lo) * scf), 0.0f), (float)(FH - 1));
 }
 
-__global__ __launch_bounds__(NT) void k_tp_prep(Args a)
+// The launch order of an fp32 batch split between the top-p passes and the
+// rest: perm[0, n) = the fp32 top-p rows in row order, perm[n, B) = the
+// others, perm[B] = n.  One workgroup at the start of the step.
+__global__ __launch_bounds__(NT) void k_rows(Args a)
 {
-    __shared__ TopRowSmem sm;
+    __shared__ Red red;
+    int32_t *perm = reinterpret_cast<int32_t *>(a.ws + a.L.perm);
+    const int tid = threadIdx.x, B = (int)a.L.B;
+    uint32_t ntp = 0u;
+    for (int r0 = 0; r0 < B; r0 += NT) {  // top-p rows: their rank in row order
+        const int row = r0 + tid;
+        const bool t = row < B && plan_row(a.params[row], a.V).mode == M_TOPP;
+        uint32_t tot;
+        const uint32_t ex = block_excl_scan<uint32_t>(t ? 1u : 0u, red, &tot);
+        if (t) perm[ntp + ex] = row;
+        ntp += tot;
+    }
+    uint32_t nother = 0u;
+    for (int r0 = 0; r0 < B; r0 += NT) {  // the others after them
+        const int row = r0 + tid;
+        const bool o = row < B && plan_row(a.params[row], a.V).mode != M_TOPP;
+        uint32_t tot;
+        const uint32_t ex = block_excl_scan<uint32_t>(o ? 1u : 0u, red, &tot);
+        if (o) perm[ntp + nother + ex] = row;
+        nother += tot;
+    }
+    if (tid == 0) perm[B] = (int32_t)ntp;
+}
+
+// LDS of k_tp_hist
+constexpr int LCAP = 4096;          // band elements of a chunk binned from a dense LDS list
+struct HistSmem {
+    double mc[CB_N];                // the row's merged coarse bins (relative to the row max)
+    double chs[G_MAX];              // per chunk: exp(ymax_g - m)
+    float off[G_MAX];               // per chunk: row top bin - chunk top bin
+    uint32_t cnt[FH];
+    double mass[FH];
+    float lx[LCAP];                 // the chunk's band elements (raw values)
+    double etab[ETAB_N];
+    Red red;
+    uint32_t bu[8];
+    int32_t bi[8];
+    double bd[8];
+    float bf[8];
+};
+
+template <int EPT>
+__global__ __launch_bounds__(NT) void k_tp_hist(Args a)
+{
+    __shared__ HistSmem sm;
+    constexpr int VEC = Traits<F32>::VEC;
     const Layout &L = a.L;
-    const int row = blockIdx.x, tid = threadIdx.x;
-    const RowPlan pl = plan_row(a.params[row], a.V);
+    const int tid = threadIdx.x, G = L.G;
+    // workgroup i serves chunk i % G of the (i / G)-th fp32 top-p row (k_rows)
+    const int g = (int)(blockIdx.x % (unsigned)G);
+    const int32_t *perm = reinterpret_cast<const int32_t *>(a.ws + L.perm);
+    const int rk = (int)(blockIdx.x / (unsigned)G);
+    if (rk >= uni(ldp(&perm[L.B]))) return;
+    const int row = uni(ldp(&perm[rk]));
+    mis_row_params P = a.params[row];
+    P.temperature = uni(P.temperature); P.top_k = uni(P.top_k); P.top_p = uni(P.top_p); P.uniform = uni(P.uniform);
+    const RowPlan pl = plan_row(P, a.V);
+    if (pl.mode != M_TOPP) return;
     TopRow *tr = top_row(a, row);
-    if (pl.mode != M_TOPP) { if (tid == 0) tr->status = TR_NONE; return; }  // the later passes read only this
-    const ChunkSum *csr = reinterpret_cast<const ChunkSum *>(a.ws + L.chunks) + (size_t)row * L.G;
-    const RoundBuf *rbf = reinterpret_cast<const RoundBuf *>(a.ws + L.rbuf) + (size_t)row * L.G;
-    const int G = L.G;
-    trace(a.ws, L, row, 2);
-    // this thread's chunk (G <= NT): its S and coarse bins are loaded beside
-    // the chunk maxima row_scales reads, one round trip instead of three
+    const bool tr0 = g == 0;
+    if (tr0) trace(a.ws, L, row, 2);
+    // the chunk's loads first: they overlap the summary loads below
+    float x[EPT];
+    const int64_t base = (int64_t)g * NT * EPT;
+    load_chunk<F32, EPT>(a.logits + (int64_t)row * a.stride_bytes, base, a.V, a.vec_ok, x);
+    exp_table(sm.etab, tid);
+    const ChunkSum *csr = reinterpret_cast<const ChunkSum *>(a.ws + L.chunks) + (size_t)row * G;
+    const RoundBuf *rbf = reinterpret_cast<const RoundBuf *>(a.ws + L.rbuf) + (size_t)row * G;
     static_assert(G_MAX <= NT, "one chunk per thread");
     const bool hasg = tid < G;
-    const double Sg = hasg ? ldp(&rbf[tid].S) : 0.0;
-    const float ygt = hasg ? ldp(&csr[tid].ymax) : -INFINITY;
-    double cbv[CB_N];
-#pragma unroll
-    for (int lb = 0; lb < CB_N; ++lb) cbv[lb] = hasg ? ldp(&rbf[tid].coarse[lb]) : 0.0;
-    uint32_t bad;
-    const float m = row_scales(sm, csr, G, &bad);
-    trace(a.ws, L, row, 3);
-    if (bad != 0u || m == -INFINITY) { if (tid == 0) tr->status = TR_DEFER; return; }
+    uint32_t flag = 0u;
+    float yg = -INFINITY, topg = 0.0f;
+    double Sg = 0.0;
+    if (hasg) { flag = ldp(&csr[tid].flags); yg = ldp(&csr[tid].ymax); topg = ldp(&rbf[tid].top); Sg = ldp(&rbf[tid].S); }
+    const float m = block_max<float>(yg, sm.red);
+    const uint32_t bad = block_sum<uint32_t>(flag ? 1u : 0u, sm.red);
+    const float Ar = coarse_bin(m);
+    // bins on the absolute grid floor(4y) stay exact small integers only while
+    // |4y| < 2^23; beyond that (and for NaN / inf rows) the generic path serves
+    if (bad != 0u || m == -INFINITY || !(fabsf(m) * CB_SCALE < 0x1p22f)) {
+        if (g == 0 && tid == 0) tr->status = TR_DEFER;
+        return;
+    }
+    const double md = (double)m;
+    if (hasg) {
+        sm.chs[tid] = yg == -INFINITY ? 0.0 : exp((double)yg - md);
+        sm.off[tid] = yg == -INFINITY ? (float)CB_N : Ar - topg;
+    }
+    for (int b = tid; b < CB_N; b += NT) sm.mc[b] = 0.0;
+    __syncthreads();
     const double S = block_sum<double>(hasg ? Sg * sm.chs[tid] : 0.0, sm.red);
     const double A = (double)pl.top_p * S;
-    const float Ar = coarse_bin(m);
-    if (tid < CB_N) sm.v.coarse[tid] = 0.0;
-    __syncthreads();
-    if (hasg && ygt != -INFINITY) {
-        const int off = (int)(Ar - coarse_bin(ygt));
-        const double sc = sm.chs[tid];
+    if (tr0) trace(a.ws, L, row, 3);
+    // merged coarse bins: chunk g's bin b is the row's bin b + off[g]; eight
+    // loads in flight per thread
+    for (int q0 = 0; q0 < G * CB_N; q0 += 8 * NT) {
+        double v[8];
 #pragma unroll
-        for (int lb = 0; lb < CB_N; ++lb)
-            if (lb + off < CB_N) atomicAdd(&sm.v.coarse[lb + off], cbv[lb] * sc);
+        for (int u = 0; u < 8; ++u) {
+            const int q = q0 + u * NT + tid;
+            v[u] = q < G * CB_N ? ldp(&rbf[q / CB_N].coarse[q % CB_N]) : 0.0;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int q = q0 + u * NT + tid, gq = q / CB_N;
+            if (q < G * CB_N && v[u] != 0.0) {
+                const float mb = (float)(q % CB_N) + sm.off[gq];
+                if (mb < (float)CB_N) atomicAdd(&sm.mc[(int)mb], v[u] * sm.chs[gq]);
+            }
+        }
     }
     __syncthreads();
-    if (tid == 0) {
-        const double delta = 1e-5 * S;
-        double cum = 0.0;
+    if (tr0) trace(a.ws, L, row, 4);
+    if (wave_id() == 0) {
+        // the band: bins whose cumulative mass (descending) can reach A within
+        // the float64 rounding of the sums; lane l holds bins 2l and 2l + 1
+        static_assert(CB_N == 128, "two coarse bins per lane");
+        const double delta = 1e-12 * S;
+        const int l = lane_id();
+        const double v0 = sm.mc[2 * l], v1 = sm.mc[2 * l + 1];
+        const double inc = wave_incl_scan(v0 + v1), exc = inc - v0 - v1;
+        const uint64_t m0 = __ballot(exc + v0 >= A - delta && exc <= A + delta);
+        const uint64_t m1 = __ballot(inc >= A - delta && exc + v0 <= A + delta);
         int ba = -1, bb = -1;
-        for (int b = 0; b < CB_N; ++b) {
-            const double nx = cum + sm.v.coarse[b];
-            if (nx >= A - delta && cum <= A + delta) { if (ba < 0) ba = b; bb = b; }
-            cum = nx;
+        if ((m0 | m1) != 0ull) {
+            const int f0 = m0 ? 2 * __builtin_ctzll(m0) : 1 << 20, f1 = m1 ? 2 * __builtin_ctzll(m1) + 1 : 1 << 20;
+            const int h0 = m0 ? 2 * (63 - __builtin_clzll(m0)) : -1, h1 = m1 ? 2 * (63 - __builtin_clzll(m1)) + 1 : -1;
+            ba = f0 < f1 ? f0 : f1;
+            bb = h0 > h1 ? h0 : h1;
         }
-        sm.bi[0] = ba; sm.bi[1] = bb;
+        const int la = ba >= 0 ? ba >> 1 : 0;
+        const double abv = __shfl(exc, la, 64) + ((ba & 1) ? __shfl(v0, la, 64) : 0.0);
+        if (l == 0) { sm.bi[0] = ba; sm.bi[1] = bb; sm.bd[0] = abv; }
     }
     __syncthreads();
     const int ba = sm.bi[0], bb = sm.bi[1];
-    if (ba < 0) { if (tid == 0) tr->status = TR_DEFER; return; }  // the cut lies below the coarse range
+    if (ba < 0) {  // the cut lies below the coarse range
+        if (g == 0 && tid == 0) tr->status = TR_DEFER;
+        return;
+    }
     const float cb_lo = Ar - (float)bb, cb_hi = Ar - (float)ba;
     if (wave_id() == 0) {
-        // floor(y / 2) >= c <=> y >= 2c: the band's keys in closed form,
-        // checked at both edges (a key search where the check fails)
+        // floor(4y) >= c <=> y >= c/4: the band's keys in closed form, checked
+        // at both edges (a key search where the check fails)
         const uint32_t kfin = row_key(-INFINITY, F32) + 1u, ktop = 0xff7fffffu;  // finite keys
         auto ge_lo = [&](uint32_t k) { return coarse_bin(f32_of_key(k)) >= cb_lo; };
         auto gt_hi = [&](uint32_t k) { return coarse_bin(f32_of_key(k)) > cb_hi; };
-        uint32_t k0 = key_of_f32(2.0f * cb_lo), k1 = key_of_f32(2.0f * (cb_hi + 1.0f)) - 1u;
+        uint32_t k0 = key_of_f32(cb_lo / CB_SCALE), k1 = key_of_f32((cb_hi + 1.0f) / CB_SCALE) - 1u;
         const bool ok0 = k0 >= kfin && k0 <= ktop && ge_lo(k0) && (k0 == kfin || !ge_lo(k0 - 1u));
         const bool ok1 = k1 >= kfin && k1 <= ktop && !gt_hi(k1) && (k1 == ktop || gt_hi(k1 + 1u));
         if (!ok0) k0 = key_search(kfin, ktop, ge_lo);
@@ -1624,250 +2057,340 @@ __global__ __launch_bounds__(NT) void k_tp_prep(Args a)
         if (lane_id() == 0) { sm.bu[5] = k0; sm.bu[6] = k1; }
     }
     __syncthreads();
-    trace(a.ws, L, row, 4);
     const uint32_t klo = sm.bu[5], khi = sm.bu[6];
     uint32_t xlo, xhi;
     x_interval<F32>(sm, klo, khi, pl.T, &xlo, &xhi);
-    trace(a.ws, L, row, 5);
-    if (tid == 0) {
-        const float lo = f32_of_key(klo), hi = f32_of_key(khi);
+    const float lo = f32_of_key(klo), hi = f32_of_key(khi);
+    const float scf = hi > lo ? (float)FH / (hi - lo) : 0.0f;
+    const float T = pl.T, rT = 1.0f / pl.T;
+    if (tr0) trace(a.ws, L, row, 5);
+    if (g == 0 && tid == 0) {
         tr->klo = klo; tr->khi = khi; tr->xlo = xlo; tr->xhi = xhi;
-        tr->m = m; tr->lo = lo; tr->scf = hi > lo ? (float)FH / (hi - lo) : 0.0f; tr->T = pl.T;
+        tr->m = m; tr->lo = lo; tr->scf = scf; tr->T = T;
         tr->S = S; tr->A = A;
-        tr->count = 0u;
         tr->status = TR_ACTIVE;
     }
-}
-
-template <int EPT>
-__global__ __launch_bounds__(NT) void k_tp_hist(Args a)
-{
-    __shared__ uint32_t cnt[FH];
-    __shared__ unsigned long long mass[FH];
-    __shared__ double etab[ETAB_N];
-    __shared__ Red red;
-    const Layout &L = a.L;
-    const int tid = threadIdx.x;
-    exp_table(etab, tid);
-    const int64_t tasks = L.B * L.G;
-    for (int64_t t = blockIdx.x; t < tasks; t += gridDim.x) {
-        const int row = (int)(t / L.G), g = (int)(t % L.G);
-        const TopRow *tr = top_row(a, row);
-        if (ldp(&tr->status) != TR_ACTIVE) continue;
-        const float xlof = f32_of_key(ldp(&tr->xlo)), xhif = f32_of_key(ldp(&tr->xhi));
-        const float m = ldp(&tr->m), lo = ldp(&tr->lo), scf = ldp(&tr->scf), T = ldp(&tr->T), rT = 1.0f / T;
-        const double md = (double)m;
-        for (int b = tid; b < FH; b += NT) { cnt[b] = 0u; mass[b] = 0ull; }
-        float x[EPT];
-        const int64_t base = (int64_t)g * NT * EPT;
-        load_chunk<F32, EPT>(a.logits + (int64_t)row * a.stride_bytes, base, a.V, a.vec_ok, x);
-        __syncthreads();  // (also publishes etab on the first task)
-        double acc = 0.0;
-#pragma unroll
-        for (int i = 0; i < EPT; ++i) {
-            const float xi = x[i];
-            if (xi >= xlof) {
-                const float y = scale_r<F32>(xi, T, rT);
-                const double e = dexp((double)y - md, etab);
-                if (xi > xhif) {
-                    acc += e;
-                } else {
-                    const int b = fine_bin(y, lo, scf);
-                    atomicAdd(&cnt[b], 1u);
-                    atomicAdd(&mass[b], (unsigned long long)rint(e * FIX_ONE));
-                }
-            }
-        }
-        const double above = block_sum<double>(acc, red);  // (its barriers publish the bins)
-        TopChunk *tc = top_chunk(a, row, g);
-        if (tid == 0) tc->above = above;
-        for (int b = tid; b < FH; b += NT) { tc->cnt[b] = cnt[b]; tc->mass[b] = mass[b]; }
-        __syncthreads();
-    }
-}
-
-__global__ __launch_bounds__(NT) void k_tp_merge(Args a)
-{
-    __shared__ uint32_t cnt[FH];
-    __shared__ double mass[FH];
-    __shared__ Red red;
-    __shared__ int32_t bi[2];
-    __shared__ uint32_t bu[2];
-    const Layout &L = a.L;
-    const int row = blockIdx.x, tid = threadIdx.x, G = L.G;
-    TopRow *tr = top_row(a, row);
-    if (ldp(&tr->status) != TR_ACTIVE) return;
-    const double S = ldp(&tr->S), A = ldp(&tr->A);
-    trace(a.ws, L, row, 6);
-    // merged fine bins (exact integer sums, then doubles) and the mass above
-    // the band; each thread keeps 8 chunks' loads of its bins in flight
-    static_assert(FH == 2 * NT, "two bins per thread");
-    {
-        uint32_t c0 = 0u, c1 = 0u;
-        unsigned long long m0 = 0ull, m1 = 0ull;
-        for (int g0 = 0; g0 < G; g0 += 8) {
-            uint32_t cc[16];
-            unsigned long long mm[16];
-#pragma unroll
-            for (int q = 0; q < 8; ++q) {
-                const bool in = g0 + q < G;
-                const TopChunk *tc = top_chunk(a, row, in ? g0 + q : 0);
-                cc[2 * q] = in ? tc->cnt[tid] : 0u;
-                cc[2 * q + 1] = in ? tc->cnt[tid + NT] : 0u;
-                mm[2 * q] = in ? tc->mass[tid] : 0ull;
-                mm[2 * q + 1] = in ? tc->mass[tid + NT] : 0ull;
-            }
-#pragma unroll
-            for (int q = 0; q < 8; ++q) { c0 += cc[2 * q]; c1 += cc[2 * q + 1]; m0 += mm[2 * q]; m1 += mm[2 * q + 1]; }
-        }
-        cnt[tid] = c0; cnt[tid + NT] = c1;
-        mass[tid] = (double)m0 * (1.0 / FIX_ONE);
-        mass[tid + NT] = (double)m1 * (1.0 / FIX_ONE);
-    }
+    // this chunk's mass above the band, from its own coarse bins
     double ab = 0.0;
-    for (int g = tid; g < G; g += NT) ab += ldp(&top_chunk(a, row, g)->above);
-    const double above = block_sum<double>(ab, red);  // (its barriers publish the bins)
-    trace(a.ws, L, row, 7);
-    if (wave_id() == 0) {
-        // every integer weight is off by at most 1/2 unit: delta covers them
-        uint32_t n = 0u;
-        for (int b = lane_id(); b < FH; b += 64) n += cnt[b];
-        n = wave_sum(n);
-        const double delta = 1e-12 * S + (double)n * (0.5 / FIX_ONE);
-        double tmp;
-        const int jb = wave_find_desc<double>(mass, FH, A - delta - above, &tmp);
-        const int ja = wave_find_desc<double>(mass, FH, A + delta - above, &tmp);
-        uint32_t c2 = 0u, nab = 0u;
-        for (int b = lane_id(); b < FH; b += 64) { c2 += (b >= ja && b <= jb) ? cnt[b] : 0u; nab += b > jb ? cnt[b] : 0u; }
-        c2 = wave_sum(c2);
-        nab = wave_sum(nab);
-        if (lane_id() == 0) {
-            const bool ok = ja <= jb && c2 > 0u && c2 <= (uint32_t)SURV_CAP;
-            bi[0] = ok ? ja : -1; bi[1] = jb; bu[0] = nab;
-        }
+    if (tid < CB_N) {
+        const float mb = (float)tid + sm.off[g];
+        if (mb < (float)ba) ab = ldp(&rbf[g].coarse[tid]) * sm.chs[g];
+    }
+    const double above_g = block_sum<double>(ab, sm.red);
+    for (int b = tid; b < FH; b += NT) { sm.cnt[b] = 0u; sm.mass[b] = 0.0; }
+    if (tr0) trace(a.ws, L, row, 6);
+    // the band's elements (raw keys in [xlo, xhi]): a dense list first
+    const float xlof = f32_of_key(xlo), xhif = f32_of_key(xhi);
+    uint64_t bm = 0ull;
+#pragma unroll
+    for (int i = 0; i < EPT; ++i) bm |= (x[i] >= xlof && x[i] <= xhif) ? (1ull << i) : 0ull;
+    uint32_t nband;
+    const uint32_t boff = block_excl_scan<uint32_t>((uint32_t)__popcll(bm), sm.red, &nband);
+    {
+        uint32_t q = boff;
+#pragma unroll
+        for (int i = 0; i < EPT; ++i)
+            if (bm & (1ull << i)) { if (q < (uint32_t)LCAP) sm.lx[q] = x[i]; ++q; }
     }
     __syncthreads();
-    const int ja = bi[0], jb = bi[1];
-    trace(a.ws, L, row, 8);
-    if (ja < 0) { if (tid == 0) tr->status = TR_DEFER; return; }
-    if (tid == 0) { tr->ja = ja; tr->jb = jb; tr->fix_err = (double)bu[0] * (0.5 / FIX_ONE); }
-    trace(a.ws, L, row, 10);
-}
-
-template <int EPT>
-__global__ __launch_bounds__(NT) void k_tp_collect(Args a)
-{
-    __shared__ Red red;
-    __shared__ uint32_t base_s;
-    const Layout &L = a.L;
-    const int tid = threadIdx.x;
-    constexpr int VEC = Traits<F32>::VEC;
-    static_assert(FH == 2 * NT, "two bins per thread");
-    const int64_t tasks = L.B * L.G;
-    for (int64_t t = blockIdx.x; t < tasks; t += gridDim.x) {
-        const int row = (int)(t / L.G), g = (int)(t % L.G);
-        TopRow *tr = top_row(a, row);
-        if (ldp(&tr->status) != TR_ACTIVE) continue;
-        const float xlof = f32_of_key(ldp(&tr->xlo)), xhif = f32_of_key(ldp(&tr->xhi));
-        const float lo = ldp(&tr->lo), scf = ldp(&tr->scf), T = ldp(&tr->T), rT = 1.0f / T;
-        const int ja = ldp(&tr->ja), jb = ldp(&tr->jb);
-        float x[EPT];
-        const int64_t base = (int64_t)g * NT * EPT;
-        load_chunk<F32, EPT>(a.logits + (int64_t)row * a.stride_bytes, base, a.V, a.vec_ok, x);
-        // the chunk's kept mass above the final band: its above-mass plus its
-        // fine bins above jb
-        const TopChunk *tc = top_chunk(a, row, g);
-        const unsigned long long m0 = tid > jb ? tc->mass[tid] : 0ull, m1 = tid + NT > jb ? tc->mass[tid + NT] : 0ull;
-        const double cwg = block_sum<double>((double)(m0 + m1) * (1.0 / FIX_ONE), red);
-        if (tid == 0) tr->cw[g] = ldp(&tc->above) + cwg;
-        // the final band's elements: raw values in the coarse band whose fine bin is in [ja, jb]
-        uint64_t fb = 0ull;  // bit i: element i is in the final band
+    auto bin_one = [&](float xv) {
+        const float y = scale_r<F32>(xv, T, rT);
+        const int b = fine_bin(y, lo, scf);
+        atomicAdd(&sm.cnt[b], 1u);
+        atomicAdd(&sm.mass[b], dexp((double)y - md, sm.etab));
+    };
+    const uint32_t nl = nband < (uint32_t)LCAP ? nband : (uint32_t)LCAP;
+    for (uint32_t q = tid; q < nl; q += NT) bin_one(sm.lx[q]);
+    if (nband > (uint32_t)LCAP) {  // a very dense band: the rest from registers
+        uint32_t q = boff;
 #pragma unroll
-        for (int i = 0; i < EPT; ++i) {
-            if (x[i] >= xlof && x[i] <= xhif) {
-                const int b = fine_bin(scale_r<F32>(x[i], T, rT), lo, scf);
-                fb |= (b >= ja && b <= jb) ? (1ull << i) : 0ull;
-            }
-        }
-        uint32_t total;
-        const uint32_t off = block_excl_scan<uint32_t>((uint32_t)__popcll(fb), red, &total);
-        if (total == 0u) continue;
-        if (tid == 0) base_s = atomicAdd(&tr->count, total);
-        __syncthreads();
-        uint32_t q = base_s + off;
-        __syncthreads();
-#pragma unroll
-        for (int i = 0; i < EPT; ++i) {
-            if (fb & (1ull << i)) {
-                if (q < (uint32_t)SURV_CAP) {
-                    const int32_t j = (int32_t)(base + (((i / VEC) * NT + tid) * VEC) + (i % VEC));
-                    tr->list[q].key = row_key(scale_r<F32>(x[i], T, rT), F32);
-                    tr->list[q].idx = j;
-                }
-                ++q;
-            }
-        }
+        for (int i = 0; i < EPT; ++i)
+            if (bm & (1ull << i)) { if (q >= (uint32_t)LCAP) bin_one(x[i]); ++q; }
     }
+    __syncthreads();
+    if (tr0) trace(a.ws, L, row, 7);
+    // the stash window: every fine bin when the band fits, otherwise the bins
+    // around this chunk's own estimate of the cut (its fine masses scaled to
+    // the row's band mass), widened while the elements fit
+    int wlo = 0, whi = FH - 1;
+    if (nband > (uint32_t)STASH_CAP) {
+        {
+            // prefix counts of the fine bins, two per thread (lx is free now)
+            static_assert(FH == 2 * NT, "two fine bins per thread");
+            const uint32_t c0 = sm.cnt[2 * tid], c1 = sm.cnt[2 * tid + 1];
+            uint32_t tot;
+            const uint32_t ex = block_excl_scan<uint32_t>(c0 + c1, sm.red, &tot);
+            sm.lx[2 * tid] = __builtin_bit_cast(float, ex + c0);
+            sm.lx[2 * tid + 1] = __builtin_bit_cast(float, ex + c0 + c1);
+            __syncthreads();
+        }
+        if (wave_id() == 0) {
+            // per lane 8 bins, descending order: bin FH-1 first
+            constexpr int PB = FH / 64;
+            double mloc = 0.0;
+            const int l = lane_id();
+#pragma unroll
+            for (int q = 0; q < PB; ++q) mloc += sm.mass[FH - 1 - (l * PB + q)];
+            double bandm_chunk = wave_sum(mloc);
+            double bandm_row = 0.0;
+            for (int b = ba; b <= bb; ++b) bandm_row += sm.mc[b];
+            const double sc = bandm_chunk > 0.0 ? bandm_row / bandm_chunk : 0.0;
+            const double need = A - sm.bd[0];  // residual mass inside the band
+            // estimated cut bin: first bin (descending) where the scaled cumulative reaches need
+            const double inc = wave_incl_scan(mloc) * sc;
+            const uint64_t mk = __ballot(inc >= need);
+            int est = 0;
+            if (mk != 0ull) {
+                const int f = __builtin_ctzll(mk);
+                if (l == f) {
+                    double run = (inc - mloc * sc);
+                    est = FH - 1 - (f * PB + PB - 1);
+                    for (int q = 0; q < PB; ++q) {
+                        const int b = FH - 1 - (f * PB + q);
+                        run += sm.mass[b] * sc;
+                        if (run >= need) { est = b; break; }
+                    }
+                }
+                est = __shfl(est, f, 64);
+            }
+            // the widest window [est - h, est + h] (clipped to the bins)
+            // holding at most STASH_CAP elements, from the prefix counts
+            // P(b) = elements in bins [0, b] (in lx), by two 64-way steps
+            auto P = [&](int b) -> uint32_t { return b < 0 ? 0u : __builtin_bit_cast(uint32_t, sm.lx[b < FH ? b : FH - 1]); };
+            auto fits = [&](int h) { return P(est + h) - P(est - h - 1) <= (uint32_t)STASH_CAP; };
+            // coarse step: h = 8 l; then fine step within the last fitting 8
+            const uint64_t fc = __ballot(fits(8 * l));
+            int h = -1;
+            if (fc & 1ull) {
+                const int lc = 63 - __builtin_clzll(fc);  // fits() only shrinks as h grows
+                const uint64_t ff = __ballot(l < 8 && fits(8 * lc + l));
+                h = 8 * lc + (63 - __builtin_clzll(ff));
+            }
+            if (l == 0) {
+                sm.bi[2] = h >= 0 ? (est - h > 0 ? est - h : 0) : 1;
+                sm.bi[3] = h >= 0 ? (est + h < FH - 1 ? est + h : FH - 1) : 0;  // empty when one bin alone overflows
+            }
+        }
+        __syncthreads();
+        wlo = sm.bi[2]; whi = sm.bi[3];
+    }
+    if (tr0) trace(a.ws, L, row, 8);
+    // stash the window's elements
+    TopChunk *tc = top_chunk(a, row, g);
+    Cand *st = top_stash(a, row, g);
+    uint64_t sb = 0ull;
+    if (nband > (uint32_t)STASH_CAP) {
+#pragma unroll
+        for (int i = 0; i < EPT; ++i)
+            if (bm & (1ull << i)) {
+                const int b = fine_bin(scale_r<F32>(x[i], T, rT), lo, scf);
+                sb |= (b >= wlo && b <= whi) ? (1ull << i) : 0ull;
+            }
+    } else {
+        sb = bm;
+    }
+    uint32_t nst;
+    uint32_t q = block_excl_scan<uint32_t>((uint32_t)__popcll(sb), sm.red, &nst);
+    const int32_t base32 = (int32_t)base;
+#pragma unroll
+    for (int i = 0; i < EPT; ++i)
+        if (sb & (1ull << i)) {
+            if (q < (uint32_t)STASH_CAP) {
+                st[q].x = x[i];
+                st[q].idx = base32 + (int32_t)((((i / VEC) * NT + tid) * VEC) + (i % VEC));
+            }
+            ++q;
+        }
+    if (tid == 0) { tc->above = above_g; tc->nstash = nst; tc->wlo = wlo; tc->whi = whi; }
+    for (int b = tid; b < FH; b += NT) { tc->cnt[b] = sm.cnt[b]; tc->mass[b] = sm.mass[b]; }
+    if (tr0) trace(a.ws, L, row, 9);
 }
 
 constexpr int NTF = 1024;           // threads of k_tp_final (16 waves)
+
+// LDS of k_tp_final
+struct TopRowSmem {
+    union {
+        struct { uint32_t key[SURV_CAP]; int32_t idx[SURV_CAP]; double e[SURV_CAP]; } s;
+        struct { uint64_t k[SURV_CAP]; double e[SURV_CAP]; } so;
+    } u;
+    uint32_t cnt[FH];
+    double mass[FH];
+    double cw[G_MAX];
+    uint32_t ns[G_MAX];             // per chunk: elements stashed
+    uint32_t ok[G_MAX];             // per chunk: its window wlo | whi << 16, all ones when it overflowed
+    double etab[ETAB_N];
+    Red red;
+    uint32_t bu[8];
+    int32_t bi[8];
+    double bd[8];
+    unsigned long long bq[2];
+};
 
 __global__ __launch_bounds__(NTF) void k_tp_final(Args a)
 {
     __shared__ TopRowSmem sm;
     const Layout &L = a.L;
     const int row = blockIdx.x, tid = threadIdx.x, G = L.G;
+    mis_row_params P = a.params[row];
+    P.temperature = uni(P.temperature); P.top_k = uni(P.top_k); P.top_p = uni(P.top_p); P.uniform = uni(P.uniform);
+    const RowPlan pl = plan_row(P, a.V);
+    if (pl.mode != M_TOPP) return;
     TopRow *tr = top_row(a, row);
-    const uint32_t st = ldp(&tr->status);
-    if (st == TR_NONE) return;
     RowOut *ro = reinterpret_cast<RowOut *>(a.ws + L.rowout) + row;
-    const uint32_t n = ldp(&tr->count);
-    if (st != TR_ACTIVE || n == 0u || n > (uint32_t)SURV_CAP) {
+    if (ldp(&tr->status) != TR_ACTIVE) {
         if (tid == 0) ro->status = ROW_DEFER;
         return;
     }
-    const RowPlan pl = plan_row(a.params[row], a.V);
     RowCx c;
     c.rowp = a.logits + (int64_t)row * a.stride_bytes;
     c.V = a.V; c.vec_ok = a.vec_ok; c.G = G; c.CH = (int64_t)NT * L.ept; c.row = row; c.T = pl.T;
-    const float m = ldp(&tr->m);
+    const float m = ldp(&tr->m), lo = ldp(&tr->lo), scf = ldp(&tr->scf);
     c.m = m;
-    const double md = (double)m, A = ldp(&tr->A);
-    trace(a.ws, L, row, 11);
+    const double md = (double)m, A = ldp(&tr->A), S = ldp(&tr->S);
+    const float T = pl.T, rT = 1.0f / pl.T;
+    trace(a.ws, L, row, 10);
     exp_table(sm.etab, tid);
-    __syncthreads();
+    // merged fine bins: thread t sums bin t % FH over the chunks t / FH,
+    // t / FH + 2, ..., eight loads in flight
+    static_assert(NTF == 2 * FH, "two threads per fine bin");
     {
-        constexpr int PT = SURV_CAP / NTF;
-        Elem el[PT];
+        const int b = tid % FH, h = tid / FH;
+        uint32_t cn = 0u;
+        double ms = 0.0;
+        for (int g0 = h; g0 < G; g0 += 16) {
+            uint32_t cc[8];
+            double mm[8];
 #pragma unroll
-        for (int q = 0; q < PT; ++q) { const int i = q * NTF + tid; if (i < (int)n) el[q] = tr->list[i]; }
+            for (int u = 0; u < 8; ++u) {
+                const int g = g0 + 2 * u;
+                const TopChunk *tc = top_chunk(a, row, g < G ? g : 0);
+                cc[u] = g < G ? tc->cnt[b] : 0u;
+                mm[u] = g < G ? tc->mass[b] : 0.0;
+            }
 #pragma unroll
-        for (int q = 0; q < PT; ++q) {
-            const int i = q * NTF + tid;
-            if (i < (int)n) {
-                sm.u.s.key[i] = el[q].key;
-                sm.u.s.idx[i] = el[q].idx;
-                sm.u.s.e[i] = dexp((double)f32_of_key(el[q].key) - md, sm.etab);
+            for (int u = 0; u < 8; ++u) { cn += cc[u]; ms += mm[u]; }
+        }
+        if (h == 0) { sm.cnt[b] = cn; sm.mass[b] = ms; }
+        __syncthreads();
+        if (h == 1) { sm.cnt[b] += cn; sm.mass[b] += ms; }
+    }
+    trace(a.ws, L, row, 11);
+    // per-chunk facts in one pass: above-band mass, stash count and window
+    static_assert(G_MAX <= NTF, "one chunk per thread");
+    if (tid < G) {
+        const TopChunk *tc = top_chunk(a, row, tid);
+        sm.cw[tid] = ldp(&tc->above);
+        const uint32_t nsg = ldp(&tc->nstash);
+        const int32_t wl = ldp(&tc->wlo), wh = ldp(&tc->whi);
+        sm.ns[tid] = nsg;
+        sm.ok[tid] = (nsg <= (uint32_t)STASH_CAP) ? ((uint32_t)wl | ((uint32_t)wh << 16)) : 0xffffffffu;
+    }
+    __syncthreads();
+    trace(a.ws, L, row, 11);
+    if (wave_id() == 0) {
+        // the final band: fine bins whose cumulative mass (descending) can hold
+        // the cut, within the float64 rounding of the sums
+        double ab = 0.0;
+        uint32_t bad = 0u;
+        int wlo_max = 0, whi_min = FH - 1;
+        for (int g = lane_id(); g < G; g += 64) {
+            ab += sm.cw[g];
+            const uint32_t o = sm.ok[g];
+            if (o == 0xffffffffu) bad = 1u;
+            else { wlo_max = max(wlo_max, (int)(o & 0xffffu)); whi_min = min(whi_min, (int)(o >> 16)); }
+        }
+        const double above_band = wave_sum(ab);
+        bad = wave_sum(bad);
+        wlo_max = wave_max(wlo_max);
+        whi_min = wave_min(whi_min);
+        const double delta = 1e-12 * S;
+        double tmp;
+        const int jb = wave_find_desc<double>(sm.mass, FH, A - delta - above_band, &tmp);
+        const int ja = wave_find_desc<double>(sm.mass, FH, A + delta - above_band, &tmp);
+        uint32_t c2 = 0u;
+        double abf = 0.0;
+        for (int b = lane_id(); b < FH; b += 64) {
+            c2 += (b >= ja && b <= jb) ? sm.cnt[b] : 0u;
+            abf += b > jb ? sm.mass[b] : 0.0;
+        }
+        c2 = wave_sum(c2);
+        abf = wave_sum(abf);
+        if (lane_id() == 0) {
+            // every chunk's stash must hold the whole final band
+            const bool ok = bad == 0u && ja <= jb && ja >= wlo_max && jb <= whi_min && c2 > 0u && c2 <= (uint32_t)SURV_CAP;
+            sm.bi[0] = ok ? ja : -1; sm.bi[1] = jb; sm.bu[0] = c2; sm.bd[0] = above_band + abf;
+            sm.bu[1] = 0u;
+        }
+    }
+    __syncthreads();
+    const int ja = sm.bi[0], jb = sm.bi[1];
+    const uint32_t nwin = sm.bu[0];
+    const double above = sm.bd[0];
+    trace(a.ws, L, row, 12);
+    if (ja < 0) {
+        if (tid == 0) ro->status = ROW_DEFER;
+        return;
+    }
+    // one wave per chunk: its kept mass above the window (above-band mass
+    // plus fine bins above jb) and its stashed elements inside the window
+    constexpr int NWF = NTF / 64;
+    for (int g = wave_id(); g < G; g += NWF) {
+        const TopChunk *tc = top_chunk(a, row, g);
+        const Cand *stg = top_stash(a, row, g);
+        const uint32_t ns = sm.ns[g];
+        double mv[FH / 64];
+        Cand cv[STASH_CAP / 64];
+#pragma unroll
+        for (int q = 0; q < FH / 64; ++q) { const int b = q * 64 + lane_id(); mv[q] = b > jb ? tc->mass[b] : 0.0; }
+#pragma unroll
+        for (int q = 0; q < STASH_CAP / 64; ++q) {
+            const uint32_t i = (uint32_t)(q * 64 + lane_id());
+            cv[q] = i < ns ? ldp_cand(&stg[i]) : Cand{0.0f, 0};
+        }
+        double w = 0.0;
+#pragma unroll
+        for (int q = 0; q < FH / 64; ++q) w += mv[q];
+        w = wave_sum(w);
+        if (lane_id() == 0) sm.cw[g] += w;
+#pragma unroll
+        for (int q = 0; q < STASH_CAP / 64; ++q) {
+            const uint32_t i = (uint32_t)(q * 64 + lane_id());
+            bool in = false;
+            float y = 0.0f;
+            if (i < ns) {
+                y = scale_r<F32>(cv[q].x, T, rT);
+                const int b = fine_bin(y, lo, scf);
+                in = b >= ja && b <= jb;
+            }
+            const uint32_t p = wave_append(in, &sm.bu[1]);
+            if (in && p < (uint32_t)SURV_CAP) {
+                sm.u.s.key[p] = row_key(y, F32);
+                sm.u.s.idx[p] = cv[q].idx;
+                sm.u.s.e[p] = dexp((double)y - md, sm.etab);
             }
         }
     }
-    double ab = 0.0;
-    for (int g = tid; g < G; g += NTF) { const double w = ldp(&tr->cw[g]); sm.cw[g] = w; ab += w; }
-    const double above = block_sum<double, NTF / 64>(ab, sm.red);  // (its barriers publish the survivors)
-    trace(a.ws, L, row, 12);
+    __syncthreads();
+    trace(a.ws, L, row, 13);
+    const uint32_t n = sm.bu[1];
+    trace(a.ws, L, row, 14);
+    if (n != nwin) {  // the stashes do not hold the band exactly
+        if (tid == 0) ro->status = ROW_DEFER;
+        return;
+    }
     uint32_t cut_key = 0u;
     int32_t cut_i = 0;
     double ql = 0.0, wl = 0.0;
     const int rl = window_resolve<NTF>(sm, n, above, A, &cut_key, &cut_i, &ql, &wl);
-    // S, the above-masses and the survivors' weights carry relative errors
-    // below 1e-15 each (dexp) plus float64 summation rounding; the fixed-point
-    // bins above the band carry fix_err
-    const double err = 1e-12 * (above + A) + ldp(&tr->fix_err) + 1e-300;
-    trace(a.ws, L, row, 13);
+    // S, the above-masses and the window's weights carry relative errors
+    // below 1e-15 each (dexp) plus float64 summation rounding
+    const double err = 1e-12 * (above + A) + 1e-300;
     if (!(rl >= 0 && (A - ql) > err && (ql + wl - A) > err)) {
         if (tid == 0) ro->status = ROW_DEFER;
         return;
     }
+    trace(a.ws, L, row, 15);
     const int chsh = __builtin_ctz((unsigned)c.CH);
     for (int q = tid; q <= rl; q += NTF) {
         const int32_t j = (int32_t)(0xffffffffu - (uint32_t)sm.u.so.k[q]);
@@ -1876,20 +2399,18 @@ __global__ __launch_bounds__(NTF) void k_tp_final(Args a)
     int gsel;
     double resid, SK;
     pick_chunk(sm, G, pl.u, &gsel, &resid, &SK);
-    trace(a.ws, L, row, 14);
     int64_t id = -1;
     if (gsel >= 0) {
-        const float T = pl.T, rT = 1.0f / pl.T;
         id = draw_in_chunk<F32, NTF>(sm, c, gsel, resid, [&](float xv, int64_t j) -> double {
             const float y = scale_r<F32>(xv, T, rT);
             return (y != -INFINITY && kept_by_cut(row_key(y, F32), j, cut_key, cut_i)) ? dexp((double)y - md, sm.etab) : 0.0;
         });
     }
     write_row(ro, a, row, id, id >= 0 ? MIS_ROW_OK : MIS_ROW_INVALID, pl.mode, m, cut_key, cut_i, SK);
-    trace(a.ws, L, row, 15);
+    trace(a.ws, L, row, 30);
 }
 
-enum : int { FIN_ALL = 0, FIN_OTHERS = 1, FIN_DEFERRED = 2, FIN_REST = 3 };
+enum : int { FIN_ALL = 0, FIN_OTHERS = 1, FIN_DEFERRED = 2, FIN_REST = 3, FIN_TAIL = 4 };
 
 // One workgroup per row: merges the chunk summaries and finishes the row:
 // greedy, temperature, small top-k from the summaries; the generic re-read
@@ -1912,14 +2433,28 @@ __global__ __launch_bounds__(NT) void k_final(Args a, int phase)
     trace(a.ws, L, row, 16);
     __syncthreads();
     const ChunkSum *csr = reinterpret_cast<const ChunkSum *>(a.ws + L.chunks) + (size_t)row * L.G;
-    // phase FIN_ALL: every row (no k_tp_* passes ran); FIN_OTHERS: every row
-    // but the fp32 top-p rows (beside the k_tp_* passes); FIN_DEFERRED: the
-    // fp32 top-p rows those passes left to the generic path; FIN_REST: both
-    const bool topp32 = DT == F32 && sm.pl.mode == M_TOPP;
-    const bool deferred = topp32 && phase != FIN_ALL && phase != FIN_OTHERS && ldp(&ro->status) == ROW_DEFER;
-    if (phase == FIN_OTHERS && topp32) return;
-    if (phase == FIN_DEFERRED && !deferred) return;
-    if (phase == FIN_REST && topp32 && !deferred) return;
+    // k_rowpass serves greedy, temperature and small top-k rows (and rejects
+    // bad ones), the k_tp_* passes fp32 top-p rows; either leaves a row it
+    // cannot finish with status ROW_DEFER.  By phase:
+    //   FIN_ALL       after k_rowpass, no top-p passes: every row but
+    //                 k_rowpass's, and the rows it deferred;
+    //   FIN_OTHERS    after k_rowpass, beside the top-p passes: the rows
+    //                 neither serves (fp16/bf16 top-p, top-k above K_SMALL);
+    //   FIN_DEFERRED  after both: every deferred row;
+    //   FIN_REST      after the top-p passes, no k_rowpass: every row but
+    //                 the top-p passes', and the rows they deferred;
+    //   FIN_TAIL      FIN_DEFERRED when FIN_OTHERS did not run: the deferred
+    //                 rows and those neither serves.
+    const int mode = sm.pl.mode;
+    const bool rp = mode == M_BAD || mode == M_INVAL || mode == M_GREEDY || mode == M_TEMP || mode == M_SMALLK;
+    const bool tp = DT == F32 && mode == M_TOPP;
+    bool serve;
+    if (phase == FIN_ALL) serve = !rp || ldp(&ro->status) == ROW_DEFER;
+    else if (phase == FIN_OTHERS) serve = !rp && !tp;
+    else if (phase == FIN_DEFERRED) serve = (rp || tp) && ldp(&ro->status) == ROW_DEFER;
+    else if (phase == FIN_TAIL) serve = (!rp && !tp) || ldp(&ro->status) == ROW_DEFER;
+    else serve = !tp || ldp(&ro->status) == ROW_DEFER;
+    if (!serve) return;
     leader_row<DT>(sm, sm.cx, sm.pl, csr, ro, sm.args);
     trace(a.ws, L, row, 31);
 }
@@ -2029,31 +2564,36 @@ static hipError_t launch_dt(const Args &a, float *probs, uint32_t *keep, hipStre
     // and k_tp_* passes on the caller's stream; the rows the passes deferred
     // follow once both are done
     const bool side = tp32 && (kinds & MIS_KIND_OTHER) != 0;
+    if (tp32) hipLaunchKernelGGL(k_rows, dim3(1), dim3(NT), 0, st, a);  // the launch order the split halves read
     Side *sd = nullptr;
     if (side) {
+        // the other rows' chunk pass and row pass on the side stream, beside
+        // the fp32 top-p rows' chunk pass and top-p passes on the caller's
         if ((e = side_of_current(&sd)) != hipSuccess) return e;
         if ((e = hipEventRecord(sd->fork, st)) != hipSuccess) return e;
         if ((e = hipStreamWaitEvent(sd->s, sd->fork, 0)) != hipSuccess) return e;
         if ((e = launch_chunks<DT>(a, sd->s, K1_OTHERS)) != hipSuccess) return e;
         if (ev && nev > 3 && (e = hipEventRecord((hipEvent_t)ev[3], sd->s)) != hipSuccess) return e;
-        hipLaunchKernelGGL((k_final<DT>), dim3(B), dim3(NT), 0, sd->s, a, (int)FIN_OTHERS);
+        hipLaunchKernelGGL((k_rowpass<DT>), dim3(B), dim3(NTS), 0, sd->s, a);
+        if (kinds & MIS_KIND_GENERIC) hipLaunchKernelGGL((k_final<DT>), dim3(B), dim3(NT), 0, sd->s, a, (int)FIN_OTHERS);
         if ((e = hipGetLastError()) != hipSuccess) return e;
         if ((e = hipEventRecord(sd->join, sd->s)) != hipSuccess) return e;
     }
     if ((e = launch_chunks<DT>(a, st, side ? K1_TOPP32 : K1_ALL)) != hipSuccess) return e;
     if (ev && (e = hipEventRecord((hipEvent_t)ev[1], st)) != hipSuccess) return e;
+    // without the split: the row pass after the chunk pass, unless the batch
+    // holds fp32 top-p rows only (then k_final's FIN_REST serves the rest)
+    const bool rowpass_here = !side && !(tp32 && (kinds & MIS_KIND_OTHER) == 0u);
+    if (rowpass_here) hipLaunchKernelGGL((k_rowpass<DT>), dim3(B), dim3(NTS), 0, st, a);
     if (tp32) {
-        const unsigned tg = (unsigned)(a.L.B * a.L.G < TP_GRID ? a.L.B * a.L.G : TP_GRID);
-        hipLaunchKernelGGL(k_tp_prep, dim3(B), dim3(NT), 0, st, a);
-        if (a.L.ept == 64) hipLaunchKernelGGL((k_tp_hist<64>), dim3(tg), dim3(NT), 0, st, a);
-        else hipLaunchKernelGGL((k_tp_hist<32>), dim3(tg), dim3(NT), 0, st, a);
-        hipLaunchKernelGGL(k_tp_merge, dim3(B), dim3(NT), 0, st, a);
-        if (a.L.ept == 64) hipLaunchKernelGGL((k_tp_collect<64>), dim3(tg), dim3(NT), 0, st, a);
-        else hipLaunchKernelGGL((k_tp_collect<32>), dim3(tg), dim3(NT), 0, st, a);
+        const unsigned bg = (unsigned)(a.L.B * a.L.G);
+        if (a.L.ept == 64) hipLaunchKernelGGL((k_tp_hist<64>), dim3(bg), dim3(NT), 0, st, a);
+        else hipLaunchKernelGGL((k_tp_hist<32>), dim3(bg), dim3(NT), 0, st, a);
         hipLaunchKernelGGL(k_tp_final, dim3(B), dim3(NTF), 0, st, a);
         if ((e = hipGetLastError()) != hipSuccess) return e;
         if (side && (e = hipStreamWaitEvent(st, sd->join, 0)) != hipSuccess) return e;
-        hipLaunchKernelGGL((k_final<DT>), dim3(B), dim3(NT), 0, st, a, (int)(side ? FIN_DEFERRED : FIN_REST));
+        const int ph = !side ? FIN_REST : (kinds & MIS_KIND_GENERIC) ? FIN_DEFERRED : FIN_TAIL;
+        hipLaunchKernelGGL((k_final<DT>), dim3(B), dim3(NT), 0, st, a, ph);
     } else {
         hipLaunchKernelGGL((k_final<DT>), dim3(B), dim3(NT), 0, st, a, (int)FIN_ALL);
     }

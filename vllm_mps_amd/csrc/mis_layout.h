@@ -20,8 +20,8 @@ constexpr int K_PROBE = 512;       // fp16/bf16 top-p rows look for their cut am
 constexpr int EPT_DEFAULT = 32;    // elements per thread of the chunk pass (64 when G would exceed G_MAX)
 constexpr int CCAP = 8192;         // small-k candidates of a row cached in LDS (64 KB)
 constexpr int G_MAX = 256;         // chunks per row
-constexpr int CB_N = 16;           // coarse top-p bins (lane-private)
-constexpr float CB_SCALE = 0.5f;   // coarse bin = floor(y * CB_SCALE): 2 units of y
+constexpr int CB_N = 128;          // coarse top-p bins below a chunk's max (float64, per wave)
+constexpr float CB_SCALE = 4.0f;   // coarse bin = floor(y * CB_SCALE): 1/4 unit of y, 32 units in all
 constexpr int REGION_MAX = 16;     // L1 bins per 16-bit chain pass at most (re-read path)
 constexpr int RUN_CAP = REGION_MAX * 256;
 constexpr int TIE_CAP = 1024;
@@ -51,12 +51,14 @@ struct ChunkSum {               // 64 B per (row, chunk)
 };
 
 // per-(row, chunk) coarse mass bins of an fp32 top-p row
-struct RoundBuf {               // 256 B
-    double coarse[CB_N];        // mass per coarse bin (relative to the chunk max)
+struct RoundBuf {               // 1280 B
+    double coarse[CB_N];        // coarse[b]: mass of bin top - b (relative to the chunk max)
     double S;                   // sum of weights relative to the chunk max
-    double pad[15];
+    float top;                  // the chunk max's coarse bin floor(ymax * CB_SCALE)
+    float pad0;
+    double pad[30];
 };
-static_assert(sizeof(RoundBuf) == 256, "RoundBuf size");
+static_assert(sizeof(RoundBuf) % 256 == 0, "RoundBuf size");
 
 struct RowOut {                 // 64 B per row, read by k_emit
     int64_t id;
@@ -73,36 +75,36 @@ struct RowOut {                 // 64 B per row, read by k_emit
 struct Cand { float x; int32_t idx; };
 struct Elem { uint32_t key; int32_t idx; };
 
-// fp32 top-p passes (k_tp_*): per (row, chunk) fine bins over the row's
-// coarse band, per row the band keys, per-chunk kept masses and survivors
+// fp32 top-p passes (k_tp_hist, k_tp_final): per (row, chunk) fine bins over
+// the row's coarse band and a stash of band elements, per row the band
 constexpr int FH = 512;             // fine bins per chunk over the coarse band
-constexpr double FIX_ONE = 1099511627776.0;  // 2^40: fine-bin masses as integers of exp(y - m)
+constexpr int STASH_CAP = 512;      // band elements one chunk stashes (a window of fine bins when more)
 struct TopChunk {
-    double above;                   // float64 mass of the chunk's elements above the coarse band
-    double pad[31];
+    double above;                   // the chunk's mass above the band (relative to the row max)
+    uint32_t nstash;                // elements stashed
+    int32_t wlo, whi;               // every band element of the chunk in fine bins [wlo, whi] is stashed
+    uint32_t pad0;
+    double pad[29];
     uint32_t cnt[FH];
-    unsigned long long mass[FH];
+    double mass[FH];
 };
 static_assert(sizeof(TopChunk) % 256 == 0, "TopChunk size");
 enum : uint32_t { TR_NONE = 0, TR_ACTIVE = 1, TR_DEFER = 2 };
-struct TopRow {
-    uint32_t status, count;         // TR_*; survivors appended by the collect pass
+struct TopRow {                     // written by the row's chunk-0 workgroup of k_tp_hist
+    uint32_t status, pad0;          // TR_*
     uint32_t klo, khi;              // coarse band (row keys)
     uint32_t xlo, xhi;              // its raw-key interval
-    int32_t ja, jb;                 // final band: fine bins [ja, jb]
     uint32_t pad1[2];
     float m, lo, scf, T;            // row max of y; fine-bin grid y -> (y - lo) * scf; temperature
-    double S, A, fix_err;           // sum of exp(y - m), top_p * S, bound of the fixed-point sums
-    double pad[22];
-    double cw[G_MAX];               // per-chunk kept mass above the final band
-    Elem list[SURV_CAP];            // the final band's elements
+    double S, A;                    // sum of exp(y - m), top_p * S
+    double pad[24];
 };
 static_assert(sizeof(TopRow) % 256 == 0, "TopRow size");
 
 struct Layout {
     int64_t B, V;
     int ept, G;
-    size_t rowout, chunks, rbuf, cand, topc, topr, total;
+    size_t rowout, chunks, rbuf, cand, topc, topr, stash, perm, total;
 };
 
 inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -122,12 +124,15 @@ inline Layout make_layout(int64_t B, int64_t V, int dtype)
     size_t off = CTL_PREFIX;
     L.rowout = off; off = align256(off + sizeof(RowOut) * (size_t)B);
     L.chunks = off; off = align256(off + sizeof(ChunkSum) * BG);
-    L.rbuf = off;   off = align256(off + sizeof(RoundBuf) * BG);
+    L.rbuf = off;   off = align256(off + (dtype == MIS_DTYPE_F32 ? sizeof(RoundBuf) * BG : 0));
     L.cand = off;   off = align256(off + sizeof(Cand) * (size_t)CAND_CAP * BG);
     // fp32 top-p: per-chunk fine bins and per-row state of the top-p passes
     const bool f32 = dtype == MIS_DTYPE_F32;
     L.topc = off;   off = align256(off + (f32 ? sizeof(TopChunk) * BG : 0));
     L.topr = off;   off = align256(off + (f32 ? sizeof(TopRow) * (size_t)B : 0));
+    L.stash = off;  off = align256(off + (f32 ? sizeof(Cand) * (size_t)STASH_CAP * BG : 0));
+    // fp32: the rows in launch order (top-p rows first) and their count
+    L.perm = off;   off = align256(off + (f32 ? sizeof(int32_t) * ((size_t)B + 1) : 0));
     L.total = off;
     return L;
 }

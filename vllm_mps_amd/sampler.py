@@ -74,25 +74,37 @@ def host_row_params(params: Sequence[SamplingParams], dtype: torch.dtype) -> np.
 
 KIND_TOPP32 = _native.KIND_TOPP32
 KIND_OTHER = _native.KIND_OTHER
+KIND_GENERIC = _native.KIND_GENERIC
 
 
 def row_kinds(temperature, top_k, top_p, V: int, dtype: torch.dtype) -> int:
     """Row-kind hint for ``mis_sample_ex`` from host-side per-row parameters
-    (sequences or arrays of floats/ints): which kinds the batch holds.  fp32
-    logits with 0 < T, top-k off (0 or >= V) and top_p < 1 are the fp32
-    top-p kind; every other row is OTHER.  Only a performance hint: the
-    results do not depend on it."""
+    (sequences or arrays of floats/ints): which kinds the batch holds.
+    * TOPP32: fp32 logits with 0 < T, top-k off (0 or >= V) and top_p < 1;
+    * OTHER: every other row;
+    * GENERIC: among the others, rows the generic row pass serves (0 < T and
+      1024 < top_k < V, or 16-bit logits with top-k off and top_p < 1).
+    Only a performance hint: the results do not depend on it."""
     t = np.asarray(temperature, dtype=np.float64).reshape(-1)
     k = np.asarray(top_k, dtype=np.int64).reshape(-1)
     p = np.asarray(top_p, dtype=np.float64).reshape(-1)
-    if dtype != torch.float32:
-        return KIND_OTHER if t.size else 0
-    topp = (t > 0) & ((k == 0) | (k >= V)) & (np.float32(1.0) > p.astype(np.float32)) & (p > 0)
+    if t.size == 0:
+        return 0
+    stoch = ~(t == 0)  # NaN temperatures are rejected rows, not greedy
+    k_off = (k <= 0) | (k >= V)
+    p_on = (np.float32(1.0) > p.astype(np.float32)) & (p > 0)
+    if dtype == torch.float32:
+        topp = stoch & k_off & p_on
+    else:
+        topp = np.zeros_like(stoch)
+    generic = stoch & ((k > 1024) & (k < V) | (dtype != torch.float32) & k_off & p_on)
     kinds = 0
     if topp.any():
         kinds |= KIND_TOPP32
     if (~topp).any():
         kinds |= KIND_OTHER
+    if generic.any():
+        kinds |= KIND_GENERIC
     return kinds
 
 
