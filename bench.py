@@ -170,7 +170,7 @@ def main():
     step_us = [t[0].elapsed_time(t[2]) * 1e3 for t in evs]
     # the chunk pass: from the first event to the later end of its launches
     # (two, and the fourth event recorded, exactly for fp32 with both kinds)
-    split = w.dtype == "f32" and kinds == 3
+    split = w.dtype == "f32" and (kinds & 3) == 3
     k1_us = [(max(t[0].elapsed_time(t[1]), t[0].elapsed_time(t[3])) if split else t[0].elapsed_time(t[1])) * 1e3
              for t in evs]
     k2_us = [st - k1 for st, k1 in zip(step_us, k1_us)]  # the rest of the step

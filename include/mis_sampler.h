@@ -17,8 +17,12 @@
  *       MIS_ROW_BAD_PARAM instead of a Python ValueError)
  *
  * All pointers except the workspace size are device pointers.  No exceptions,
- * no host synchronisation and no allocation happen inside mis_sample(); every
- * launch goes on `stream` (a hipStream_t; NULL = the legacy default stream).
+ * no host synchronisation and no allocation happen inside mis_sample(),
+ * mis_sample_profiled() and mis_sample_ex(); every launch goes on `stream` (a
+ * hipStream_t; NULL = the legacy default stream), or on a caller-created
+ * side stream (mis_context) that `stream` joins.  The library keeps no
+ * process-global state: calls on different streams with their own
+ * workspaces (and contexts) may run concurrently.
  */
 #ifndef MIS_SAMPLER_H
 #define MIS_SAMPLER_H
@@ -30,7 +34,7 @@
 extern "C" {
 #endif
 
-#define MIS_ABI_VERSION 5
+#define MIS_ABI_VERSION 6
 
 /* logits element type */
 enum { MIS_DTYPE_F32 = 0, MIS_DTYPE_F16 = 1, MIS_DTYPE_BF16 = 2 };
@@ -134,23 +138,38 @@ int mis_sample_profiled(const void *logits, int dtype, int64_t B, int64_t V, int
 enum { MIS_KIND_TOPP32 = 1, MIS_KIND_OTHER = 2, MIS_KIND_GENERIC = 4, MIS_KIND_ALL = 7 };
 
 /*
- * mis_sample() with a row-kind hint and optional events: NULL, or four
- * hipEvent_t handles, events[0..2] as by mis_sample_profiled() and events[3]
- * after the chunk pass of the rows the side stream serves.  A batch holding
- * both fp32 top-p rows and other rows splits the chunk pass: the other rows'
- * half runs on a per-device side stream (default priority), so events[1]
- * (on `stream`) then closes only the top-p rows' half and events[3] the other
- * half; both halves start after events[0], and the chunk pass as a whole ends
- * at the later of the two.  The split happens exactly when dtype is
- * MIS_DTYPE_F32 and kinds holds both bits; without it events[3] is not
- * recorded (events[1] closes the whole chunk pass).  No counterpart in the reference: its sampler runs on the host,
- * which knows each request's SamplingParams; the engine's batch builder
- * passes what it knows.
+ * A caller's side stream: a second stream on the device current at creation
+ * (default priority) and two events that fork it from the caller's stream
+ * and join it back.  mis_context_create allocates them; mis_sample_ex uses
+ * them when given the context, and creates nothing itself.  Calls that
+ * overlap in time need contexts (and workspaces) of their own.  No
+ * counterpart in the reference (its sampler runs on the host, one row at a
+ * time, engine/llm_engine.py:341-344).
+ */
+typedef struct mis_context mis_context;
+int mis_context_create(mis_context **out);
+int mis_context_destroy(mis_context *ctx);
+
+/*
+ * mis_sample() with a row-kind hint, optional events and an optional
+ * context.  events: NULL, or four hipEvent_t handles, events[0..2] as by
+ * mis_sample_profiled() and events[3] after the chunk pass of the rows the
+ * side stream serves.  ctx: NULL (every launch on `stream`), or a context of
+ * the current device.  With a context, a batch holding both fp32 top-p rows
+ * and other rows splits: the other rows' chunk pass and row pass run on the
+ * context's side stream beside the top-p rows' passes on `stream`, which
+ * joins the side stream before the call's last launch.  events[1] (on
+ * `stream`) then closes only the top-p rows' half of the chunk pass and
+ * events[3] the other half; both start after events[0].  Without the split
+ * events[3] is not recorded (events[1] closes the whole chunk pass).  No
+ * counterpart in the reference: its sampler runs on the host, which knows
+ * each request's SamplingParams; the engine's batch builder passes what it
+ * knows.
  */
 int mis_sample_ex(const void *logits, int dtype, int64_t B, int64_t V, int64_t row_stride,
                   const mis_row_params *params, int64_t *out_ids, int32_t *out_status,
                   float *out_probs, uint32_t *out_keep, void *workspace, size_t workspace_bytes,
-                  void *stream, unsigned kinds, void *const *events);
+                  void *stream, unsigned kinds, void *const *events, mis_context *ctx);
 
 /* Human-readable text for an API return code. */
 const char *mis_strerror(int code);

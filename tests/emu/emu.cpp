@@ -353,8 +353,15 @@ int main(int argc, char **argv)
     float *probs = want ? (float *)malloc((size_t)B * V * 4) : nullptr;
     uint32_t *keep = want ? (uint32_t *)malloc((size_t)B * W * 4) : nullptr;
     if (want) { for (int64_t i = 0; i < B * V; ++i) probs[i] = -1.0f; memset(keep, 0, (size_t)B * W * 4); }
+    // EMU_SIDE=1: with a context (the split schedule), else one stream
+    mis_context *ctx = nullptr;
+    if (getenv("EMU_SIDE") && atoi(getenv("EMU_SIDE")) && mis_context_create(&ctx) != MIS_OK) {
+        fprintf(stderr, "mis_context_create failed\n");
+        return 3;
+    }
     const int rc = mis_sample_ex(logits, dtype, B, V, V, params, ids, status, probs, keep, ws, ws_bytes, nullptr,
-                                 (unsigned)kinds, nullptr);
+                                 (unsigned)kinds, nullptr, ctx);
+    mis_context_destroy(ctx);
     if (rc != MIS_OK) { fprintf(stderr, "mis_sample_ex: %s\n", mis_strerror(rc)); return 3; }
     FILE *o = fopen(argv[2], "wb");
     if (!o) { perror("out"); return 2; }

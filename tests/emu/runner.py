@@ -21,9 +21,11 @@ DTYPE_CODE = {"f32": 0, "f16": 1, "bf16": 2}
 MAGIC = 0x4D495345
 
 
-def run(w: W.Workload, debug: bool = True, kinds: int = 7, timeout: float = 600.0, trace: bool = False) -> dict:
+def run(w: W.Workload, debug: bool = True, kinds: int = 7, timeout: float = 600.0, trace: bool = False,
+        side: bool = True) -> dict:
     """trace=True: also returns the MIS_TRACE phase table (``trace`` [B, 32],
-    a logical clock: nonzero where a row passed that phase)."""
+    a logical clock: nonzero where a row passed that phase).  side=True:
+    with a mis_context (the split schedule), else every launch in one stream."""
     exe = build_emu.build(trace=trace)
     B, V = w.shape
     params = np.zeros((B, 4), dtype=np.int32)
@@ -41,6 +43,7 @@ def run(w: W.Workload, debug: bool = True, kinds: int = 7, timeout: float = 600.
             f.write(params.tobytes())
         env = dict(os.environ, ASAN_OPTIONS="detect_leaks=0:abort_on_error=1:detect_stack_use_after_return=0")
         ctr = os.path.join(td, "trace.bin")
+        env["EMU_SIDE"] = "1" if side else "0"
         if trace:
             env["EMU_TRACE_OUT"] = ctr
         res = subprocess.run([exe, cin, cout], capture_output=True, text=True, timeout=timeout, env=env)

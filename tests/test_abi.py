@@ -46,7 +46,8 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version_and_strings(lib):
-    assert lib.mis_abi_version() == 4
+    from vllm_mps_amd import _native
+    assert lib.mis_abi_version() == _native.ABI_VERSION == 6
     assert lib.mis_strerror(0) == b"ok"
     assert b"workspace" in lib.mis_strerror(2)
     assert lib.mis_last_hip_error() == 0
@@ -81,11 +82,14 @@ def test_argument_validation_without_gpu(lib):
     assert lib.mis_sample_profiled(fake, 0, 1, 10, 10, fake, fake, None, None, None, fake, 1 << 20, None, ev) == 1
     # the hinted entry: unknown kind bits and partial event sets (four handles) are argument errors
     lib.mis_sample_ex.argtypes = [vp, ctypes.c_int, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, vp, vp, vp, vp, vp,
-                                  vp, ctypes.c_size_t, vp, ctypes.c_uint, vp]
-    assert lib.mis_sample_ex(fake, 0, 1, 10, 10, fake, fake, None, None, None, fake, 1 << 20, None, 4, None) == 1
+                                  vp, ctypes.c_size_t, vp, ctypes.c_uint, vp, vp]
+    assert lib.mis_sample_ex(fake, 0, 1, 10, 10, fake, fake, None, None, None, fake, 1 << 20, None, 8, None, None) == 1
     ev4 = (vp * 4)(fake, fake, fake, None)  # the fourth event missing
-    assert lib.mis_sample_ex(fake, 0, 1, 10, 10, fake, fake, None, None, None, fake, 1 << 20, None, 3, ev4) == 1
-    assert lib.mis_sample_ex(fake, 0, 0, 10, 10, fake, fake, None, None, None, fake, 1 << 20, None, 3, None) == 0
+    assert lib.mis_sample_ex(fake, 0, 1, 10, 10, fake, fake, None, None, None, fake, 1 << 20, None, 3, ev4, None) == 1
+    assert lib.mis_sample_ex(fake, 0, 0, 10, 10, fake, fake, None, None, None, fake, 1 << 20, None, 7, None, None) == 0
+    # a context pointer out of nowhere is never dereferenced before the checks above
+    lib.mis_context_create.argtypes = [ctypes.POINTER(vp)]
+    assert lib.mis_context_create(None) == 1
 
 
 def test_product_path_fails_loudly_without_library(tmp_path):

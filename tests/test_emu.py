@@ -24,9 +24,9 @@ def _emu(w, **kw):
     return runner.run(w, **kw)
 
 
-def _check(name, w, kinds=7):
+def _check(name, w, kinds=7, side=True):
     print(f"[emu] {name} dtype={w.dtype} shape={w.shape}", flush=True)
-    g = _emu(w, kinds=kinds)
+    g = _emu(w, kinds=kinds, side=side)
     rep = C.compare(w.dtype, H.params_of(w), g, H.run_oracle(w))
     print(f"[emu] {name}: {rep.summary()}", flush=True)
     assert rep.ok, rep.summary()
@@ -70,9 +70,12 @@ def test_emu_mixed_modes(dtype):
     p = [1.0, 1.0, 1.0, 0.8, 0.5, 0.9, 0.7, 0.95]
     w = H.synthetic(dtype, len(T), V, seed=3, temperature=T, top_k=k, top_p=p, ninf_frac=0.1, dup_max=True)
     _check("mixed", w)
-    # hints that leave kinds out: the same results through the fallback phases
+    # hints that leave kinds out, and one stream without a context: the same
+    # results through the fallback phases
     for kinds in (3, 2, 1):
         _check(f"mixed kinds={kinds}", w, kinds=kinds)
+    _check("mixed one stream", w, side=False)
+    _check("mixed one stream kinds=3", w, kinds=3, side=False)
 
 
 def test_emu_config_c2():

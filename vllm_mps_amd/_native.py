@@ -12,14 +12,14 @@ from . import build as _build
 
 DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
 ROW_OK, ROW_BAD_PARAM, ROW_INVALID, ROW_UNSUPPORTED, ROW_INTERNAL = 0, 1, 2, 3, 4
-ABI_VERSION = 5
+ABI_VERSION = 6
 KIND_TOPP32 = 1  # MIS_KIND_TOPP32
 KIND_OTHER = 2   # MIS_KIND_OTHER
 KIND_GENERIC = 4  # MIS_KIND_GENERIC
 KIND_ALL = 7     # MIS_KIND_ALL
 
-EXPORTED = ("mis_workspace_bytes", "mis_workspace_init", "mis_sample", "mis_sample_profiled", "mis_sample_ex", "mis_strerror", "mis_last_hip_error",
-            "mis_abi_version")
+EXPORTED = ("mis_workspace_bytes", "mis_workspace_init", "mis_sample", "mis_sample_profiled", "mis_sample_ex",
+            "mis_context_create", "mis_context_destroy", "mis_strerror", "mis_last_hip_error", "mis_abi_version")
 
 _lib = None
 
@@ -53,8 +53,12 @@ def load():
                                         ctypes.POINTER(vp)]
     lib.mis_sample_profiled.restype = ctypes.c_int
     lib.mis_sample_ex.argtypes = [vp, ctypes.c_int, i64, i64, i64, vp, vp, vp, vp, vp, vp, ctypes.c_size_t, vp,
-                                  ctypes.c_uint, vp]
+                                  ctypes.c_uint, vp, vp]
     lib.mis_sample_ex.restype = ctypes.c_int
+    lib.mis_context_create.argtypes = [ctypes.POINTER(vp)]
+    lib.mis_context_create.restype = ctypes.c_int
+    lib.mis_context_destroy.argtypes = [vp]
+    lib.mis_context_destroy.restype = ctypes.c_int
     lib.mis_strerror.argtypes = [ctypes.c_int]
     lib.mis_strerror.restype = ctypes.c_char_p
     lib.mis_last_hip_error.restype = ctypes.c_int
@@ -77,18 +81,47 @@ def workspace_init(ws_ptr: int, ws_bytes: int, stream: int) -> None:
         raise MisError(f"mis_workspace_init failed: {lib.mis_strerror(rc).decode()}")
 
 
+class Context:
+    """A mis_context: a side stream and its fork / join events on the device
+    current at creation (mis_context_create); destroyed with the object."""
+
+    def __init__(self) -> None:
+        self._lib = load()
+        h = ctypes.c_void_p()
+        rc = self._lib.mis_context_create(ctypes.byref(h))
+        if rc != 0:
+            raise MisError(f"mis_context_create failed: {self._lib.mis_strerror(rc).decode()} "
+                           f"(hipError {self._lib.mis_last_hip_error()})")
+        self.handle = h.value
+
+    def close(self) -> None:
+        if getattr(self, "handle", None):
+            self._lib.mis_context_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 def sample(logits_ptr: int, dtype: int, B: int, V: int, row_stride: int, params_ptr: int, ids_ptr: int,
            status_ptr: int | None, probs_ptr: int | None, keep_ptr: int | None, ws_ptr: int, ws_bytes: int,
-           stream: int, events: tuple | None = None, kinds: int | None = None) -> None:
+           stream: int, events: tuple | None = None, kinds: int | None = None, context: Context | None = None) -> None:
     """events: None, or three handles (mis_sample_profiled), or four with
-    kinds (mis_sample_ex: the fourth closes the side stream's chunk pass)."""
+    kinds (mis_sample_ex: the fourth closes the side stream's chunk pass).
+    context: a Context for mis_sample_ex's split schedule (needs kinds)."""
     lib = load()
+    if context is not None and kinds is None:
+        kinds = KIND_ALL
     if kinds is not None:
         if events is not None and len(events) != 4:
             raise ValueError("mis_sample_ex takes four events")
         ev = None if events is None else (ctypes.c_void_p * 4)(*events)
         rc = lib.mis_sample_ex(logits_ptr, dtype, B, V, row_stride, params_ptr, ids_ptr, status_ptr, probs_ptr,
-                               keep_ptr, ws_ptr, ws_bytes, stream, kinds, ev)
+                               keep_ptr, ws_ptr, ws_bytes, stream, kinds, ev,
+                               None if context is None else context.handle)
     elif events is None:
         rc = lib.mis_sample(logits_ptr, dtype, B, V, row_stride, params_ptr, ids_ptr, status_ptr, probs_ptr,
                             keep_ptr, ws_ptr, ws_bytes, stream)

@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <new>
+
 #include "mis_launch.h"
 #include "mis_layout.h"
 #include "mis_sampler.h"
@@ -11,6 +13,12 @@
 namespace mis {
 static thread_local int g_last_hip = 0;
 }  // namespace mis
+
+// A caller's side stream for one device (mis_context_create).
+struct mis_context {
+    int device;
+    mis::SideStreams side;
+};
 
 extern "C" {
 
@@ -33,7 +41,7 @@ int mis_workspace_init(void *workspace, size_t workspace_bytes, void *stream)
 static int sample_impl(const void *logits, int dtype, int64_t B, int64_t V, int64_t row_stride,
                        const mis_row_params *params, int64_t *out_ids, int32_t *out_status, float *out_probs,
                        uint32_t *out_keep, void *workspace, size_t workspace_bytes, void *stream,
-                       unsigned kinds, void *const *events, int nev)
+                       unsigned kinds, void *const *events, int nev, const mis_context *ctx)
 {
     using namespace mis;
     if (dtype < 0 || dtype > 2 || B < 0 || V <= 0 || row_stride < V) return MIS_ERR_INVALID_ARG;
@@ -56,9 +64,16 @@ static int sample_impl(const void *logits, int dtype, int64_t B, int64_t V, int6
     a.out_status = out_status;
     hipStream_t st = (hipStream_t)stream;
     hipError_t e;
-    if (dtype == MIS_DTYPE_F32) e = launch_f32(a, out_probs, out_keep, st, kinds, events, nev);
-    else if (dtype == MIS_DTYPE_F16) e = launch_f16(a, out_probs, out_keep, st, kinds, events, nev);
-    else e = launch_bf16(a, out_probs, out_keep, st, kinds, events, nev);
+    const SideStreams *sd = nullptr;
+    if (ctx) {
+        int dev = -1;
+        if ((e = hipGetDevice(&dev)) != hipSuccess) { g_last_hip = (int)e; return MIS_ERR_HIP; }
+        if (dev != ctx->device) return MIS_ERR_INVALID_ARG;
+        sd = &ctx->side;
+    }
+    if (dtype == MIS_DTYPE_F32) e = launch_f32(a, out_probs, out_keep, st, kinds, events, nev, sd);
+    else if (dtype == MIS_DTYPE_F16) e = launch_f16(a, out_probs, out_keep, st, kinds, events, nev, sd);
+    else e = launch_bf16(a, out_probs, out_keep, st, kinds, events, nev, sd);
     if (e != hipSuccess) { g_last_hip = (int)e; return MIS_ERR_HIP; }
     return MIS_OK;
 }
@@ -68,7 +83,7 @@ int mis_sample(const void *logits, int dtype, int64_t B, int64_t V, int64_t row_
                uint32_t *out_keep, void *workspace, size_t workspace_bytes, void *stream)
 {
     return sample_impl(logits, dtype, B, V, row_stride, params, out_ids, out_status, out_probs, out_keep,
-                       workspace, workspace_bytes, stream, MIS_KIND_ALL, nullptr, 0);
+                       workspace, workspace_bytes, stream, MIS_KIND_ALL, nullptr, 0, nullptr);
 }
 
 int mis_sample_profiled(const void *logits, int dtype, int64_t B, int64_t V, int64_t row_stride,
@@ -78,18 +93,48 @@ int mis_sample_profiled(const void *logits, int dtype, int64_t B, int64_t V, int
 {
     if (!events || !events[0] || !events[1] || !events[2]) return MIS_ERR_INVALID_ARG;
     return sample_impl(logits, dtype, B, V, row_stride, params, out_ids, out_status, out_probs, out_keep,
-                       workspace, workspace_bytes, stream, MIS_KIND_ALL, events, 3);
+                       workspace, workspace_bytes, stream, MIS_KIND_ALL, events, 3, nullptr);
 }
 
 int mis_sample_ex(const void *logits, int dtype, int64_t B, int64_t V, int64_t row_stride,
                   const mis_row_params *params, int64_t *out_ids, int32_t *out_status, float *out_probs,
                   uint32_t *out_keep, void *workspace, size_t workspace_bytes, void *stream, unsigned kinds,
-                  void *const *events)
+                  void *const *events, mis_context *ctx)
 {
     if ((kinds & ~(unsigned)MIS_KIND_ALL) != 0u) return MIS_ERR_INVALID_ARG;
     if (events && (!events[0] || !events[1] || !events[2] || !events[3])) return MIS_ERR_INVALID_ARG;
     return sample_impl(logits, dtype, B, V, row_stride, params, out_ids, out_status, out_probs, out_keep,
-                       workspace, workspace_bytes, stream, kinds, events, 4);
+                       workspace, workspace_bytes, stream, kinds, events, 4, ctx);
+}
+
+int mis_context_create(mis_context **out)
+{
+    if (!out) return MIS_ERR_INVALID_ARG;
+    *out = nullptr;
+    mis_context *c = new (std::nothrow) mis_context();
+    if (!c) return MIS_ERR_HIP;
+    hipError_t e = hipGetDevice(&c->device);
+    if (e == hipSuccess) e = hipStreamCreateWithFlags(&c->side.s, hipStreamNonBlocking);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&c->side.fork, hipEventDisableTiming);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&c->side.join, hipEventDisableTiming);
+    if (e != hipSuccess) {
+        mis::g_last_hip = (int)e;
+        mis_context_destroy(c);
+        return MIS_ERR_HIP;
+    }
+    *out = c;
+    return MIS_OK;
+}
+
+int mis_context_destroy(mis_context *ctx)
+{
+    if (!ctx) return MIS_OK;
+    int rc = MIS_OK;
+    if (ctx->side.fork && hipEventDestroy(ctx->side.fork) != hipSuccess) rc = MIS_ERR_HIP;
+    if (ctx->side.join && hipEventDestroy(ctx->side.join) != hipSuccess) rc = MIS_ERR_HIP;
+    if (ctx->side.s && hipStreamDestroy(ctx->side.s) != hipSuccess) rc = MIS_ERR_HIP;
+    delete ctx;
+    return rc;
 }
 
 const char *mis_strerror(int code)
@@ -99,7 +144,7 @@ const char *mis_strerror(int code)
     case MIS_ERR_INVALID_ARG: return "invalid argument";
     case MIS_ERR_WORKSPACE: return "workspace too small or not 256-byte aligned";
     case MIS_ERR_HIP: return "HIP launch failed";
-    case MIS_ERR_UNSUPPORTED: return "shape not supported (V > 2^30, B > 65535 or too many chunks)";
+    case MIS_ERR_UNSUPPORTED: return "shape not supported (V > 2^30, B > 2^31 - 1 or more than 256 chunks per row)";
     default: return "unknown error";
     }
 }

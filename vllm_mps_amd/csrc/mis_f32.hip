@@ -5,9 +5,9 @@
 namespace mis {
 
 hipError_t launch_f32(const Args &a, float *probs, uint32_t *keep, hipStream_t st, unsigned kinds,
-                     void *const *ev, int nev)
+                     void *const *ev, int nev, const SideStreams *side)
 {
-    return launch_dt<F32>(a, probs, keep, st, kinds, ev, nev);
+    return launch_dt<F32>(a, probs, keep, st, kinds, ev, nev, side);
 }
 
 }  // namespace mis

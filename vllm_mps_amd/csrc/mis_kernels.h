@@ -40,9 +40,9 @@
 #include <math.h>
 #include <stdint.h>
 
-#include <mutex>
 
 #include "mis_device.h"
+#include "mis_launch.h"
 #include "mis_layout.h"
 #include "mis_sampler.h"
 
@@ -1809,6 +1809,7 @@ __global__ __launch_bounds__(NTS) void k_rowpass(Args a)
             sm.u.so.e[i] = et;
             __syncthreads();
             block_sort_desc<NTS, SURV_CAP>(sm.u.so.k, sm.u.so.e, (int)ns);
+            trace(a.ws, L, row, 23);
             const uint32_t st = i < (int)ns && (i == 0 || (uint32_t)(sm.u.so.k[i] >> 32) != (uint32_t)(sm.u.so.k[i - 1] >> 32)) ? 1u : 0u;
             uint32_t nr;
             const uint32_t r = block_excl_scan<uint32_t, NW>(st, sm.red, &nr);
@@ -1819,6 +1820,7 @@ __global__ __launch_bounds__(NTS) void k_rowpass(Args a)
             __syncthreads();
             if ((uint32_t)i < nr) sm.rcnt[i] = ((uint32_t)i + 1 < nr ? sm.rkey[i + 1] : ns) - sm.rkey[i];
             __syncthreads();
+            trace(a.ws, L, row, 24);
             if (tid == 0) {
                 const float thr16 = rn_dtype(pl.top_p, DT);
                 float F = 0.0f;
@@ -1834,6 +1836,7 @@ __global__ __launch_bounds__(NTS) void k_rowpass(Args a)
                 }
             }
             __syncthreads();
+            trace(a.ws, L, row, 25);
             if (sm.bu[0] == 0u) {  // nothing kept: not a distribution
                 write_row(ro, a, row, -1, MIS_ROW_INVALID, pl.mode, m, 0u, 0, 0.0);
                 return;
@@ -2501,34 +2504,6 @@ __global__ __launch_bounds__(NT) void k_emit(const char *__restrict__ logits, in
 
 // ------------------------------------------------------------------ host side
 
-// Per device: a second stream (default priority) and the two events that
-// fork it from the caller's stream and join it back, made on the first call
-// on that device and kept until the process ends.  Calls that overlap on one
-// device share them, as they would share a workspace: such calls race.
-struct Side { hipStream_t s; hipEvent_t fork, join; };
-constexpr int MAX_DEVICES = 64;
-static Side g_side[MAX_DEVICES];
-static std::mutex g_side_mu;
-static hipError_t side_of_current(Side **out)
-{
-    int dev = 0;
-    hipError_t e = hipGetDevice(&dev);
-    if (e != hipSuccess) return e;
-    if (dev < 0 || dev >= MAX_DEVICES) return hipErrorInvalidDevice;
-    std::lock_guard<std::mutex> lk(g_side_mu);
-    Side &sd = g_side[dev];
-    if (!sd.s) {
-        hipStream_t s = nullptr;
-        hipEvent_t f = nullptr, j = nullptr;
-        if ((e = hipStreamCreateWithFlags(&s, hipStreamNonBlocking)) != hipSuccess) return e;
-        if ((e = hipEventCreateWithFlags(&f, hipEventDisableTiming)) != hipSuccess) return e;
-        if ((e = hipEventCreateWithFlags(&j, hipEventDisableTiming)) != hipSuccess) return e;
-        sd.fork = f; sd.join = j; sd.s = s;
-    }
-    *out = &sd;
-    return hipSuccess;
-}
-
 template <int DT, int EPT>
 static hipError_t launch_sample(const Args &a, hipStream_t st, int part)
 {
@@ -2551,25 +2526,24 @@ static hipError_t launch_chunks(const Args &a, hipStream_t st, int part)
 // [2] after the row pass (before the debug emit), [3] after the side stream's
 // chunk pass (recorded only with the split: one more marker on the caller's
 // stream would add its own gap to the step)
+// One step's launches.  With fp32 top-p rows beside other rows and a side
+// stream from the caller, the other rows' chunk pass and row pass run on the
+// side stream beside the top-p rows' chunk pass and top-p passes; the rows
+// either deferred follow once both are done.  Without a side stream the same
+// kernels run in one stream.  k_rows first writes the launch order the split
+// chunk-pass halves and k_tp_hist read.
 template <int DT>
 static hipError_t launch_dt(const Args &a, float *probs, uint32_t *keep, hipStream_t st, unsigned kinds,
-                            void *const *ev, int nev)
+                            void *const *ev, int nev, const SideStreams *sd)
 {
     hipError_t e;
     if (ev && (e = hipEventRecord((hipEvent_t)ev[0], st)) != hipSuccess) return e;
     const unsigned B = (unsigned)a.L.B;
     const bool tp32 = DT == F32 && (kinds & MIS_KIND_TOPP32);
-    // fp32 top-p rows with other rows beside them: the other rows' chunk pass
-    // and row pass run on the side stream, beside the top-p rows' chunk pass
-    // and k_tp_* passes on the caller's stream; the rows the passes deferred
-    // follow once both are done
-    const bool side = tp32 && (kinds & MIS_KIND_OTHER) != 0;
-    if (tp32) hipLaunchKernelGGL(k_rows, dim3(1), dim3(NT), 0, st, a);  // the launch order the split halves read
-    Side *sd = nullptr;
+    const bool others = (kinds & MIS_KIND_OTHER) != 0u;
+    const bool side = tp32 && others && sd != nullptr;
+    if (tp32) hipLaunchKernelGGL(k_rows, dim3(1), dim3(NT), 0, st, a);
     if (side) {
-        // the other rows' chunk pass and row pass on the side stream, beside
-        // the fp32 top-p rows' chunk pass and top-p passes on the caller's
-        if ((e = side_of_current(&sd)) != hipSuccess) return e;
         if ((e = hipEventRecord(sd->fork, st)) != hipSuccess) return e;
         if ((e = hipStreamWaitEvent(sd->s, sd->fork, 0)) != hipSuccess) return e;
         if ((e = launch_chunks<DT>(a, sd->s, K1_OTHERS)) != hipSuccess) return e;
@@ -2581,9 +2555,9 @@ static hipError_t launch_dt(const Args &a, float *probs, uint32_t *keep, hipStre
     }
     if ((e = launch_chunks<DT>(a, st, side ? K1_TOPP32 : K1_ALL)) != hipSuccess) return e;
     if (ev && (e = hipEventRecord((hipEvent_t)ev[1], st)) != hipSuccess) return e;
-    // without the split: the row pass after the chunk pass, unless the batch
-    // holds fp32 top-p rows only (then k_final's FIN_REST serves the rest)
-    const bool rowpass_here = !side && !(tp32 && (kinds & MIS_KIND_OTHER) == 0u);
+    // the row pass in this stream: unless the side stream runs it, or the
+    // batch holds fp32 top-p rows only (k_final's FIN_REST then serves the rest)
+    const bool rowpass_here = !side && !(tp32 && !others);
     if (rowpass_here) hipLaunchKernelGGL((k_rowpass<DT>), dim3(B), dim3(NTS), 0, st, a);
     if (tp32) {
         const unsigned bg = (unsigned)(a.L.B * a.L.G);
@@ -2592,7 +2566,7 @@ static hipError_t launch_dt(const Args &a, float *probs, uint32_t *keep, hipStre
         hipLaunchKernelGGL(k_tp_final, dim3(B), dim3(NTF), 0, st, a);
         if ((e = hipGetLastError()) != hipSuccess) return e;
         if (side && (e = hipStreamWaitEvent(st, sd->join, 0)) != hipSuccess) return e;
-        const int ph = !side ? FIN_REST : (kinds & MIS_KIND_GENERIC) ? FIN_DEFERRED : FIN_TAIL;
+        const int ph = side ? ((kinds & MIS_KIND_GENERIC) ? FIN_DEFERRED : FIN_TAIL) : rowpass_here ? FIN_TAIL : FIN_REST;
         hipLaunchKernelGGL((k_final<DT>), dim3(B), dim3(NT), 0, st, a, ph);
     } else {
         hipLaunchKernelGGL((k_final<DT>), dim3(B), dim3(NT), 0, st, a, (int)FIN_ALL);

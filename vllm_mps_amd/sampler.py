@@ -121,6 +121,7 @@ class Sampler:
     def __init__(self, generator: torch.Generator | None = None) -> None:
         self.generator = generator
         self._workspace: dict[int, torch.Tensor] = {}
+        self._context: dict[int, _native.Context] = {}
 
     # -- workspace -------------------------------------------------------
     def workspace(self, device: torch.device, B: int, V: int, code: int) -> torch.Tensor:
@@ -134,6 +135,17 @@ class Sampler:
             _native.workspace_init(ws.data_ptr(), ws.numel(), torch.cuda.current_stream(device).cuda_stream)
             self._workspace[idx] = ws
         return ws
+
+    def context(self, device: torch.device) -> _native.Context:
+        """This sampler's side stream on `device` (made once, kept with the
+        sampler, as the engine keeps one Sampler: engine/llm_engine.py:108)."""
+        idx = device.index if device.index is not None else torch.cuda.current_device()
+        ctx = self._context.get(idx)
+        if ctx is None:
+            with torch.cuda.device(idx):
+                ctx = _native.Context()
+            self._context[idx] = ctx
+        return ctx
 
     # -- batched device entry point ---------------------------------------
     def sample_packed(self, logits: torch.Tensor, packed: torch.Tensor, *, out: torch.Tensor | None = None,
@@ -165,9 +177,10 @@ class Sampler:
         stream = torch.cuda.current_stream(dev).cuda_stream
         ptr = lambda t: None if t is None else t.data_ptr()
         evs = None if events is None else tuple(int(e.cuda_event) for e in events)
+        ctx = self.context(dev) if kinds is not None else None
         _native.sample(logits.data_ptr(), code, B, V, logits.stride(0), packed.data_ptr(), out.data_ptr(),
                        ptr(status_out), ptr(probs_out), ptr(keep_out), ws.data_ptr(), ws.numel(), stream, evs,
-                       kinds=kinds)
+                       kinds=kinds, context=ctx)
         return out
 
     def sample_rows(self, logits: torch.Tensor, params: Sequence[SamplingParams],
