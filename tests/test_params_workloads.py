@@ -98,9 +98,11 @@ def test_bench_refuses_multi_gpu():
 
 def test_row_kinds_hint():
     """Host-side row-kind hint: fp32 top-p rows (T > 0, top-k off, top_p < 1)
-    versus every other row; 16-bit batches have no fp32 top-p rows."""
+    versus every other row; 16-bit batches have no fp32 top-p rows; GENERIC
+    marks the others the generic row pass serves (1024 < k' < V, 16-bit
+    top-p without top-k)."""
     import torch
-    from vllm_mps_amd.sampler import KIND_OTHER, KIND_TOPP32, row_kinds
+    from vllm_mps_amd.sampler import KIND_GENERIC, KIND_OTHER, KIND_TOPP32, row_kinds
     V = 100
     assert row_kinds([1.0], [0], [0.9], V, torch.float32) == KIND_TOPP32
     assert row_kinds([1.0], [V], [0.9], V, torch.float32) == KIND_TOPP32      # k >= V is off
@@ -108,5 +110,10 @@ def test_row_kinds_hint():
     assert row_kinds([0.0], [0], [0.9], V, torch.float32) == KIND_OTHER        # greedy
     assert row_kinds([1.0], [0], [1.0], V, torch.float32) == KIND_OTHER        # top-p off
     assert row_kinds([1.0, 0.0], [0, 0], [0.5, 1.0], V, torch.float32) == KIND_TOPP32 | KIND_OTHER
-    assert row_kinds([1.0], [0], [0.9], V, torch.float16) == KIND_OTHER
+    assert row_kinds([1.0], [0], [0.9], V, torch.float16) == KIND_OTHER | KIND_GENERIC
+    assert row_kinds([1.0], [20], [0.9], V, torch.bfloat16) == KIND_OTHER
+    assert row_kinds([1.0], [0], [1.0], V, torch.bfloat16) == KIND_OTHER
+    assert row_kinds([1.0], [50], [1.0], 5000, torch.float32) == KIND_OTHER
+    assert row_kinds([1.0], [2000], [1.0], 5000, torch.float32) == KIND_OTHER | KIND_GENERIC
+    assert row_kinds([0.0], [2000], [0.5], 5000, torch.float16) == KIND_OTHER  # greedy ignores the filters
     assert row_kinds([], [], [], V, torch.float32) == 0
