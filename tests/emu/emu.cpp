@@ -369,6 +369,10 @@ int main(int argc, char **argv)
     fwrite(status, 4, (size_t)B, o);
     if (want) { fwrite(probs, 4, (size_t)(B * V), o); fwrite(keep, 4, (size_t)(B * W), o); }
     fclose(o);
+    if (const char *wo = getenv("EMU_WS_OUT")) {  // the workspace after the call
+        FILE *t = fopen(wo, "wb");
+        if (t) { fwrite(ws, 1, ws_bytes, t); fclose(t); }
+    }
     if (trace_out) {
         FILE *t = fopen(trace_out, "wb");
         if (t) { fwrite((char *)ws + ws_bytes, 1, tr_bytes, t); fclose(t); }

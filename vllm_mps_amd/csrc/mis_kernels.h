@@ -180,10 +180,10 @@ __device__ __forceinline__ Cand ldp_cand(const Cand *p)
     return c;
 }
 // candidates a chunk wrote (its summary says so; never more than the buffer)
-__device__ __forceinline__ uint32_t ncand_of(const ChunkSum *cs)
+__device__ __forceinline__ uint32_t ncand_of(const ChunkSum *cs, int ccap)
 {
     const uint32_t n = ldp(&cs->ncand);
-    return n < (uint32_t)CAND_CAP ? n : (uint32_t)CAND_CAP;
+    return n < (uint32_t)ccap ? n : (uint32_t)ccap;
 }
 
 
@@ -756,7 +756,7 @@ __device__ __forceinline__ bool leader_smallk(Smem &sm, const RowCx &c, const Ro
     uint32_t *pre = reinterpret_cast<uint32_t *>(sm.chs);
     {
         static_assert(G_MAX <= NT, "one chunk per thread");
-        const uint32_t nc = (int)threadIdx.x < c.G ? ncand_of(&cs[threadIdx.x]) : 0u;
+        const uint32_t nc = (int)threadIdx.x < c.G ? ncand_of(&cs[threadIdx.x], a.L.ccap) : 0u;
         uint32_t tot;
         const uint32_t off = block_excl_scan<uint32_t>(nc, sm.red, &tot);
         if ((int)threadIdx.x < c.G) pre[threadIdx.x] = off;
@@ -787,7 +787,7 @@ __device__ __forceinline__ bool leader_smallk(Smem &sm, const RowCx &c, const Ro
             const int mid = (lo + hi + 1) >> 1;
             if (pre[mid] <= f) lo = mid; else hi = mid - 1;
         }
-        return cand + (size_t)lo * CAND_CAP + (f - pre[lo]);
+        return cand + (size_t)lo * a.L.ccap + (f - pre[lo]);
     };
     constexpr int BATCH = 8;  // candidate loads in flight per thread
     // the row's candidates, copied once into LDS when they fit
@@ -1182,7 +1182,7 @@ __device__ __forceinline__ void leader_row(Smem &sm, RowCx &c, const RowPlan &pl
         const double S_row = block_sum<double>(s, sm.red);
         RowPlan pk = pl;
         pk.kk = (int)(c.V < (int64_t)K_PROBE ? c.V : (int64_t)K_PROBE);
-        const Cand *cand = reinterpret_cast<const Cand *>(a.ws + L.cand) + (size_t)row * L.G * CAND_CAP;
+        const Cand *cand = reinterpret_cast<const Cand *>(a.ws + L.cand) + (size_t)row * L.G * L.ccap;
         // S_row sums wexp weights (relative error <= WEXP_REL_ERR each, all
         // positive) in float64; twice that bound covers the float64 sums and
         // the chunk rescales
@@ -1449,9 +1449,9 @@ __global__ __launch_bounds__(NT) void k_sample(Args a, int part)
                     tkey = block_min<uint32_t>(tw, sm.red);
                 } else {
                     // larger nc (few chunks per row): bisect the raw key for
-                    // a threshold with nc <= count <= CAND_CAP
+                    // a threshold with nc <= count <= the chunk's candidate slots
                     uint32_t lo = 0u, hi = key_of_f32(xmax) + 1u, clo = nfin;
-                    while (clo > (uint32_t)CAND_CAP && hi - lo > 1u) {
+                    while (clo > (uint32_t)L.ccap && hi - lo > 1u) {
                         const uint32_t mid = lo + (hi - lo) / 2u;
                         uint32_t c = 0u;
 #pragma unroll
@@ -1474,8 +1474,8 @@ __global__ __launch_bounds__(NT) void k_sample(Args a, int part)
             for (int i = 0; i < EPT; ++i) mine += x[i] >= xlof ? 1u : 0u;
             uint32_t total;
             uint32_t off = block_excl_scan<uint32_t>(mine, sm.red, &total);
-            if (total <= (uint32_t)CAND_CAP) {
-                Cand *cand = reinterpret_cast<Cand *>(a.ws + L.cand) + ((size_t)row * G + chunk) * CAND_CAP;
+            if (total <= (uint32_t)L.ccap) {
+                Cand *cand = reinterpret_cast<Cand *>(a.ws + L.cand) + ((size_t)row * G + chunk) * L.ccap;
 #pragma unroll
                 for (int i = 0; i < EPT; ++i)
                     if (x[i] >= xlof) {
@@ -1616,7 +1616,7 @@ __global__ __launch_bounds__(NTS) void k_rowpass(Args a)
         write_row(ro, a, row, id, id >= 0 ? MIS_ROW_OK : MIS_ROW_INVALID, pl.mode, m, row_key(-INFINITY, DT), -1, SK);
         return;
     }
-    const Cand *cand = reinterpret_cast<const Cand *>(a.ws + L.cand) + (size_t)row * G * CAND_CAP;
+    const Cand *cand = reinterpret_cast<const Cand *>(a.ws + L.cand) + (size_t)row * G * L.ccap;
     trace(a.ws, L, row, 17);
     exp_table(sm.etab, tid);
     // 1. summaries
@@ -1625,7 +1625,7 @@ __global__ __launch_bounds__(NTS) void k_rowpass(Args a)
     if (tid < G) {
         const uint32_t n = ldp(&cs[tid].ncand);
         ovf = n == NCAND_OVERFLOW ? 1u : 0u;
-        nc = n <= (uint32_t)CAND_CAP ? n : 0u;
+        nc = n <= (uint32_t)L.ccap ? n : 0u;
         ntr = ldp(&cs[tid].trunc) != 0u ? 1u : 0u;
         nfin = ldp(&cs[tid].nfin);
         flg = ldp(&cs[tid].flags) != 0u ? 1u : 0u;
@@ -1654,7 +1654,7 @@ __global__ __launch_bounds__(NTS) void k_rowpass(Args a)
     // 2. candidates into LDS, one wave per chunk, eight loads in flight
     for (int g = wave_id(); g < G; g += NW) {
         const uint32_t n = g + 1 < G ? sm.pre[g + 1] - sm.pre[g] : ntot - sm.pre[g];
-        const Cand *cg = cand + (size_t)g * CAND_CAP;
+        const Cand *cg = cand + (size_t)g * L.ccap;
         Cand *dst = sm.cc + sm.pre[g];
         for (uint32_t i0 = 0; i0 < n; i0 += 8 * 64) {
             Cand v[8];

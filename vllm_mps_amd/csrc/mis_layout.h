@@ -13,7 +13,7 @@ constexpr int NT = 256;            // threads per workgroup (4 waves of 64)
 constexpr int NWAVE = NT / 64;
 
 constexpr int K_SMALL = 1024;      // largest k' served by the candidate path
-constexpr int CAND_CAP = 2048;     // candidates one chunk may emit
+constexpr int CAND_CAP = 2048;     // candidates one chunk may emit, at most (Layout::ccap per shape)
 constexpr int SURV_CAP = 1024;     // top-k survivors / top-p window held in LDS
 constexpr int K_PROBE = 512;       // fp16/bf16 top-p rows look for their cut among this many largest values
                                    // first (ties at the last one stay within SURV_CAP)
@@ -104,6 +104,7 @@ static_assert(sizeof(TopRow) % 256 == 0, "TopRow size");
 struct Layout {
     int64_t B, V;
     int ept, G;
+    int ccap;                       // candidate slots per (row, chunk)
     size_t rowout, chunks, rbuf, cand, topc, topr, stash, perm, total;
 };
 
@@ -120,12 +121,22 @@ inline Layout make_layout(int64_t B, int64_t V, int dtype)
     L.ept = EPT_DEFAULT;
     if (chunks(L.ept) > G_MAX) L.ept = 64;
     L.G = (int)chunks(L.ept);
+    // candidate slots per chunk: four times what the chunk pass aims at for
+    // the largest k' the candidate path serves (2 * ceil(K_SMALL / G) + 32,
+    // all K_SMALL when the row is one chunk), plus 64, in multiples of 64.
+    // Measured on the configs the largest chunk emits at most 60 % of this;
+    // a chunk with more overflows to the exact generic path.
+    {
+        const int64_t nc = L.G == 1 ? (int64_t)K_SMALL : 2 * (((int64_t)K_SMALL + L.G - 1) / L.G) + 32;
+        const int64_t c = (4 * nc + 64 + 63) / 64 * 64;
+        L.ccap = (int)(c < (int64_t)CAND_CAP ? c : (int64_t)CAND_CAP);
+    }
     const size_t BG = (size_t)B * L.G;
     size_t off = CTL_PREFIX;
     L.rowout = off; off = align256(off + sizeof(RowOut) * (size_t)B);
     L.chunks = off; off = align256(off + sizeof(ChunkSum) * BG);
     L.rbuf = off;   off = align256(off + (dtype == MIS_DTYPE_F32 ? sizeof(RoundBuf) * BG : 0));
-    L.cand = off;   off = align256(off + sizeof(Cand) * (size_t)CAND_CAP * BG);
+    L.cand = off;   off = align256(off + sizeof(Cand) * (size_t)L.ccap * BG);
     // fp32 top-p: per-chunk fine bins and per-row state of the top-p passes
     const bool f32 = dtype == MIS_DTYPE_F32;
     L.topc = off;   off = align256(off + (f32 ? sizeof(TopChunk) * BG : 0));
