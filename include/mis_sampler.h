@@ -18,10 +18,12 @@
  *
  * All pointers except the workspace size are device pointers.  No exceptions,
  * no host synchronisation and no allocation happen inside mis_sample(),
- * mis_sample_profiled() and mis_sample_ex(); every launch goes on `stream` (a
- * hipStream_t; NULL = the legacy default stream), or on a caller-created
- * side stream (mis_context) that `stream` joins.  The library keeps no
- * process-global state: calls on different streams with their own
+ * mis_sample_profiled(), mis_sample_ex() and mis_sample_noalloc(); every
+ * launch goes on `stream` (a hipStream_t; NULL = the legacy default stream),
+ * or on a caller-created side stream (mis_context) that `stream` joins.  The
+ * library's only process-global state is the static scratch of
+ * mis_sample_noalloc() (one copy per device) and its per-device address:
+ * calls of the other entry points on different streams with their own
  * workspaces (and contexts) may run concurrently.
  */
 #ifndef MIS_SAMPLER_H
@@ -34,7 +36,7 @@
 extern "C" {
 #endif
 
-#define MIS_ABI_VERSION 6
+#define MIS_ABI_VERSION 7
 
 /* logits element type */
 enum { MIS_DTYPE_F32 = 0, MIS_DTYPE_F16 = 1, MIS_DTYPE_BF16 = 2 };
@@ -45,7 +47,9 @@ enum {
     MIS_ERR_INVALID_ARG = 1,   /* null pointer, bad dtype, B < 0, V <= 0, row_stride < V */
     MIS_ERR_WORKSPACE = 2,     /* workspace too small or misaligned */
     MIS_ERR_HIP = 3,           /* a HIP launch failed; see mis_last_hip_error() */
-    MIS_ERR_UNSUPPORTED = 4    /* V or B beyond the supported range */
+    MIS_ERR_UNSUPPORTED = 4,   /* V or B beyond the supported range */
+    MIS_ERR_SCRATCH = 5        /* mis_sample_noalloc(): the shape needs more than
+                                  MIS_SCRATCH_BYTES of scratch */
 };
 
 /* per-row status written to out_status */
@@ -170,6 +174,31 @@ int mis_sample_ex(const void *logits, int dtype, int64_t B, int64_t V, int64_t r
                   const mis_row_params *params, int64_t *out_ids, int32_t *out_status,
                   float *out_probs, uint32_t *out_keep, void *workspace, size_t workspace_bytes,
                   void *stream, unsigned kinds, void *const *events, mis_context *ctx);
+
+/*
+ * Size of the static device scratch behind mis_sample_noalloc(): 96 MiB, one
+ * copy on each device the call runs on, held until the process ends.  It
+ * covers every shape whose mis_workspace_bytes() fits, e.g. B = 256 fp32 rows
+ * or B = 1024 fp16/bf16 rows of V = 128256.
+ */
+#define MIS_SCRATCH_BYTES ((size_t)96 << 20)
+
+/*
+ * mis_sample_ex() without a workspace, events or context, for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  No counterpart in the reference.
+ * Its scratch is a file-scope device array of MIS_SCRATCH_BYTES per device,
+ * whose address the first call on a device looks up; the call allocates
+ * nothing and every launch goes on `stream`.  Returns MIS_ERR_SCRATCH when
+ * mis_workspace_bytes(B, V, dtype) exceeds MIS_SCRATCH_BYTES.  Every call on
+ * a device shares that device's scratch, which keeps the last call's
+ * contents (the kernels write every word they later read, so nothing needs
+ * clearing): calls that overlap in time on one device (other streams, other
+ * threads) race and must be ordered by the caller.
+ */
+int mis_sample_noalloc(const void *logits, int dtype, int64_t B, int64_t V, int64_t row_stride,
+                       const mis_row_params *params, int64_t *out_ids, int32_t *out_status,
+                       float *out_probs, uint32_t *out_keep, void *stream, unsigned kinds);
 
 /* Human-readable text for an API return code. */
 const char *mis_strerror(int code);

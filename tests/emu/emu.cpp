@@ -359,10 +359,14 @@ int main(int argc, char **argv)
         fprintf(stderr, "mis_context_create failed\n");
         return 3;
     }
-    const int rc = mis_sample_ex(logits, dtype, B, V, V, params, ids, status, probs, keep, ws, ws_bytes, nullptr,
-                                 (unsigned)kinds, nullptr, ctx);
+    // EMU_NOALLOC=1: through mis_sample_noalloc (its static scratch, one stream)
+    const bool noalloc = getenv("EMU_NOALLOC") && atoi(getenv("EMU_NOALLOC"));
+    const int rc = noalloc ? mis_sample_noalloc(logits, dtype, B, V, V, params, ids, status, probs, keep, nullptr,
+                                                (unsigned)kinds)
+                           : mis_sample_ex(logits, dtype, B, V, V, params, ids, status, probs, keep, ws, ws_bytes,
+                                           nullptr, (unsigned)kinds, nullptr, ctx);
     mis_context_destroy(ctx);
-    if (rc != MIS_OK) { fprintf(stderr, "mis_sample_ex: %s\n", mis_strerror(rc)); return 3; }
+    if (rc != MIS_OK) { fprintf(stderr, "mis_sample: %s\n", mis_strerror(rc)); return 3; }
     FILE *o = fopen(argv[2], "wb");
     if (!o) { perror("out"); return 2; }
     fwrite(ids, 8, (size_t)B, o);

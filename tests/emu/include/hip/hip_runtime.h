@@ -19,6 +19,7 @@
 
 #define __global__
 #define __device__
+#define __align__(n) __attribute__((aligned(n)))
 #define __host__
 #define __forceinline__ inline
 #define __launch_bounds__(...)
@@ -119,6 +120,9 @@ enum : unsigned { hipStreamNonBlocking = 1u, hipEventDisableTiming = 2u };
 
 inline hipError_t hipGetDevice(int *d) { *d = 0; return hipSuccess; }
 inline hipError_t hipGetLastError() { return hipSuccess; }
+// a __device__ variable is an ordinary host object here: its address is the symbol's
+#define HIP_SYMBOL(x) (&(x))
+inline hipError_t hipGetSymbolAddress(void **p, const void *sym) { *p = const_cast<void *>(sym); return hipSuccess; }
 inline hipError_t hipStreamCreateWithFlags(hipStream_t *s, unsigned) { *s = (hipStream_t)(uintptr_t)0x5151; return hipSuccess; }
 inline hipError_t hipEventCreateWithFlags(hipEvent_t *e, unsigned) { *e = (hipEvent_t)(uintptr_t)0xe7e7; return hipSuccess; }
 inline hipError_t hipEventRecord(hipEvent_t, hipStream_t) { return hipSuccess; }

@@ -22,10 +22,11 @@ MAGIC = 0x4D495345
 
 
 def run(w: W.Workload, debug: bool = True, kinds: int = 7, timeout: float = 600.0, trace: bool = False,
-        side: bool = True) -> dict:
+        side: bool = True, noalloc: bool = False) -> dict:
     """trace=True: also returns the MIS_TRACE phase table (``trace`` [B, 32],
     a logical clock: nonzero where a row passed that phase).  side=True:
-    with a mis_context (the split schedule), else every launch in one stream."""
+    with a mis_context (the split schedule), else every launch in one stream.
+    noalloc=True: through mis_sample_noalloc (the static scratch; one stream)."""
     exe = build_emu.build(trace=trace)
     B, V = w.shape
     params = np.zeros((B, 4), dtype=np.int32)
@@ -44,6 +45,7 @@ def run(w: W.Workload, debug: bool = True, kinds: int = 7, timeout: float = 600.
         env = dict(os.environ, ASAN_OPTIONS="detect_leaks=0:abort_on_error=1:detect_stack_use_after_return=0")
         ctr = os.path.join(td, "trace.bin")
         env["EMU_SIDE"] = "1" if side else "0"
+        env["EMU_NOALLOC"] = "1" if noalloc else "0"
         if trace:
             env["EMU_TRACE_OUT"] = ctr
         res = subprocess.run([exe, cin, cout], capture_output=True, text=True, timeout=timeout, env=env)

@@ -47,9 +47,10 @@ def test_library_exports_every_declared_symbol(lib):
 
 def test_abi_version_and_strings(lib):
     from vllm_mps_amd import _native
-    assert lib.mis_abi_version() == _native.ABI_VERSION == 6
+    assert lib.mis_abi_version() == _native.ABI_VERSION == 7
     assert lib.mis_strerror(0) == b"ok"
     assert b"workspace" in lib.mis_strerror(2)
+    assert b"scratch" in lib.mis_strerror(_native.ERR_SCRATCH)
     assert lib.mis_last_hip_error() == 0
 
 
@@ -90,6 +91,22 @@ def test_argument_validation_without_gpu(lib):
     # a context pointer out of nowhere is never dereferenced before the checks above
     lib.mis_context_create.argtypes = [ctypes.POINTER(vp)]
     assert lib.mis_context_create(None) == 1
+    # the allocation-free entry: the same checks, then the scratch limit, all
+    # before the scratch address is looked up on a device
+    na = lambda *a: lib.mis_sample_noalloc(*a)
+    lib.mis_sample_noalloc.argtypes = [vp, ctypes.c_int, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, vp, vp, vp,
+                                       vp, vp, vp, ctypes.c_uint]
+    assert na(fake, 0, 1, 10, 10, fake, fake, None, None, None, None, 8) == 1
+    assert na(fake, 3, 1, 10, 10, fake, fake, None, None, None, None, 7) == 1
+    assert na(fake, 0, 1, 10, 9, fake, fake, None, None, None, None, 7) == 1
+    assert na(None, 0, 1, 10, 10, fake, fake, None, None, None, None, 7) == 1
+    assert na(fake, 0, 0, 10, 10, fake, fake, None, None, None, None, 7) == 0
+    assert na(fake, 0, 1 << 31, 10, 10, fake, fake, None, None, None, None, 7) == 4
+    from vllm_mps_amd import _native
+    assert lib.mis_workspace_bytes(1024, 128256, 0) > _native.SCRATCH_BYTES
+    assert na(fake, 0, 1024, 128256, 128256, fake, fake, None, None, None, None, 7) == _native.ERR_SCRATCH
+    for B, V, dt in [(256, 128256, 0), (1024, 128256, 1), (1024, 128256, 2), (8, 32000, 0), (1, 152064, 2)]:
+        assert lib.mis_workspace_bytes(B, V, dt) <= _native.SCRATCH_BYTES, (B, V, dt)
 
 
 def test_product_path_fails_loudly_without_library(tmp_path):

@@ -24,9 +24,9 @@ def _emu(w, **kw):
     return runner.run(w, **kw)
 
 
-def _check(name, w, kinds=7, side=True):
+def _check(name, w, kinds=7, side=True, noalloc=False):
     print(f"[emu] {name} dtype={w.dtype} shape={w.shape}", flush=True)
-    g = _emu(w, kinds=kinds, side=side)
+    g = _emu(w, kinds=kinds, side=side, noalloc=noalloc)
     rep = C.compare(w.dtype, H.params_of(w), g, H.run_oracle(w))
     print(f"[emu] {name}: {rep.summary()}", flush=True)
     assert rep.ok, rep.summary()
@@ -76,6 +76,8 @@ def test_emu_mixed_modes(dtype):
         _check(f"mixed kinds={kinds}", w, kinds=kinds)
     _check("mixed one stream", w, side=False)
     _check("mixed one stream kinds=3", w, kinds=3, side=False)
+    # the allocation-free entry point: the static scratch instead of a workspace
+    _check("mixed noalloc", w, noalloc=True)
 
 
 def test_emu_config_c2():

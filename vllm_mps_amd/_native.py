@@ -12,14 +12,16 @@ from . import build as _build
 
 DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
 ROW_OK, ROW_BAD_PARAM, ROW_INVALID, ROW_UNSUPPORTED, ROW_INTERNAL = 0, 1, 2, 3, 4
-ABI_VERSION = 6
+ABI_VERSION = 7
+SCRATCH_BYTES = 96 << 20  # MIS_SCRATCH_BYTES: the static scratch of mis_sample_noalloc
+ERR_SCRATCH = 5  # MIS_ERR_SCRATCH
 KIND_TOPP32 = 1  # MIS_KIND_TOPP32
 KIND_OTHER = 2   # MIS_KIND_OTHER
 KIND_GENERIC = 4  # MIS_KIND_GENERIC
 KIND_ALL = 7     # MIS_KIND_ALL
 
 EXPORTED = ("mis_workspace_bytes", "mis_workspace_init", "mis_sample", "mis_sample_profiled", "mis_sample_ex",
-            "mis_context_create", "mis_context_destroy", "mis_strerror", "mis_last_hip_error", "mis_abi_version")
+            "mis_sample_noalloc", "mis_context_create", "mis_context_destroy", "mis_strerror", "mis_last_hip_error", "mis_abi_version")
 
 _lib = None
 
@@ -55,6 +57,8 @@ def load():
     lib.mis_sample_ex.argtypes = [vp, ctypes.c_int, i64, i64, i64, vp, vp, vp, vp, vp, vp, ctypes.c_size_t, vp,
                                   ctypes.c_uint, vp, vp]
     lib.mis_sample_ex.restype = ctypes.c_int
+    lib.mis_sample_noalloc.argtypes = [vp, ctypes.c_int, i64, i64, i64, vp, vp, vp, vp, vp, vp, ctypes.c_uint]
+    lib.mis_sample_noalloc.restype = ctypes.c_int
     lib.mis_context_create.argtypes = [ctypes.POINTER(vp)]
     lib.mis_context_create.restype = ctypes.c_int
     lib.mis_context_destroy.argtypes = [vp]
@@ -134,3 +138,19 @@ def sample(logits_ptr: int, dtype: int, B: int, V: int, row_stride: int, params_
         if rc == 3:
             msg += f" (hipError {lib.mis_last_hip_error()})"
         raise MisError(f"mis_sample failed: {msg}")
+
+
+def sample_noalloc(logits_ptr: int, dtype: int, B: int, V: int, row_stride: int, params_ptr: int, ids_ptr: int,
+                   status_ptr: int | None, probs_ptr: int | None, keep_ptr: int | None, stream: int,
+                   kinds: int = KIND_ALL) -> None:
+    """mis_sample_noalloc: no workspace; the library's static per-device
+    scratch (SCRATCH_BYTES) serves instead.  Calls that overlap on one device
+    race on it."""
+    lib = load()
+    rc = lib.mis_sample_noalloc(logits_ptr, dtype, B, V, row_stride, params_ptr, ids_ptr, status_ptr, probs_ptr,
+                                keep_ptr, stream, kinds)
+    if rc != 0:
+        msg = lib.mis_strerror(rc).decode()
+        if rc == 3:
+            msg += f" (hipError {lib.mis_last_hip_error()})"
+        raise MisError(f"mis_sample_noalloc failed: {msg}")

@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <mutex>
 #include <new>
 
 #include "mis_launch.h"
@@ -12,6 +13,37 @@
 
 namespace mis {
 static thread_local int g_last_hip = 0;
+}  // namespace mis
+
+// The scratch of mis_sample_noalloc(): one copy per device, loaded with this
+// file's code object and held until the process ends.  On the host the name
+// stands for the host-side shadow, not a device address: device work uses the
+// address hipGetSymbolAddress returns for the current device.
+static __device__ __align__(256) unsigned char scratch[MIS_SCRATCH_BYTES];
+
+namespace mis {
+constexpr int SCRATCH_DEVICES = 64;  // device ordinals the per-device table covers
+static std::once_flag g_scratch_once[SCRATCH_DEVICES];
+static void *g_scratch_ptr[SCRATCH_DEVICES];
+static hipError_t g_scratch_err[SCRATCH_DEVICES];
+
+// The current device's copy of `scratch`, looked up once per device with
+// that device current.
+static int scratch_of_current_device(void **out)
+{
+    int dev = -1;
+    const hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) { g_last_hip = (int)e; return MIS_ERR_HIP; }
+    if (dev < 0 || dev >= SCRATCH_DEVICES) return MIS_ERR_UNSUPPORTED;
+    std::call_once(g_scratch_once[dev], [dev] {
+        void *p = nullptr;
+        g_scratch_err[dev] = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        g_scratch_ptr[dev] = g_scratch_err[dev] == hipSuccess ? p : nullptr;
+    });
+    if (g_scratch_err[dev] != hipSuccess) { g_last_hip = (int)g_scratch_err[dev]; return MIS_ERR_HIP; }
+    *out = g_scratch_ptr[dev];
+    return MIS_OK;
+}
 }  // namespace mis
 
 // A caller's side stream for one device (mis_context_create).
@@ -107,6 +139,23 @@ int mis_sample_ex(const void *logits, int dtype, int64_t B, int64_t V, int64_t r
                        workspace, workspace_bytes, stream, kinds, events, 4, ctx);
 }
 
+int mis_sample_noalloc(const void *logits, int dtype, int64_t B, int64_t V, int64_t row_stride,
+                       const mis_row_params *params, int64_t *out_ids, int32_t *out_status, float *out_probs,
+                       uint32_t *out_keep, void *stream, unsigned kinds)
+{
+    if ((kinds & ~(unsigned)MIS_KIND_ALL) != 0u) return MIS_ERR_INVALID_ARG;
+    if (dtype < 0 || dtype > 2 || B < 0 || V <= 0 || row_stride < V) return MIS_ERR_INVALID_ARG;
+    if (B == 0) return MIS_OK;
+    if (!logits || !params || !out_ids) return MIS_ERR_INVALID_ARG;
+    if (V > (int64_t)1 << 30 || B > 0x7fffffff) return MIS_ERR_UNSUPPORTED;
+    if (mis::make_layout(B, V, dtype).total > MIS_SCRATCH_BYTES) return MIS_ERR_SCRATCH;
+    void *ws = nullptr;
+    const int rc = mis::scratch_of_current_device(&ws);
+    if (rc != MIS_OK) return rc;
+    return sample_impl(logits, dtype, B, V, row_stride, params, out_ids, out_status, out_probs, out_keep, ws,
+                       MIS_SCRATCH_BYTES, stream, kinds, nullptr, 0, nullptr);
+}
+
 int mis_context_create(mis_context **out)
 {
     if (!out) return MIS_ERR_INVALID_ARG;
@@ -145,6 +194,7 @@ const char *mis_strerror(int code)
     case MIS_ERR_WORKSPACE: return "workspace too small or not 256-byte aligned";
     case MIS_ERR_HIP: return "HIP launch failed";
     case MIS_ERR_UNSUPPORTED: return "shape not supported (V > 2^30, B > 2^31 - 1 or more than 256 chunks per row)";
+    case MIS_ERR_SCRATCH: return "shape needs more than the static scratch of mis_sample_noalloc (MIS_SCRATCH_BYTES)";
     default: return "unknown error";
     }
 }
