@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define MIS_ABI_VERSION 7
+#define MIS_ABI_VERSION 8
 
 /* logits element type */
 enum { MIS_DTYPE_F32 = 0, MIS_DTYPE_F16 = 1, MIS_DTYPE_BF16 = 2 };
@@ -199,6 +199,30 @@ int mis_sample_ex(const void *logits, int dtype, int64_t B, int64_t V, int64_t r
 int mis_sample_noalloc(const void *logits, int dtype, int64_t B, int64_t V, int64_t row_stride,
                        const mis_row_params *params, int64_t *out_ids, int32_t *out_status,
                        float *out_probs, uint32_t *out_keep, void *stream, unsigned kinds);
+
+/*
+ * Per-request generator state, 24 bytes, device array [B], for
+ * mis_fill_uniforms(): the key and counter of one draw.
+ *   seed     the generator key (an engine-wide or per-request seed)
+ *   request  the request (sequence) id
+ *   step     which draw of that request (tokens sampled for it so far)
+ */
+typedef struct mis_rng_row {
+    uint64_t seed;
+    uint64_t request;
+    uint64_t step;
+} mis_rng_row;
+
+/*
+ * Writes params[r].uniform for r < B from rng[r]: Philox4x32-10 (Salmon et
+ * al., SC 2011) with key = seed (low word first) and counter = (step low,
+ * step high, request low, request high); u = (first output word >> 8) * 2^-24.
+ * Replaces the global generator torch.multinomial draws from
+ * (model/sampler.py:59): a request's token then depends only on
+ * (seed, request, step) and its logits, not on the batch, the stream or the
+ * order of calls.  One launch on `stream`; no allocation.
+ */
+int mis_fill_uniforms(mis_row_params *params, const mis_rng_row *rng, int64_t B, void *stream);
 
 /* Human-readable text for an API return code. */
 const char *mis_strerror(int code);

@@ -349,3 +349,52 @@ void orc_round_array(int dt, int64_t n, const float *x, float *y)
 {
     for (int64_t j = 0; j < n; ++j) y[j] = orc_rn_dtype(x[j], dt);
 }
+
+/* ------------------------------------------------------------- uniforms
+ *
+ * The per-request uniforms of the device generator: Philox4x32-10 (Salmon,
+ * Moraes, Dror and Shaw, "Parallel random numbers: as easy as 1, 2, 3",
+ * SC 2011), the draw's replacement for torch.multinomial's global generator
+ * (model/sampler.py:59).  Restated from the paper's definition:
+ *   round:  (L0, R0, L1, R1) -> (hi(M1*L1) ^ k0 ^ R0, lo(M1*L1),
+ *                                hi(M0*L0) ^ k1 ^ R1, lo(M0*L0))
+ *   key schedule: k += (0x9E3779B9, 0xBB67AE85) before every round but the
+ *   first; ten rounds.
+ * Pinned by the known-answer vectors the authors publish with Random123.
+ * Uniform: key = seed (low word first), counter = (step lo, step hi,
+ * request lo, request hi); u = (first output word >> 8) / 2^24.
+ */
+static void orc_mulhilo(uint32_t a, uint32_t b, uint32_t *hi, uint32_t *lo)
+{
+    const uint64_t p = (uint64_t)a * (uint64_t)b;
+    *hi = (uint32_t)(p >> 32);
+    *lo = (uint32_t)(p & 0xffffffffu);
+}
+
+void orc_philox4x32_10(const uint32_t in[4], const uint32_t key[2], uint32_t out[4])
+{
+    uint32_t L0 = in[0], R0 = in[1], L1 = in[2], R1 = in[3];
+    uint32_t k0 = key[0], k1 = key[1];
+    for (int round = 0; round < 10; ++round) {
+        uint32_t hi0, lo0, hi1, lo1;
+        orc_mulhilo(0xD2511F53u, L0, &hi0, &lo0);
+        orc_mulhilo(0xCD9E8D57u, L1, &hi1, &lo1);
+        const uint32_t a = hi1 ^ k0 ^ R0, b = lo1, c = hi0 ^ k1 ^ R1, d = lo0;
+        L0 = a; R0 = b; L1 = c; R1 = d;
+        k0 += 0x9E3779B9u;
+        k1 += 0xBB67AE85u;
+    }
+    out[0] = L0; out[1] = R0; out[2] = L1; out[3] = R1;
+}
+
+void orc_uniforms(int64_t n, const uint64_t *seed, const uint64_t *request, const uint64_t *step, float *u)
+{
+    for (int64_t i = 0; i < n; ++i) {
+        const uint32_t ctr[4] = {(uint32_t)step[i], (uint32_t)(step[i] >> 32), (uint32_t)request[i],
+                                 (uint32_t)(request[i] >> 32)};
+        const uint32_t key[2] = {(uint32_t)seed[i], (uint32_t)(seed[i] >> 32)};
+        uint32_t out[4];
+        orc_philox4x32_10(ctr, key, out);
+        u[i] = (float)ldexp((double)(out[0] >> 8), -24);
+    }
+}

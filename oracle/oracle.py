@@ -40,6 +40,8 @@ def _load():
     lib.orc_f32_to_f16.restype = ctypes.c_uint16
     lib.orc_f32_to_bf16.argtypes = [ctypes.c_float]
     lib.orc_f32_to_bf16.restype = ctypes.c_uint16
+    lib.orc_philox4x32_10.argtypes = [p, p, p]
+    lib.orc_uniforms.argtypes = [i64, p, p, p, p]
     _lib = lib
     return lib
 
@@ -120,3 +122,20 @@ def round_to(x: np.ndarray, dtype: str) -> np.ndarray:
     lib.orc_round_array(DTYPE_CODES[dtype], x.shape[0], x.ctypes.data_as(ctypes.c_void_p),
                         y.ctypes.data_as(ctypes.c_void_p))
     return y
+
+
+def philox4x32_10(counter, key) -> np.ndarray:
+    """Philox4x32-10 of one 128-bit counter (4 words) under a 64-bit key (2 words)."""
+    c = np.ascontiguousarray(counter, dtype=np.uint32)
+    k = np.ascontiguousarray(key, dtype=np.uint32)
+    out = np.zeros(4, dtype=np.uint32)
+    _load().orc_philox4x32_10(c.ctypes.data, k.ctypes.data, out.ctypes.data)
+    return out
+
+
+def uniforms(seed, request, step) -> np.ndarray:
+    """Per-request uniforms of the device generator (broadcast uint64 arrays)."""
+    s, r, t = (np.ascontiguousarray(a, dtype=np.uint64) for a in np.broadcast_arrays(seed, request, step))
+    out = np.zeros(s.shape, dtype=np.float32)
+    _load().orc_uniforms(s.size, s.ctypes.data, r.ctypes.data, t.ctypes.data, out.ctypes.data)
+    return out

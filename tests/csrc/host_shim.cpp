@@ -20,6 +20,17 @@ void shim_dexp_array(const double *d, double *out, int64_t n)
     for (int64_t i = 0; i < n; ++i) out[i] = mis::dexp(d[i], tab);
 }
 float shim_div_rcp(float x, float T) { return mis::div_rcp(x, T, 1.0f / T); }
+// the device generator's uniforms for n (seed, request, step) triples
+void shim_philox_uniforms(int64_t n, const uint64_t *seed, const uint64_t *request, const uint64_t *step, float *u)
+{
+    for (int64_t i = 0; i < n; ++i) u[i] = mis::philox_uniform(seed[i], request[i], step[i]);
+}
+void shim_philox4x32_10(const uint32_t *in, const uint32_t *key, uint32_t *out)
+{
+    uint32_t c[4] = {in[0], in[1], in[2], in[3]};
+    mis::philox4x32_10(c, key[0], key[1]);
+    for (int i = 0; i < 4; ++i) out[i] = c[i];
+}
 // bit patterns [lo, hi) of x (step `stride`): mismatches of div_rcp against
 // IEEE x / T, the first one in *first (NaN quotients compare as NaN)
 uint64_t shim_div_rcp_sweep(float T, uint64_t lo, uint64_t hi, uint64_t stride, uint32_t *first)

@@ -19,7 +19,7 @@ CSRC = os.path.join(ROOT, "vllm_mps_amd", "csrc")
 OUT_DIR = os.path.join(HERE, "_build")
 EXE = os.path.join(OUT_DIR, "emu_driver")
 EXE_TRACE = os.path.join(OUT_DIR, "emu_driver_trace")
-UNITS = ["mis_api.hip", "mis_f32.hip", "mis_f16.hip", "mis_bf16.hip"]
+UNITS = ["mis_api.hip", "mis_f32.hip", "mis_f16.hip", "mis_bf16.hip", "mis_rng.hip"]
 
 
 def clangxx() -> str:

@@ -47,7 +47,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 def test_abi_version_and_strings(lib):
     from vllm_mps_amd import _native
-    assert lib.mis_abi_version() == _native.ABI_VERSION == 7
+    assert lib.mis_abi_version() == _native.ABI_VERSION == 8
     assert lib.mis_strerror(0) == b"ok"
     assert b"workspace" in lib.mis_strerror(2)
     assert b"scratch" in lib.mis_strerror(_native.ERR_SCRATCH)
@@ -107,6 +107,13 @@ def test_argument_validation_without_gpu(lib):
     assert na(fake, 0, 1024, 128256, 128256, fake, fake, None, None, None, None, 7) == _native.ERR_SCRATCH
     for B, V, dt in [(256, 128256, 0), (1024, 128256, 1), (1024, 128256, 2), (8, 32000, 0), (1, 152064, 2)]:
         assert lib.mis_workspace_bytes(B, V, dt) <= _native.SCRATCH_BYTES, (B, V, dt)
+    # the generator fill: negative or empty batches and null buffers, before any launch
+    lib.mis_fill_uniforms.argtypes = [vp, vp, ctypes.c_int64, vp]
+    assert lib.mis_fill_uniforms(fake, fake, -1, None) == 1
+    assert lib.mis_fill_uniforms(fake, fake, 0, None) == 0
+    assert lib.mis_fill_uniforms(None, fake, 4, None) == 1
+    assert lib.mis_fill_uniforms(fake, None, 4, None) == 1
+    assert lib.mis_fill_uniforms(fake, fake, 1 << 31, None) == 4
 
 
 def test_product_path_fails_loudly_without_library(tmp_path):

@@ -36,6 +36,9 @@ def shim(tmp_path_factory):
     L.shim_div_rcp.argtypes = [f, f]; L.shim_div_rcp.restype = f
     L.shim_div_rcp_sweep.argtypes = [f, u64, u64, u64, ctypes.POINTER(ctypes.c_uint32)]
     L.shim_div_rcp_sweep.restype = u64
+    L.shim_philox_uniforms.argtypes = [ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                       ctypes.c_void_p]
+    L.shim_philox4x32_10.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
     return L
 
 
@@ -181,3 +184,36 @@ def test_div_rcp_every_binade_strided(shim):
     for T in (0.8, 1.2345678):
         bad = shim.shim_div_rcp_sweep(ctypes.c_float(T), 0, 1 << 32, 7, ctypes.byref(first))
         assert bad == 0, (T, bad, hex(first.value))
+
+
+# Philox4x32-10 known answers published with the authors' Random123 library
+# (counter words, key words, output words)
+PHILOX_KAT = [
+    ([0, 0, 0, 0], [0, 0], [0x6627E8D5, 0xE169C58D, 0xBC57AC4C, 0x9B00DBD8]),
+    ([0xFFFFFFFF] * 4, [0xFFFFFFFF] * 2, [0x408F276D, 0x41C83B0E, 0xA20BC7C6, 0x6D5451FD]),
+    ([0x243F6A88, 0x85A308D3, 0x13198A2E, 0x03707344], [0xA4093822, 0x299F31D0],
+     [0xD16CFE09, 0x94FDCCEB, 0x5001E420, 0x24126EA1]),
+]
+
+
+def test_device_philox_known_answers(shim):
+    for ctr, key, want in PHILOX_KAT:
+        c, k = np.array(ctr, np.uint32), np.array(key, np.uint32)
+        out = np.zeros(4, np.uint32)
+        shim.shim_philox4x32_10(c.ctypes.data, k.ctypes.data, out.ctypes.data)
+        assert out.tolist() == want
+
+
+def test_device_uniforms_match_oracle(shim):
+    """The kernels' uniform (mis_common.h) against the oracle's restatement,
+    bit for bit, over triples that set every word of the key and counter."""
+    from oracle import oracle as O
+    rng = np.random.default_rng(11)
+    n = 20000
+    seed, req, step = (rng.integers(0, 2**64 - 1, n, dtype=np.uint64, endpoint=True) for _ in range(3))
+    step[:100] = np.arange(100, dtype=np.uint64)  # small counters, as a new request has
+    req[100:200] = 0
+    got = np.zeros(n, np.float32)
+    shim.shim_philox_uniforms(n, seed.ctypes.data, req.ctypes.data, step.ctypes.data, got.ctypes.data)
+    want = O.uniforms(seed, req, step)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))

@@ -13,6 +13,9 @@ against something that fixes it independently:
 * draw            searchsorted on a float64 CDF; chi-square frequencies
 * invariants      monotone in top_p, top-p mask within the top-k mask, rank 0
                   always kept, T = 0 ignores top_k/top_p
+* uniforms        Philox4x32-10 known-answer vectors (Random123), the
+                  (seed, request, step) -> (key, counter) wiring, and
+                  distribution checks (Kolmogorov-Smirnov, lag correlation)
 * golden          committed fixtures (tests/golden) and workload digests
 """
 from __future__ import annotations
@@ -325,3 +328,49 @@ def test_golden_rows_c3_c4():
             assert int(r["n_kept"][b]) == exp["n_kept"], (name, b)
             sha = hashlib.sha1(np.packbits(r["keep"][b].astype(np.uint8)).tobytes()).hexdigest()
             assert sha == exp["keep_sha1"], (name, b)
+
+
+# Philox4x32-10 known answers published with the authors' Random123 library
+PHILOX_KAT = [
+    ([0, 0, 0, 0], [0, 0], [0x6627E8D5, 0xE169C58D, 0xBC57AC4C, 0x9B00DBD8]),
+    ([0xFFFFFFFF] * 4, [0xFFFFFFFF] * 2, [0x408F276D, 0x41C83B0E, 0xA20BC7C6, 0x6D5451FD]),
+    ([0x243F6A88, 0x85A308D3, 0x13198A2E, 0x03707344], [0xA4093822, 0x299F31D0],
+     [0xD16CFE09, 0x94FDCCEB, 0x5001E420, 0x24126EA1]),
+]
+
+
+def test_philox_known_answers():
+    for ctr, key, want in PHILOX_KAT:
+        assert O.philox4x32_10(ctr, key).tolist() == want
+
+
+def test_uniform_wiring():
+    """u(seed, request, step) is the first Philox word of counter (step lo,
+    step hi, request lo, request hi) under key (seed lo, seed hi), top 24
+    bits over 2^24: a swapped field or word order fails here."""
+    cases = [(0, 0, 0), (1, 2, 3), (2**64 - 1, 2**63 + 5, 2**40 + 7), (0x0123456789ABCDEF, 9, 2**32)]
+    for seed, req, step in cases:
+        ctr = [step & 0xFFFFFFFF, step >> 32, req & 0xFFFFFFFF, req >> 32]
+        key = [seed & 0xFFFFFFFF, seed >> 32]
+        w = int(O.philox4x32_10(ctr, key)[0])
+        u = O.uniforms(np.uint64(seed), np.uint64(req), np.uint64(step))
+        assert float(u) == (w >> 8) / 2.0**24
+    # the fields are not interchangeable
+    a = O.uniforms(np.uint64(1), np.uint64(2), np.uint64(3))
+    assert a != O.uniforms(np.uint64(1), np.uint64(3), np.uint64(2))
+    assert a != O.uniforms(np.uint64(2), np.uint64(1), np.uint64(3))
+
+
+def test_uniform_distribution():
+    """Uniform on [0, 1) across requests and across steps, with no lag-1
+    correlation along a request's steps."""
+    from scipy import stats
+    n = 200000
+    by_req = O.uniforms(np.uint64(42), np.arange(n, dtype=np.uint64), np.uint64(0))
+    by_step = O.uniforms(np.uint64(42), np.uint64(7), np.arange(n, dtype=np.uint64))
+    for u in (by_req, by_step):
+        assert u.min() >= 0.0 and u.max() < 1.0
+        assert stats.kstest(u, "uniform").pvalue > 1e-4
+        assert abs(np.corrcoef(u[:-1], u[1:])[0, 1]) < 0.01
+    # 24-bit values: repeats only at the birthday rate (n^2 / 2^25 ~ 1200)
+    assert n - np.unique(by_req).size < 2000

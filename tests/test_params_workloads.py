@@ -117,3 +117,33 @@ def test_row_kinds_hint():
     assert row_kinds([1.0], [2000], [1.0], 5000, torch.float32) == KIND_OTHER | KIND_GENERIC
     assert row_kinds([0.0], [2000], [0.5], 5000, torch.float16) == KIND_OTHER  # greedy ignores the filters
     assert row_kinds([], [], [], V, torch.float32) == 0
+
+
+def test_rng_rows_records():
+    from vllm_mps_amd.sampler import rng_rows
+    r = rng_rows(3, 7, [10, 11, 12], 0)
+    assert r.dtype == np.uint64 and r.shape == (3, 3)
+    assert r[:, 0].tolist() == [7, 7, 7] and r[:, 1].tolist() == [10, 11, 12] and r[:, 2].tolist() == [0, 0, 0]
+    big = rng_rows(1, 2**64 - 1, 2**63, 2**40)
+    assert big.tolist() == [[2**64 - 1, 2**63, 2**40]]
+    with pytest.raises(ValueError):
+        rng_rows(2, 0, [1, 2, 3], 0)      # wrong length
+    with pytest.raises(ValueError):
+        rng_rows(1, -1, 0, 0)             # negative
+    with pytest.raises(ValueError):
+        rng_rows(1, 0, 2**64, 0)          # beyond 64 bits
+
+
+def test_step_sampler_checks_without_gpu():
+    import torch
+    from vllm_mps_amd import StepSampler, SamplingParams
+    s = StepSampler(seed=5)
+    assert s.sample_step(torch.zeros((0, 10)), [], {}) == []
+    with pytest.raises(ValueError):
+        s.sample_step(torch.zeros((2, 10)), [1], {})            # rows != ids
+    with pytest.raises(ValueError):
+        s.sample_step(torch.zeros((2, 10)), [4, 4], {})         # duplicate id
+    with pytest.raises(ValueError):
+        StepSampler(seed=-1)
+    assert s.step_of(3) == 0
+    s.release(3)  # unknown ids are fine

@@ -7,5 +7,6 @@ hand-written HIP kernels for gfx950 behind the C ABI in
 """
 from .sampling_params import SamplingParams
 from .sampler import Sampler, pack_params
+from .engine_step import StepSampler
 
-__all__ = ["Sampler", "SamplingParams", "pack_params"]
+__all__ = ["Sampler", "SamplingParams", "StepSampler", "pack_params"]

@@ -12,7 +12,7 @@ from . import build as _build
 
 DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
 ROW_OK, ROW_BAD_PARAM, ROW_INVALID, ROW_UNSUPPORTED, ROW_INTERNAL = 0, 1, 2, 3, 4
-ABI_VERSION = 7
+ABI_VERSION = 8
 SCRATCH_BYTES = 96 << 20  # MIS_SCRATCH_BYTES: the static scratch of mis_sample_noalloc
 ERR_SCRATCH = 5  # MIS_ERR_SCRATCH
 KIND_TOPP32 = 1  # MIS_KIND_TOPP32
@@ -21,7 +21,7 @@ KIND_GENERIC = 4  # MIS_KIND_GENERIC
 KIND_ALL = 7     # MIS_KIND_ALL
 
 EXPORTED = ("mis_workspace_bytes", "mis_workspace_init", "mis_sample", "mis_sample_profiled", "mis_sample_ex",
-            "mis_sample_noalloc", "mis_context_create", "mis_context_destroy", "mis_strerror", "mis_last_hip_error", "mis_abi_version")
+            "mis_sample_noalloc", "mis_fill_uniforms", "mis_context_create", "mis_context_destroy", "mis_strerror", "mis_last_hip_error", "mis_abi_version")
 
 _lib = None
 
@@ -59,6 +59,8 @@ def load():
     lib.mis_sample_ex.restype = ctypes.c_int
     lib.mis_sample_noalloc.argtypes = [vp, ctypes.c_int, i64, i64, i64, vp, vp, vp, vp, vp, vp, ctypes.c_uint]
     lib.mis_sample_noalloc.restype = ctypes.c_int
+    lib.mis_fill_uniforms.argtypes = [vp, vp, i64, vp]
+    lib.mis_fill_uniforms.restype = ctypes.c_int
     lib.mis_context_create.argtypes = [ctypes.POINTER(vp)]
     lib.mis_context_create.restype = ctypes.c_int
     lib.mis_context_destroy.argtypes = [vp]
@@ -83,6 +85,18 @@ def workspace_init(ws_ptr: int, ws_bytes: int, stream: int) -> None:
     rc = lib.mis_workspace_init(ws_ptr, ws_bytes, stream)
     if rc != 0:
         raise MisError(f"mis_workspace_init failed: {lib.mis_strerror(rc).decode()}")
+
+
+def fill_uniforms(params_ptr: int, rng_ptr: int, B: int, stream: int) -> None:
+    """mis_fill_uniforms: params[r].uniform from the device generator state
+    rng[r] = (seed, request, step), 24 bytes a row."""
+    lib = load()
+    rc = lib.mis_fill_uniforms(params_ptr, rng_ptr, B, stream)
+    if rc != 0:
+        msg = lib.mis_strerror(rc).decode()
+        if rc == 3:
+            msg += f" (hipError {lib.mis_last_hip_error()})"
+        raise MisError(f"mis_fill_uniforms failed: {msg}")
 
 
 class Context:

@@ -156,6 +156,17 @@ int mis_sample_noalloc(const void *logits, int dtype, int64_t B, int64_t V, int6
                        MIS_SCRATCH_BYTES, stream, kinds, nullptr, 0, nullptr);
 }
 
+int mis_fill_uniforms(mis_row_params *params, const mis_rng_row *rng, int64_t B, void *stream)
+{
+    if (B < 0) return MIS_ERR_INVALID_ARG;
+    if (B == 0) return MIS_OK;
+    if (!params || !rng) return MIS_ERR_INVALID_ARG;
+    if (B > 0x7fffffff) return MIS_ERR_UNSUPPORTED;
+    const hipError_t e = mis::launch_uniforms(params, rng, B, (hipStream_t)stream);
+    if (e != hipSuccess) { mis::g_last_hip = (int)e; return MIS_ERR_HIP; }
+    return MIS_OK;
+}
+
 int mis_context_create(mis_context **out)
 {
     if (!out) return MIS_ERR_INVALID_ARG;

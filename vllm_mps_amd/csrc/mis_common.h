@@ -272,4 +272,35 @@ MIS_HD double dexp(double d, const double *tab)
     return ldexp(tab[ni & (ETAB_N - 1)] * p, ni >> 6);
 }
 
+// ---------------------------------------------------------------- Philox RNG
+//
+// Philox4x32-10, the counter-based generator of Salmon, Moraes, Dror and Shaw,
+// "Parallel random numbers: as easy as 1, 2, 3" (SC 2011): ten rounds of two
+// 32x32->64-bit multiplies over a 128-bit counter, the 64-bit key advanced by
+// the Weyl constants between rounds.  A function of (counter, key) alone, so
+// any thread computes any request's draw without shared state.
+
+constexpr uint32_t PHILOX_M0 = 0xD2511F53u, PHILOX_M1 = 0xCD9E8D57u;  // round multipliers
+constexpr uint32_t PHILOX_W0 = 0x9E3779B9u, PHILOX_W1 = 0xBB67AE85u;  // key increments
+
+MIS_HD void philox4x32_10(uint32_t c[4], uint32_t k0, uint32_t k1)
+{
+    for (int r = 0; r < 10; ++r) {
+        if (r > 0) { k0 += PHILOX_W0; k1 += PHILOX_W1; }
+        const uint64_t p0 = (uint64_t)PHILOX_M0 * c[0], p1 = (uint64_t)PHILOX_M1 * c[2];
+        const uint32_t n0 = (uint32_t)(p1 >> 32) ^ c[1] ^ k0, n2 = (uint32_t)(p0 >> 32) ^ c[3] ^ k1;
+        c[0] = n0; c[1] = (uint32_t)p1; c[2] = n2; c[3] = (uint32_t)p0;
+    }
+}
+
+// The uniform of one draw: key = seed, counter = (step, request) as
+// little-endian 32-bit words; the top 24 bits of the first output word give
+// u = n * 2^-24 in [0, 1), exact in float.
+MIS_HD float philox_uniform(uint64_t seed, uint64_t request, uint64_t step)
+{
+    uint32_t c[4] = {(uint32_t)step, (uint32_t)(step >> 32), (uint32_t)request, (uint32_t)(request >> 32)};
+    philox4x32_10(c, (uint32_t)seed, (uint32_t)(seed >> 32));
+    return (float)(c[0] >> 8) * 5.9604644775390625e-08f;
+}
+
 }  // namespace mis

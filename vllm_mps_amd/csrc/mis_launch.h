@@ -5,6 +5,7 @@
 #include <hip/hip_runtime.h>
 
 #include "mis_layout.h"
+#include "mis_sampler.h"
 
 namespace mis {
 
@@ -24,5 +25,8 @@ hipError_t launch_f16(const Args &a, float *probs, uint32_t *keep, hipStream_t s
                       void *const *ev, int nev, const SideStreams *side);
 hipError_t launch_bf16(const Args &a, float *probs, uint32_t *keep, hipStream_t st, unsigned kinds,
                        void *const *ev, int nev, const SideStreams *side);
+
+// Fills params[r].uniform from rng[r] for r < B (mis_rng.hip).
+hipError_t launch_uniforms(mis_row_params *params, const mis_rng_row *rng, int64_t B, hipStream_t st);
 
 }  // namespace mis

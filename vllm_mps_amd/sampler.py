@@ -10,13 +10,14 @@ Mirrors the reference's ``Sampler`` (``model/sampler.py:11-79``):
 and adds the batched entry point the engine's per-row loop
 (``engine/llm_engine.py:339-345``) collapses into:
 
-* ``sample_rows(logits[B, V], params_per_row, uniforms=None) -> int64[B]`` on
-  the device, one launch sequence and no host synchronisation.
+* ``sample_rows(logits[B, V], params_per_row, uniforms=None, rng=None) ->
+  int64[B]`` on the device, one launch sequence and no host synchronisation.
 
 Differences from the reference, all contract decisions:
 * the draw is an inverse CDF in vocabulary order from one uniform per row
   instead of ``torch.multinomial``; uniforms come from ``torch.rand`` on the
-  device (``generator`` selects the stream) unless the caller passes them;
+  device (``generator`` selects the stream) unless the caller passes them or
+  asks for the per-request device generator (``rng``);
 * top-p ties at the cut keep the lowest indices first (stable order);
 * fp32 top-p masses are exact softmax masses, not torch's float softmax.
 
@@ -69,6 +70,22 @@ def host_row_params(params: Sequence[SamplingParams], dtype: torch.dtype) -> np.
         if p < 1.0 and p32 == np.float32(1.0) and dtype != torch.float32:
             p32 = np.float32(_ONE_BELOW)
         f[i, 2] = p32
+    return out
+
+
+def rng_rows(B: int, seed, requests, steps) -> np.ndarray:
+    """[B, 3] uint64 ``mis_rng_row`` records (seed, request, step); each
+    argument is a scalar or a length-B sequence of non-negative integers
+    below 2^64."""
+    out = np.zeros((B, 3), dtype=np.uint64)
+    for j, v in enumerate((seed, requests, steps)):
+        a = np.asarray(v, dtype=object).reshape(-1) if not np.isscalar(v) else np.array([v], dtype=object)
+        if a.size not in (1, B):
+            raise ValueError(f"generator state needs 1 or {B} values, got {a.size}")
+        for x in a:
+            if not 0 <= int(x) < 1 << 64:
+                raise ValueError(f"generator state value {x} outside [0, 2^64)")
+        out[:, j] = np.array([int(x) for x in a], dtype=np.uint64)
     return out
 
 
@@ -184,8 +201,14 @@ class Sampler:
         return out
 
     def sample_rows(self, logits: torch.Tensor, params: Sequence[SamplingParams],
-                    uniforms: torch.Tensor | None = None, **buffers) -> torch.Tensor:
-        """Per-row params, device int64[B] token ids (-1 where a row is invalid)."""
+                    uniforms: torch.Tensor | None = None, rng=None, **buffers) -> torch.Tensor:
+        """Per-row params, device int64[B] token ids (-1 where a row is invalid).
+
+        The draw's uniforms: ``uniforms`` when given; else, with ``rng =
+        (seed, requests, steps)`` (scalars or length-B integer sequences),
+        the per-request device generator (``mis_fill_uniforms``: a row's
+        uniform depends only on its seed, request and step); else
+        ``torch.rand`` with this sampler's ``generator``."""
         B = logits.shape[0]
         if len(params) != B:
             raise ValueError(f"{len(params)} SamplingParams for {B} rows")
@@ -196,13 +219,19 @@ class Sampler:
         host = torch.from_numpy(hp)
         hf = hp.view(np.float32)
         buffers.setdefault("kinds", row_kinds(hf[:, 0], hp[:, 1], hf[:, 2], logits.shape[1], logits.dtype))
-        if uniforms is None:
+        if uniforms is None and rng is None:
             uniforms = torch.rand(B, device=dev, dtype=torch.float32, generator=self.generator)
         packed = torch.empty((B, 4), dtype=torch.int32, device=dev)
         # staged through pinned host memory: the copy is queued on the stream
         # and the host does not wait for the device
         packed[:, :3].copy_(host.pin_memory(), non_blocking=True)
-        packed[:, 3].copy_(uniforms.to(device=dev, dtype=torch.float32).view(torch.int32))
+        if uniforms is not None:
+            packed[:, 3].copy_(uniforms.to(device=dev, dtype=torch.float32).view(torch.int32))
+        elif B > 0:
+            state = torch.from_numpy(rng_rows(B, *rng).view(np.int64)).pin_memory()
+            dstate = torch.empty((B, 3), dtype=torch.int64, device=dev)
+            dstate.copy_(state, non_blocking=True)
+            _native.fill_uniforms(packed.data_ptr(), dstate.data_ptr(), B, torch.cuda.current_stream(dev).cuda_stream)
         return self.sample_packed(logits, packed, **buffers)
 
     # -- reference call surface -------------------------------------------
