@@ -176,12 +176,12 @@ int mis_sample_ex(const void *logits, int dtype, int64_t B, int64_t V, int64_t r
                   void *stream, unsigned kinds, void *const *events, mis_context *ctx);
 
 /*
- * Size of the static device scratch behind mis_sample_noalloc(): 96 MiB, one
+ * Size of the static device scratch behind mis_sample_noalloc(): 128 MiB, one
  * copy on each device the call runs on, held until the process ends.  It
  * covers every shape whose mis_workspace_bytes() fits, e.g. B = 256 fp32 rows
  * or B = 1024 fp16/bf16 rows of V = 128256.
  */
-#define MIS_SCRATCH_BYTES ((size_t)96 << 20)
+#define MIS_SCRATCH_BYTES ((size_t)128 << 20)
 
 /*
  * mis_sample_ex() without a workspace, events or context, for callers that

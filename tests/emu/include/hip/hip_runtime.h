@@ -106,6 +106,8 @@ inline int __popc(unsigned v) { return __builtin_popcount(v); }
 
 // Lanes run one at a time, so atomics are plain read-modify-writes.
 template <class T, class U> inline T atomicAdd(T *p, U v) { T o = *p; *p = (T)(o + (T)v); return o; }
+// workgroups run one after another here: device-scope fences have nothing to order
+#define __threadfence() ((void)0)
 template <class T, class U> inline T atomicMin(T *p, U v) { T o = *p; if ((T)v < o) *p = (T)v; return o; }
 template <class T, class U> inline T atomicMax(T *p, U v) { T o = *p; if ((T)v > o) *p = (T)v; return o; }
 template <class T, class U> inline T atomicOr(T *p, U v) { T o = *p; *p = (T)(o | (T)v); return o; }

@@ -95,3 +95,44 @@ def test_emu_fp32_topp_passes():
     g = _emu(w, kinds=2)  # wrong hint: every row on the generic paths, same results
     rep = C.compare(w.dtype, H.params_of(w), g, H.run_oracle(w))
     assert rep.ok, rep.summary()
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+def test_emu_t16_ties_across_chunks(dtype):
+    """16-bit top-p rows whose logits take a few dozen values, each held by
+    thousands of elements over many chunks: the cut falls inside a run that
+    spans chunks (the tie index resolved in one chunk, or at a chunk's end)."""
+    from vllm_mps_amd import workloads as W
+    B, V = 6, 60000
+    rng = np.random.default_rng(21)
+    x = np.round(rng.normal(0.0, 1.0, (B, V)) * 4.0) / 4.0
+    w = W.Workload("ties", dtype, W.to_dtype_bits(x, dtype), np.full(B, 1.0, np.float32),
+                   np.zeros(B, np.int32), np.array([0.3, 0.5, 0.7, 0.9, 0.95, 0.99], np.float32),
+                   rng.random(B, dtype=np.float32))
+    _check("t16 ties", w)
+
+
+def test_emu_t16_wide_key_range_defers():
+    """fp16 values spread over more binades than the key histogram holds,
+    with nearly equal masses: the cut lies under the histogram's range and
+    the generic path serves the row, with the same results."""
+    from vllm_mps_amd import workloads as W
+    B, V = 3, 20000
+    rng = np.random.default_rng(22)
+    x = np.exp2(rng.uniform(-14.0, -6.0, (B, V)))
+    w = W.Workload("wide", "f16", W.to_dtype_bits(x, "f16"), np.full(B, 1.0, np.float32), np.zeros(B, np.int32),
+                   np.array([0.9, 0.5, 0.999], np.float32), rng.random(B, dtype=np.float32))
+    _check("t16 wide range", w)
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+def test_emu_topp16_both_paths(dtype):
+    """The same 16-bit top-p rows in a batch of 256 rows (each row one
+    workgroup: the K_PROBE probe, then the generic path) and in a batch of 64
+    (the t16 passes): both give the oracle's results."""
+    B, V = 256, 3000
+    rng = np.random.default_rng(23)
+    p = rng.choice([0.01, 0.3, 0.9, 0.99], B).astype(np.float32)
+    w = H.synthetic(dtype, B, V, seed=24, temperature=rng.uniform(0.5, 1.5, B).astype(np.float32), top_k=0, top_p=p)
+    _check("topp16 B=256", w)
+    _check("topp16 B=64", w.rows(np.arange(64)))

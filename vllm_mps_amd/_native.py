@@ -13,7 +13,7 @@ from . import build as _build
 DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
 ROW_OK, ROW_BAD_PARAM, ROW_INVALID, ROW_UNSUPPORTED, ROW_INTERNAL = 0, 1, 2, 3, 4
 ABI_VERSION = 8
-SCRATCH_BYTES = 96 << 20  # MIS_SCRATCH_BYTES: the static scratch of mis_sample_noalloc
+SCRATCH_BYTES = 128 << 20  # MIS_SCRATCH_BYTES: the static scratch of mis_sample_noalloc
 ERR_SCRATCH = 5  # MIS_ERR_SCRATCH
 KIND_TOPP32 = 1  # MIS_KIND_TOPP32
 KIND_OTHER = 2   # MIS_KIND_OTHER

@@ -484,6 +484,224 @@ __device__ __forceinline__ bool chain_walk(const uint32_t *rcnt, const float *rp
     return false;
 }
 
+// chain_walk's result computed by one wave (all 64 lanes call it with the
+// same arguments and receive the same result), 64 runs at a time.
+//
+// Inside one binade of F (ulp u), F + p rounds to F + q*u or F + (q+1)*u with
+// q = floor(p / u): a run of n equal p adds a fixed number of ulps per step,
+// except when p / u - q is exactly 1/2, where the first step rounds to even
+// and so depends on the parity of F / u (every later step then starts even).
+// A run is therefore a map parity -> (ulps added, parity after); composing
+// such maps is associative, so a wave's inclusive scan gives F after each of
+// its 64 runs at once, valid up to the first run whose steps would leave the
+// binade.  That run takes its in-binade steps in closed form and the
+// crossing step as a plain float addition, and the next window starts there
+// in the new binade.  E (chain_E) never decreases along the chain, so the cut
+// is in the first run whose last element reaches thr16, at the element a
+// bisection finds.  run(r, &n, &p) gives the count and probability of run r
+// (every lane asks for its own r); *run_at / *t_keep as chain_walk's.
+template <class RunF>
+__device__ __forceinline__ bool chain_cut_wave(int nr, RunF &&run, float thr16, int dt, int *run_at, uint32_t *t_keep)
+{
+    constexpr int32_t CAP = 1 << 30;  // ulp counts saturate here (any value past a binade: lim <= 2^24)
+    const int l = lane_id();
+    float F = 0.0f;
+    int r0 = 0;        // current run
+    uint32_t i0 = 0u;  // its elements already added
+    auto sat = [](int64_t v) { return (int32_t)(v < (int64_t)CAP ? v : (int64_t)CAP); };
+    while (r0 < nr) {
+        if (F == 0.0f) {
+            // 0 + p = p exactly; with p = 0 the whole run leaves F at 0
+            uint32_t n;
+            float p;
+            run(r0, &n, &p);
+            if (p == 0.0f) {
+                if (chain_E(0.0f, 0.0f, dt) >= thr16) { *run_at = r0; *t_keep = i0; return true; }
+                ++r0; i0 = 0u;
+                continue;
+            }
+            F = p;
+            if (chain_E(F, p, dt) >= thr16) { *run_at = r0; *t_keep = i0; return true; }
+            if (++i0 == n) { ++r0; i0 = 0u; }
+            continue;
+        }
+        {
+            // exact window: F and every p here multiples of 2^ez with the
+            // window's total below 2^(ez + 24): every partial sum is then a
+            // float, each addition exact, and F after each run one integer
+            // prefix sum (fp16 probabilities below 1 always qualify, bf16 ones
+            // from 2^-17 up)
+            const int r = r0 + l;
+            uint32_t n = 0u;
+            float p = 0.0f;
+            if (r < nr) run(r, &n, &p);
+            const int64_t m = r < nr ? (int64_t)(r == r0 ? n - i0 : n) : 0;
+            auto low_exp = [](float v) {  // exponent of the lowest set bit of v > 0
+                const uint32_t b = f32_bits(v), e = (b >> 23) & 0xffu, mt = b & 0x7fffffu;
+                const uint32_t mant = e == 0u ? mt : (mt | 0x800000u);
+                return (e == 0u ? -149 : (int)e - 150) + (int)__builtin_ctz(mant);
+            };
+            const int ez = wave_min<int>((m > 0 && p > 0.0f) ? low_exp(p) : low_exp(F));
+            const int ef = low_exp(F) < ez ? low_exp(F) : ez;
+            const double Pz = (m > 0 && p > 0.0f) ? ldexp((double)p, -ef) : 0.0;  // integer, exact
+            const double F0z = ldexp((double)F, -ef);
+            if (wave_sum((double)m * Pz) + F0z < 16777216.0) {  // 2^24: exact in double too
+                const int64_t inc = (int64_t)m * (int64_t)Pz;
+                const int64_t Nend = (int64_t)F0z + wave_incl_scan(inc);
+                const bool hit = m > 0 && chain_E(ldexpf((float)Nend, ef), p, dt) >= thr16;
+                const uint64_t hb = __ballot(hit);
+                if (hb == 0ull) {
+                    if (r0 + 64 >= nr) return false;
+                    F = ldexpf((float)__shfl(Nend, 63, 64), ef);
+                    r0 += 64;
+                    i0 = 0u;
+                    continue;
+                }
+                // the first run whose last element reaches thr16: bisect its steps
+                const int h = __builtin_ctzll(hb);
+                const int64_t hm = __shfl(m, h, 64), hN = __shfl(Nend, h, 64), hinc = __shfl(inc, h, 64);
+                const float hp = __shfl(p, h, 64);
+                const int64_t hP = hm > 0 ? hinc / hm : 0, hb0 = hN - hinc;  // per-step ulps, F before the run
+                int64_t lo = 1, hi = hm;
+                while (lo < hi) {
+                    const int64_t span = hi - lo + 1, stride = (span + 63) / 64;
+                    const int64_t cand = lo + (int64_t)l * stride;
+                    const bool ok = cand < hi && chain_E(ldexpf((float)(hb0 + cand * hP), ef), hp, dt) >= thr16;
+                    const uint64_t b = __ballot(ok);
+                    if (b) {
+                        const int f = __builtin_ctzll(b);
+                        hi = lo + (int64_t)f * stride;
+                        lo = f > 0 ? lo + (int64_t)(f - 1) * stride + 1 : lo;
+                    } else {
+                        const int64_t Lm = (hi - 1 - lo) / stride < 63 ? (hi - 1 - lo) / stride : 63;
+                        lo = lo + Lm * stride + 1;
+                    }
+                }
+                *run_at = r0 + h;
+                *t_keep = (h == 0 ? i0 : 0u) + (uint32_t)(lo - 1);
+                return true;
+            }
+        }
+        // the binade of F: F = N0 * u with u = 2^eu, lim = top / u
+        const uint32_t fb = f32_bits(F), fe = (fb >> 23) & 0xffu;
+        const int eu = fe == 0u ? -149 : (int)fe - 150;
+        const int32_t lim = fe == 0u ? (1 << 23) : (1 << 24);
+        const int32_t N0 = fe == 0u ? (int32_t)(fb & 0x7fffffu) : (int32_t)((fb & 0x7fffffu) | 0x800000u);
+        const int r = r0 + l;
+        uint32_t n = 0u;
+        float p = 0.0f;
+        if (r < nr) run(r, &n, &p);
+        const int64_t m = r < nr ? (int64_t)(r == r0 ? n - i0 : n) : 0;
+        const double P = ldexp((double)p, -eu);  // p / u, exact
+        const bool big = !(P < (double)CAP);     // the first step leaves the binade
+        const int32_t q = big ? CAP : (int32_t)P;
+        const double fr = big ? 0.0 : P - (double)q;
+        const bool tie = fr == 0.5;
+        const int32_t qs = fr > 0.5 ? q + 1 : q;
+        const int32_t inc = tie ? q + (q & 1) : qs;  // every step after the first
+        auto first_inc = [&](int32_t par) { return tie ? q + ((par + q) & 1) : qs; };
+        // this run's ulps added, for F / u even (D0) and odd (D1); the parity
+        // after follows from the parity before and the ulps added
+        int32_t D0 = 0, D1 = 0;
+        if (m > 0) {
+            D0 = sat((int64_t)first_inc(0) + (m - 1) * (int64_t)inc);
+            D1 = sat((int64_t)first_inc(1) + (m - 1) * (int64_t)inc);
+        }
+        // inclusive scan: the lanes before first, then this lane's run
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const int32_t pD0 = __shfl_up(D0, off, 64), pD1 = __shfl_up(D1, off, 64);
+            if (l >= off) {
+                const int32_t n0 = sat((int64_t)pD0 + ((pD0 & 1) ? D1 : D0));
+                const int32_t n1 = sat((int64_t)pD1 + (((1 + pD1) & 1) ? D1 : D0));
+                D0 = n0; D1 = n1;
+            }
+        }
+        const int32_t Nend = sat((int64_t)N0 + ((N0 & 1) ? D1 : D0));
+        int32_t Nbef = __shfl_up(Nend, 1, 64);
+        if (l == 0) Nbef = N0;
+        const int32_t inc1 = first_inc(Nbef & 1);
+        // every step stays inside iff its pre-value v has v + q <= lim - 1
+        // (the exact sum then lies below the binade's top); the last
+        // step's pre-value is the largest
+        const int64_t last_pre = m <= 1 ? (int64_t)Nbef : (int64_t)Nend - inc;
+        const bool inside = m == 0 || (Nbef < CAP && Nend < CAP && last_pre + q <= (int64_t)lim - 1);
+        const bool hit = inside && m > 0 && chain_E(ldexpf((float)Nend, eu), p, dt) >= thr16;
+        const uint64_t out = __ballot(!inside), hb = __ballot(hit);
+        const int c = out ? __builtin_ctzll(out) : 64, h = hb ? __builtin_ctzll(hb) : 64;
+        if (h == 64 && c == 64) {
+            if (r0 + 64 >= nr) return false;  // the chain never reaches thr16
+            F = ldexpf((float)__shfl(Nend, 63, 64), eu);
+            r0 += 64;
+            i0 = 0u;
+            continue;
+        }
+        // the run that decides this window, broadcast from its lane
+        const int w = h < c ? h : c;
+        const int64_t wm = __shfl(m, w, 64);
+        const int32_t wq = __shfl(q, w, 64), winc = __shfl(inc, w, 64), wnb = __shfl(Nbef, w, 64),
+                      winc1 = __shfl(inc1, w, 64);
+        const float wp = __shfl(p, w, 64);
+        const uint32_t wn = __shfl(n, w, 64);
+        const uint32_t kept0 = w == 0 ? i0 : 0u;  // elements of the run added before this window
+        // F after s in-binade steps of that run (1 <= s, inside the binade)
+        auto F_after = [&](int64_t s) { return ldexpf((float)((int64_t)wnb + winc1 + (s - 1) * winc), eu); };
+        // first step in [1, hi] whose E reaches thr16 (E(hi) does): 64-way
+        // steps over the lanes
+        auto first_hit = [&](int64_t hi) {
+            int64_t lo = 1;
+            while (lo < hi) {
+                const int64_t span = hi - lo + 1, stride = (span + 63) / 64;
+                const int64_t cand = lo + (int64_t)l * stride;
+                const bool ok = cand < hi && chain_E(F_after(cand), wp, dt) >= thr16;
+                const uint64_t b = __ballot(ok);
+                if (b) {  // between the last failing candidate and the first passing one
+                    const int f = __builtin_ctzll(b);
+                    hi = lo + (int64_t)f * stride;
+                    lo = f > 0 ? lo + (int64_t)(f - 1) * stride + 1 : lo;
+                } else {  // past the last candidate tested (the largest below hi)
+                    const int64_t L = (hi - 1 - lo) / stride < 63 ? (hi - 1 - lo) / stride : 63;
+                    lo = lo + L * stride + 1;
+                }
+            }
+            return lo;
+        };
+        if (h < c) {
+            *run_at = r0 + w;
+            *t_keep = kept0 + (uint32_t)(first_hit(wm) - 1);
+            return true;
+        }
+        // the crossing run: s steps inside, then one plain addition
+        const int64_t R = (int64_t)lim - 1 - wq;
+        int64_t s = 0;
+        if (wnb <= R) {
+            s = 1;
+            const int64_t N1 = (int64_t)wnb + winc1;
+            if (wm > 1 && N1 <= R) s = winc > 0 ? 2 + (R - N1) / winc : wm;
+            if (s > wm) s = wm;
+        }
+        float Fs = ldexpf((float)wnb, eu);
+        if (s > 0) {
+            Fs = F_after(s);
+            if (chain_E(Fs, wp, dt) >= thr16) {
+                *run_at = r0 + w;
+                *t_keep = kept0 + (uint32_t)(first_hit(s) - 1);
+                return true;
+            }
+        }
+        F = Fs + wp;
+        if (chain_E(F, wp, dt) >= thr16) {
+            *run_at = r0 + w;
+            *t_keep = kept0 + (uint32_t)s;
+            return true;
+        }
+        r0 += w;
+        i0 = kept0 + (uint32_t)s + 1u;
+        if (i0 == wn) { ++r0; i0 = 0u; }
+    }
+    return false;
+}
+
 // Top-p cut over elements with key >= floor_key; sm.v.l1 holds their 256-bin
 // histogram and S their total weight.
 template <int DT>
@@ -1172,7 +1390,7 @@ __device__ __forceinline__ void leader_row(Smem &sm, RowCx &c, const RowPlan &pl
         write_row(ro, a, row, id, id >= 0 ? MIS_ROW_OK : MIS_ROW_INVALID, pl.mode, m, row_key(-INFINITY, DT), -1, SK);
     } else if (pl.mode == M_SMALLK) {
         final_generic<DT>(sm, c, pl, ro, a);  // the rows k_rowpass deferred (or no row pass ran)
-    } else if (DT != F32 && pl.mode == M_TOPP) {
+    } else if (DT != F32 && pl.mode == M_TOPP && !L.t16) {
         // the cut among the row's K_PROBE largest values first
         double s = 0.0;
         for (int g = tid; g < L.G; g += NT) {
@@ -1261,6 +1479,32 @@ __device__ __forceinline__ void load_chunk(const char *rowp, int64_t base, int64
     }
 }
 
+// load_chunk for a block of NTH threads holding EPT elements each (the chunk
+// is NTH * EPT elements: the chunk pass's own chunk when NTH * EPT = NT *
+// its EPT).  Element i of thread t is base + ((i / VEC) * NTH + t) * VEC + i % VEC.
+template <int DT, int EPT, int NTH>
+__device__ __forceinline__ void load_chunk_n(const char *rowp, int64_t base, int64_t V, int vec_ok, float (&x)[EPT])
+{
+    constexpr int VEC = Traits<DT>::VEC, NV = EPT / VEC, CH = NTH * EPT;
+    static_assert(EPT % VEC == 0, "whole vectors per thread");
+    const int tid = threadIdx.x;
+    if (vec_ok && base + CH <= V) {
+#pragma unroll
+        for (int v = 0; v < NV; ++v) loadvec<DT>(rowp, base + ((int64_t)v * NTH + tid) * VEC, &x[v * VEC]);
+    } else {
+#pragma unroll
+        for (int v = 0; v < NV; ++v) {
+            const int64_t j0 = base + ((int64_t)v * NTH + tid) * VEC;
+            if (vec_ok && j0 + VEC <= V) {
+                loadvec<DT>(rowp, j0, &x[v * VEC]);
+            } else {
+#pragma unroll
+                for (int e = 0; e < VEC; ++e) x[v * VEC + e] = (j0 + e < V) ? load1<DT>(rowp, j0 + e) : -INFINITY;
+            }
+        }
+    }
+}
+
 // ------------------------------------------------------------------ the kernel
 
 // ascending bitonic sort of one value per lane across a wave
@@ -1321,6 +1565,11 @@ __global__ __launch_bounds__(NT) void k_sample(Args a, int part)
     load_chunk<DT, EPT>(rowp, base, V, a.vec_ok, x);
     const int32_t base32 = (int32_t)base;  // V < 2^31
     auto idx_of = [&](int i) -> int32_t { return base32 + (int32_t)((((i / VEC) * NT + tid) * VEC) + (i % VEC)); };
+    if (DT != F32 && pl.mode == M_TOPP && L.t16) {
+        // this chunk's share of the row's key histogram, which k_t16_hist adds into
+        uint32_t *rh = reinterpret_cast<uint32_t *>(a.ws + L.t16h) + (size_t)row * NB16;
+        for (int b = chunk + G * tid; b < NB16; b += G * NT) rh[b] = 0u;
+    }
 
     const bool topp32 = DT == F32 && pl.mode == M_TOPP;
     float ymax = -INFINITY;
@@ -1353,9 +1602,10 @@ __global__ __launch_bounds__(NT) void k_sample(Args a, int part)
             tmax = fmaxf(tmax, x[i]);
             nan |= x[i] != x[i] ? 1u : 0u;
         }
-        // fp16/bf16 top-p rows first try their cut among the row's K_PROBE
-        // largest values: the chunk pass also emits those candidates
-        const bool topp16 = DT != F32 && pl.mode == M_TOPP;
+        // fp16/bf16 top-p rows of a large batch first try their cut among the
+        // row's K_PROBE largest values: the chunk pass also emits those
+        // candidates (a small batch's rows take the t16 passes instead)
+        const bool topp16 = DT != F32 && pl.mode == M_TOPP && !L.t16;
         if (pl.mode == M_SMALLK || topp16) {  // the finite count only candidate rows use
 #pragma unroll
             for (int i = 0; i < EPT; ++i) nf += x[i] != -INFINITY ? 1u : 0u;
@@ -2413,7 +2663,395 @@ __global__ __launch_bounds__(NTF) void k_tp_final(Args a)
     trace(a.ws, L, row, 30);
 }
 
+// ------------------------------------------------------------------ fp16/bf16 top-p rows
+//
+// Two launches after the chunk pass spread a 16-bit top-p row (top-k off)
+// over the GPU.  A 16-bit scaled logit takes one of 65536 values, and torch's
+// rounding chain depends only on the descending sequence of those values:
+//   k_t16_hist  one workgroup per (row, chunk): the row max m from the chunk
+//               maxima fixes the histogram's range, the NB16 16-bit keys at
+//               and below m's key; the chunk's elements are counted per key
+//               in LDS and the counts added into the row's histogram (integer
+//               atomics: the sum does not depend on their order; the chunk
+//               pass cleared the histogram); the chunk's exact mass sum
+//               exp(y - m) (float64, one dexp per occupied key) goes to its
+//               T16Chunk.
+//   k_t16_walk  one workgroup per (row, chunk): each workgroup of a row reads
+//               the merged histogram and S, rounds every run's probability
+//               (all threads), walks the chain over the runs of equal keys
+//               (chain_cut_wave, one wave) to the same cut, and writes its
+//               own chunk's mass above the cut key and its count of elements
+//               holding the cut key.
+// k_final's final_t16 then draws from those chunk masses, the tie index at
+// the cut key resolved in the one chunk where the kept ties end.  A row whose
+// chain runs past the histogram's range with elements left under it takes
+// the generic path (T16_DEFER).
+
+__device__ __forceinline__ T16Row *t16_row(const Args &a, int row)
+{
+    return reinterpret_cast<T16Row *>(a.ws + a.L.t16r) + row;
+}
+__device__ __forceinline__ T16Chunk *t16_chunk(const Args &a, int row, int g)
+{
+    return reinterpret_cast<T16Chunk *>(a.ws + a.L.t16c) + (size_t)row * a.L.G + g;
+}
+__device__ __forceinline__ uint32_t *t16_hist(const Args &a, int row)
+{
+    return reinterpret_cast<uint32_t *>(a.ws + a.L.t16h) + (size_t)row * NB16;
+}
+__device__ __forceinline__ uint32_t key16(float y, int dt) { return row_key(y, dt) >> 16; }
+__device__ __forceinline__ float value16(uint32_t k, int dt) { return value_of_row_key(k << 16, dt); }
+__device__ __forceinline__ uint32_t t16_base(float m, int dt)  // lowest key of the histogram's range
+{
+    const uint32_t km = key16(m, dt);
+    return km >= (uint32_t)(NB16 - 1) ? km - (uint32_t)(NB16 - 1) : 0u;
+}
+
+constexpr int NT16 = 1024;          // threads of k_t16_hist / k_t16_walk (16 waves, 8 or 16 elements each)
+constexpr int NW16 = NT16 / 64;
+struct T16Smem {
+    uint32_t h[NB16];               // k_t16_hist: the chunk's counts; k_t16_walk: run keys
+    uint32_t rc[NB16];              // run counts
+    float rp[NB16];                 // run probabilities (rounded to the dtype)
+    double etab[ETAB_N];
+    Red red;
+    uint32_t bu[8];
+    int32_t bi[8];
+};
+
+// EPT: the chunk pass's elements per thread (its chunk = NT * EPT elements,
+// here NT16 threads of EPT * NT / NT16 each)
+template <int DT, int EPT>
+__global__ __launch_bounds__(NT16) void k_t16_hist(Args a)
+{
+    constexpr int E = EPT * NT / NT16;
+    __shared__ T16Smem sm;
+    const Layout &L = a.L;
+    const int tid = threadIdx.x, G = L.G;
+    const int row = (int)(blockIdx.x / (unsigned)G), g = (int)(blockIdx.x % (unsigned)G);
+    mis_row_params P = a.params[row];
+    P.temperature = uni(P.temperature); P.top_k = uni(P.top_k); P.top_p = uni(P.top_p); P.uniform = uni(P.uniform);
+    const RowPlan pl = plan_row(P, a.V);
+    if (pl.mode != M_TOPP) return;
+    if (g == 0) trace(a.ws, L, row, 2);
+    float x[E];
+    const int64_t base = (int64_t)g * NT * EPT;
+    load_chunk_n<DT, E, NT16>(a.logits + (int64_t)row * a.stride_bytes, base, a.V, a.vec_ok, x);
+    exp_table(sm.etab, tid);
+    for (int b = tid; b < NB16; b += NT16) sm.h[b] = 0u;
+    T16Row *tr = t16_row(a, row);
+    // the row max from the chunk maxima (its barriers order the clearing above)
+    const ChunkSum *csr = reinterpret_cast<const ChunkSum *>(a.ws + L.chunks) + (size_t)row * G;
+    uint32_t flag = 0u;
+    float yg = -INFINITY;
+    if (tid < G) { flag = ldp(&csr[tid].flags); yg = ldp(&csr[tid].ymax); }
+    static_assert(G_MAX <= NT16, "one chunk per thread");
+    const float m = block_max<float, NW16>(yg, sm.red);
+    const uint32_t bad = block_sum<uint32_t, NW16>(flag ? 1u : 0u, sm.red);
+    if (bad != 0u || m == -INFINITY) {  // NaN / +inf: the generic path rejects the row
+        if (g == 0 && tid == 0) tr->status = T16_DEFER;
+        return;
+    }
+    const uint32_t kb = t16_base(m, DT);
+    const double md = (double)m;
+    if (g == 0) trace(a.ws, L, row, 9);
+    scale_all<DT, E>(x, pl.T, 1.0f / pl.T);  // x now holds y
+    double sb = 0.0;
+    uint32_t nb = 0u;
+#pragma unroll
+    for (int i = 0; i < E; ++i) {
+        const float y = x[i];
+        if (y == -INFINITY) continue;
+        const uint32_t k = key16(y, DT);
+        if (k >= kb) {
+            atomicAdd(&sm.h[k - kb], 1u);
+        } else {
+            sb += dexp((double)y - md, sm.etab);
+            ++nb;
+        }
+    }
+    __syncthreads();
+    if (g == 0) trace(a.ws, L, row, 3);
+    uint32_t *rh = t16_hist(a, row);
+    double s = sb;
+    for (int b = tid; b < NB16; b += NT16) {
+        const uint32_t c = sm.h[b];
+        if (c != 0u) {
+            s += (double)c * dexp((double)value16(kb + (uint32_t)b, DT) - md, sm.etab);
+            atomicAdd(&rh[b], c);
+        }
+    }
+    s = block_sum<double, NW16>(s, sm.red);
+    nb = block_sum<uint32_t, NW16>(nb, sm.red);
+    if (tid == 0) {
+        T16Chunk *tc = t16_chunk(a, row, g);
+        tc->S = s;
+        tc->below = nb;
+        if (g == 0) tr->status = T16_NONE;
+    }
+    if (g == 0) trace(a.ws, L, row, 4);
+}
+
+template <int DT, int EPT>
+__global__ __launch_bounds__(NT16) void k_t16_walk(Args a)
+{
+    constexpr int E = EPT * NT / NT16;
+    __shared__ T16Smem sm;
+    const Layout &L = a.L;
+    const int tid = threadIdx.x, G = L.G;
+    const int row = (int)(blockIdx.x / (unsigned)G), g = (int)(blockIdx.x % (unsigned)G);
+    mis_row_params P = a.params[row];
+    P.temperature = uni(P.temperature); P.top_k = uni(P.top_k); P.top_p = uni(P.top_p); P.uniform = uni(P.uniform);
+    const RowPlan pl = plan_row(P, a.V);
+    if (pl.mode != M_TOPP) return;
+    T16Row *tr = t16_row(a, row);
+    if (uni(ldp(&tr->status)) == T16_DEFER) return;
+    if (g == 0) trace(a.ws, L, row, 5);
+    float x[E];
+    const int64_t base = (int64_t)g * NT * EPT;
+    load_chunk_n<DT, E, NT16>(a.logits + (int64_t)row * a.stride_bytes, base, a.V, a.vec_ok, x);
+    exp_table(sm.etab, tid);
+    const ChunkSum *csr = reinterpret_cast<const ChunkSum *>(a.ws + L.chunks) + (size_t)row * G;
+    // the row max, S and the count under the range, in one fixed order
+    float yg = -INFINITY;
+    double sg = 0.0;
+    uint32_t bg = 0u;
+    if (tid < G) {
+        yg = ldp(&csr[tid].ymax);
+        const T16Chunk *tq = t16_chunk(a, row, tid);
+        sg = ldp(&tq->S);
+        bg = ldp(&tq->below);
+    }
+    const float m = block_max<float, NW16>(yg, sm.red);
+    const double S = block_sum<double, NW16>(sg, sm.red);
+    const uint32_t below = block_sum<uint32_t, NW16>(bg, sm.red);
+    const uint32_t kb = t16_base(m, DT);
+    const double md = (double)m;
+    // runs: the occupied keys in descending order, NB16 / NT16 bins per thread
+    constexpr int PER = NB16 / NT16;
+    const uint32_t *rh = t16_hist(a, row);
+    uint32_t hc[PER];
+    uint32_t nmine = 0u;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+        hc[j] = ldp(&rh[NB16 - 1 - (tid * PER + j)]);
+        nmine += hc[j] != 0u ? 1u : 0u;
+    }
+    uint32_t nr;
+    uint32_t o = block_excl_scan<uint32_t, NW16>(nmine, sm.red, &nr);
+    if (g == 0) trace(a.ws, L, row, 10);
+    // each run's key, count and probability RN16(RN32(exp(y - m) / S))
+#pragma unroll
+    for (int j = 0; j < PER; ++j)
+        if (hc[j] != 0u) {
+            const uint32_t b = (uint32_t)(NB16 - 1 - (tid * PER + j));
+            sm.h[o] = b;
+            sm.rc[o] = hc[j];
+            sm.rp[o] = rn_dtype((float)(dexp((double)value16(kb + b, DT) - md, sm.etab) / S), DT);
+            ++o;
+        }
+    __syncthreads();
+    if (g == 0) trace(a.ws, L, row, 6);
+    const float thr16 = rn_dtype(pl.top_p, DT);
+    if (wave_id() == 0) {
+        auto run = [&](int r, uint32_t *n, float *p) { *n = sm.rc[r]; *p = sm.rp[r]; };
+        int run_at = -1;
+        uint32_t tk = 0u;
+        const bool found = chain_cut_wave((int)nr, run, thr16, DT, &run_at, &tk);
+        if (lane_id() == 0) { sm.bi[0] = found ? run_at : -1; sm.bu[0] = tk; }
+    }
+    __syncthreads();
+    if (g == 0) trace(a.ws, L, row, 7);
+    const int run_at = sm.bi[0];
+    const uint32_t tk = sm.bu[0];
+    uint32_t status = T16_CUT, ck = 0u, t = 0u;
+    if (run_at < 0) {
+        // the chain never reaches thr16 over the range: everything in it is
+        // kept, and the row is done only if nothing lies under it
+        if (below != 0u || nr == 0u) status = T16_DEFER;
+        else { ck = kb + sm.h[nr - 1]; t = sm.rc[nr - 1]; }
+    } else if (tk > 0u) {
+        ck = kb + sm.h[run_at]; t = tk;
+    } else if (run_at > 0) {
+        ck = kb + sm.h[run_at - 1]; t = sm.rc[run_at - 1];
+    } else {
+        status = T16_EMPTY;  // rank 0 removed: nothing left to sample
+    }
+    if (status == T16_CUT) {
+        // this chunk: mass above the cut key and the elements holding it
+        scale_all<DT, E>(x, pl.T, 1.0f / pl.T);
+        double s = 0.0;
+        uint32_t cc = 0u;
+#pragma unroll
+        for (int i = 0; i < E; ++i) {
+            const float y = x[i];
+            if (y == -INFINITY) continue;
+            const uint32_t k = key16(y, DT);
+            if (k > ck) s += dexp((double)y - md, sm.etab);
+            cc += k == ck ? 1u : 0u;
+        }
+        s = block_sum<double, NW16>(s, sm.red);
+        cc = block_sum<uint32_t, NW16>(cc, sm.red);
+        if (tid == 0) {
+            T16Chunk *tc = t16_chunk(a, row, g);
+            tc->kept = s;
+            tc->ccnt = cc;
+        }
+    }
+    if (g == 0 && tid == 0) {
+        tr->ck = ck;
+        tr->t = t;
+        tr->S = S;
+        tr->status = status;
+    }
+    if (g == 0) trace(a.ws, L, row, 8);
+}
+
+// Index of the t-th (1-based) element of chunk g, in index order, whose
+// scaled value has key rk (kept_by_cut's key form); -1 when the chunk holds
+// fewer.  Thread i takes the contiguous elements [cbeg + i*per, cbeg +
+// (i+1)*per), loaded up front, as draw_in_chunk.
+template <int DT, int NTH = NT, class SM>
+__device__ __forceinline__ int64_t nth_key_in_chunk(SM &sm, const RowCx &c, int g, uint32_t rk, uint32_t t)
+{
+    constexpr int VEC = Traits<DT>::VEC, MAXPER = 64 * NT / NTH;
+    const int64_t cbeg = (int64_t)g * c.CH;
+    const int64_t cend = cbeg + c.CH < c.V ? cbeg + c.CH : c.V;
+    const int per = (int)(c.CH / NTH);
+    const int64_t jb = cbeg + (int64_t)threadIdx.x * per;
+    float xs[MAXPER];
+#pragma unroll
+    for (int v = 0; v < MAXPER / VEC; ++v) {
+        if (v * VEC < per) {
+            const int64_t j0 = jb + (int64_t)v * VEC;
+            if (c.vec_ok && j0 + VEC <= cend) {
+                loadvec<DT>(c.rowp, j0, &xs[v * VEC]);
+            } else {
+#pragma unroll
+                for (int e = 0; e < VEC; ++e) xs[v * VEC + e] = (j0 + e < cend) ? load1<DT>(c.rowp, j0 + e) : -INFINITY;
+            }
+        }
+    }
+    const float T = c.T, rT = 1.0f / c.T;
+    uint64_t hit = 0ull;
+#pragma unroll
+    for (int i = 0; i < MAXPER; ++i) {
+        if (i < per && jb + i < cend) {
+            const float y = scale_r<DT>(xs[i], T, rT);
+            hit |= (y != -INFINITY && row_key(y, DT) == rk) ? (1ull << i) : 0ull;
+        }
+    }
+    const uint32_t mine = (uint32_t)__popcll(hit);
+    uint32_t tot;
+    const uint32_t before = block_excl_scan<uint32_t, NTH / 64>(mine, sm.red, &tot);
+    if (threadIdx.x == 0) sm.bq[0] = 0xffffffffffffffffull;
+    __syncthreads();
+    if (mine > 0u && before < t && t <= before + mine) {
+        uint64_t hh = hit;
+        for (uint32_t k = before + 1u; k < t; ++k) hh &= hh - 1ull;  // drop the lower set bits
+        sm.bq[0] = (unsigned long long)(jb + __builtin_ctzll(hh));
+    }
+    __syncthreads();
+    const unsigned long long r = sm.bq[0];
+    __syncthreads();
+    return r == 0xffffffffffffffffull ? -1 : (int64_t)r;
+}
+
+// LDS of k_t16_final
+struct T16FinSmem {
+    double e16[NB16];               // exp(y - m) per key in [ck, key of m] (index key - kb)
+    double cw[G_MAX];               // per-chunk kept mass
+    double etab[ETAB_N];
+    Red red;
+    uint32_t bu[8];
+    int32_t bi[8];
+    double bd[8];
+    unsigned long long bq[2];
+};
+
+// One workgroup per 16-bit top-p row after the t16 passes: per-chunk kept
+// masses, the tie index at the cut key (in the one chunk where the kept ties
+// end), the draw.  Rows the passes left to the generic path (T16_DEFER) are
+// k_final's.  The chunk masses were summed from the same dexp values this
+// table holds (a 16-bit y is its key's value), so the draw inside a chunk
+// adds the same numbers.
+template <int DT>
+__global__ __launch_bounds__(NTF) void k_t16_final(Args a)
+{
+    __shared__ T16FinSmem sm;
+    constexpr int NW = NTF / 64;
+    const Layout &L = a.L;
+    const int tid = threadIdx.x, G = L.G, row = blockIdx.x;
+    mis_row_params P = a.params[row];
+    P.temperature = uni(P.temperature); P.top_k = uni(P.top_k); P.top_p = uni(P.top_p); P.uniform = uni(P.uniform);
+    const RowPlan pl = plan_row(P, a.V);
+    if (pl.mode != M_TOPP) return;
+    const T16Row *tr = t16_row(a, row);
+    const uint32_t st = uni(ldp(&tr->status));
+    RowOut *ro = reinterpret_cast<RowOut *>(a.ws + L.rowout) + row;
+    if (st == T16_EMPTY) {  // rank 0 removed: torch.multinomial's invalid distribution
+        write_row(ro, a, row, -1, MIS_ROW_INVALID, pl.mode, 0.0f, 0u, 0, 0.0);
+        return;
+    }
+    if (st != T16_CUT) return;
+    trace(a.ws, L, row, 11);
+    const uint32_t ck = uni(ldp(&tr->ck)), t = uni(ldp(&tr->t));
+    exp_table(sm.etab, tid);
+    const ChunkSum *csr = reinterpret_cast<const ChunkSum *>(a.ws + L.chunks) + (size_t)row * G;
+    float yg = -INFINITY;
+    double kept = 0.0;
+    uint32_t cg = 0u;
+    static_assert(G_MAX <= NTF, "one chunk per thread");
+    if (tid < G) {
+        yg = ldp(&csr[tid].ymax);
+        const T16Chunk *tq = t16_chunk(a, row, tid);
+        kept = ldp(&tq->kept);
+        cg = ldp(&tq->ccnt);
+    }
+    const float m = block_max<float, NW>(yg, sm.red);
+    uint32_t tot;
+    const uint32_t pre = block_excl_scan<uint32_t, NW>(cg, sm.red, &tot);
+    const double md = (double)m;
+    const uint32_t kb = t16_base(m, DT), km = key16(m, DT);
+    for (uint32_t k = ck + (uint32_t)tid; k <= km; k += NTF) sm.e16[k - kb] = dexp((double)value16(k, DT) - md, sm.etab);
+    if (tid == 0) sm.bi[2] = -1;
+    __syncthreads();
+    // the chunk holding the t-th tie (index order) keeps part of its ties
+    if (tid < G) {
+        const uint32_t kc = t > pre ? (t - pre < cg ? t - pre : cg) : 0u;
+        sm.cw[tid] = kept + sm.e16[ck - kb] * (double)kc;
+        if (cg != 0u && pre < t && t <= pre + cg) { sm.bi[2] = tid; sm.bu[2] = t - pre; sm.bu[3] = cg; }
+    }
+    __syncthreads();
+    RowCx c;
+    c.rowp = a.logits + (int64_t)row * a.stride_bytes;
+    c.V = a.V; c.vec_ok = a.vec_ok; c.T = pl.T; c.m = m; c.G = G; c.CH = (int64_t)NT * L.ept; c.row = row;
+    const int gb = sm.bi[2];
+    const uint32_t tb = sm.bu[2], cb = sm.bu[3];
+    const uint32_t rk = ck << 16;  // the cut key as a row key
+    int32_t cut_i = IDX_ALL;
+    if (gb >= 0 && tb < cb) cut_i = (int32_t)nth_key_in_chunk<DT, NTF>(sm, c, gb, rk, tb);
+    else if (gb >= 0 && tot > t) cut_i = (int32_t)((int64_t)(gb + 1) * c.CH - 1);  // every tie up to chunk gb's end
+    trace(a.ws, L, row, 12);
+    int gsel;
+    double resid, SK;
+    pick_chunk(sm, G, pl.u, &gsel, &resid, &SK);
+    int64_t id = -1;
+    if (gsel >= 0) {
+        const float T = pl.T, rT = 1.0f / pl.T;
+        id = draw_in_chunk<DT, NTF>(sm, c, gsel, resid, [&](float xv, int64_t j) -> double {
+            const float y = scale_r<DT>(xv, T, rT);
+            if (y == -INFINITY) return 0.0;
+            const uint32_t k = row_key(y, DT);
+            return kept_by_cut(k, j, rk, cut_i) ? sm.e16[(k >> 16) - kb] : 0.0;
+        });
+    }
+    write_row(ro, a, row, id, id >= 0 ? MIS_ROW_OK : MIS_ROW_INVALID, pl.mode, m, rk, cut_i, SK);
+    trace(a.ws, L, row, 13);
+}
+
 enum : int { FIN_ALL = 0, FIN_OTHERS = 1, FIN_DEFERRED = 2, FIN_REST = 3, FIN_TAIL = 4 };
+constexpr int FIN_T16 = 8;  // flag: the t16 passes ran before this k_final
 
 // One workgroup per row: merges the chunk summaries and finishes the row:
 // greedy, temperature, small top-k from the summaries; the generic re-read
@@ -2448,15 +3086,20 @@ __global__ __launch_bounds__(NT) void k_final(Args a, int phase)
     //                 the top-p passes', and the rows they deferred;
     //   FIN_TAIL      FIN_DEFERRED when FIN_OTHERS did not run: the deferred
     //                 rows and those neither serves.
-    const int mode = sm.pl.mode;
+    //   FIN_T16       (flag) the t16 passes ran: of the 16-bit top-p rows
+    //                 only those they deferred.
+    const int mode = sm.pl.mode, ph = phase & ~FIN_T16;
     const bool rp = mode == M_BAD || mode == M_INVAL || mode == M_GREEDY || mode == M_TEMP || mode == M_SMALLK;
     const bool tp = DT == F32 && mode == M_TOPP;
     bool serve;
-    if (phase == FIN_ALL) serve = !rp || ldp(&ro->status) == ROW_DEFER;
-    else if (phase == FIN_OTHERS) serve = !rp && !tp;
-    else if (phase == FIN_DEFERRED) serve = (rp || tp) && ldp(&ro->status) == ROW_DEFER;
-    else if (phase == FIN_TAIL) serve = (!rp && !tp) || ldp(&ro->status) == ROW_DEFER;
+    if (ph == FIN_ALL) serve = !rp || ldp(&ro->status) == ROW_DEFER;
+    else if (ph == FIN_OTHERS) serve = !rp && !tp;
+    else if (ph == FIN_DEFERRED) serve = (rp || tp) && ldp(&ro->status) == ROW_DEFER;
+    else if (ph == FIN_TAIL) serve = (!rp && !tp) || ldp(&ro->status) == ROW_DEFER;
     else serve = !tp || ldp(&ro->status) == ROW_DEFER;
+    // after the t16 passes a 16-bit top-p row is k_t16_final's unless they deferred it
+    if (serve && DT != F32 && mode == M_TOPP && (phase & FIN_T16) != 0)
+        serve = ldp(&reinterpret_cast<const T16Row *>(a.ws + L.t16r)[row].status) == T16_DEFER;
     if (!serve) return;
     leader_row<DT>(sm, sm.cx, sm.pl, csr, ro, sm.args);
     trace(a.ws, L, row, 31);
@@ -2568,6 +3211,17 @@ static hipError_t launch_dt(const Args &a, float *probs, uint32_t *keep, hipStre
         if (side && (e = hipStreamWaitEvent(st, sd->join, 0)) != hipSuccess) return e;
         const int ph = side ? ((kinds & MIS_KIND_GENERIC) ? FIN_DEFERRED : FIN_TAIL) : rowpass_here ? FIN_TAIL : FIN_REST;
         hipLaunchKernelGGL((k_final<DT>), dim3(B), dim3(NT), 0, st, a, ph);
+    } else if (DT != F32 && a.L.t16 && (kinds & MIS_KIND_GENERIC)) {
+        const unsigned bg = (unsigned)(a.L.B * a.L.G);
+        if (a.L.ept == 64) {
+            hipLaunchKernelGGL((k_t16_hist<DT, 64>), dim3(bg), dim3(NT16), 0, st, a);
+            hipLaunchKernelGGL((k_t16_walk<DT, 64>), dim3(bg), dim3(NT16), 0, st, a);
+        } else {
+            hipLaunchKernelGGL((k_t16_hist<DT, 32>), dim3(bg), dim3(NT16), 0, st, a);
+            hipLaunchKernelGGL((k_t16_walk<DT, 32>), dim3(bg), dim3(NT16), 0, st, a);
+        }
+        hipLaunchKernelGGL((k_t16_final<DT>), dim3(B), dim3(NTF), 0, st, a);
+        hipLaunchKernelGGL((k_final<DT>), dim3(B), dim3(NT), 0, st, a, (int)(FIN_ALL | FIN_T16));
     } else {
         hipLaunchKernelGGL((k_final<DT>), dim3(B), dim3(NT), 0, st, a, (int)FIN_ALL);
     }

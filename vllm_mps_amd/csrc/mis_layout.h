@@ -101,18 +101,44 @@ struct TopRow {                     // written by the row's chunk-0 workgroup of
 };
 static_assert(sizeof(TopRow) % 256 == 0, "TopRow size");
 
+// fp16/bf16 top-p passes (k_t16_hist, k_t16_walk): per row a count
+// histogram over the NB16 16-bit keys at and below the row max's key, per
+// (row, chunk) its exact mass and kept mass, per row the cut
+constexpr int NB16 = 4096;
+struct T16Chunk {                   // 32 B per (row, chunk)
+    double S;                       // sum of exp(y - m) over the chunk's finite elements (m = row max)
+    double kept;                    // mass of its elements with keys above the cut key
+    uint32_t below;                 // finite elements with keys under the histogram's range
+    uint32_t ccnt;                  // elements holding the cut key
+    uint32_t pad[2];
+};
+enum : uint32_t { T16_NONE = 0, T16_CUT = 1, T16_DEFER = 2, T16_EMPTY = 3 };
+struct T16Row {                     // 32 B per row
+    uint32_t status;                // T16_*: CUT = ck / t below hold the cut, EMPTY = nothing kept
+    uint32_t ck;                    // cut key (16-bit): every element with a larger key is kept
+    uint32_t t;                     // elements holding ck that are kept (the first t in index order)
+    uint32_t pad0;
+    double S;                       // sum of exp(y - m) over the row
+    double pad1;
+};
+
+// fp16/bf16 top-p rows spread over the t16 passes while the batch has fewer
+// rows than this (a CU count); a larger batch gives each row one workgroup
+// (the K_PROBE probe, then the generic path), which fills the GPU by itself
+constexpr int64_t T16_ROWS = 256;
+
 struct Layout {
     int64_t B, V;
     int ept, G;
     int ccap;                       // candidate slots per (row, chunk)
-    size_t rowout, chunks, rbuf, cand, topc, topr, stash, perm, total;
+    int t16;                        // fp16/bf16 and B < T16_ROWS: the t16 passes serve the top-p rows
+    size_t rowout, chunks, rbuf, cand, topc, topr, stash, perm, t16h, t16c, t16r, total;
 };
 
 inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-// Elements per thread: 16 (chunks of 4096 elements; 16 vector registers of
-// logits per thread keep the chunk pass at six or more waves per SIMD), 64
-// when the row would need more than G_MAX chunks.
+// Elements per thread: 32 (chunks of 8192 elements), 64 when the row would
+// need more than G_MAX chunks.
 inline Layout make_layout(int64_t B, int64_t V, int dtype)
 {
     Layout L;
@@ -144,6 +170,12 @@ inline Layout make_layout(int64_t B, int64_t V, int dtype)
     L.stash = off;  off = align256(off + (f32 ? sizeof(Cand) * (size_t)STASH_CAP * BG : 0));
     // fp32: the rows in launch order (top-p rows first) and their count
     L.perm = off;   off = align256(off + (f32 ? sizeof(int32_t) * ((size_t)B + 1) : 0));
+    // fp16/bf16 top-p of a small batch: per-row key histograms, per-chunk
+    // masses, per-row cuts
+    L.t16 = (!f32 && B < T16_ROWS) ? 1 : 0;
+    L.t16h = off;   off = align256(off + (L.t16 ? sizeof(uint32_t) * (size_t)NB16 * (size_t)B : 0));
+    L.t16c = off;   off = align256(off + (L.t16 ? sizeof(T16Chunk) * BG : 0));
+    L.t16r = off;   off = align256(off + (L.t16 ? sizeof(T16Row) * (size_t)B : 0));
     L.total = off;
     return L;
 }
