@@ -459,33 +459,12 @@ __device__ __forceinline__ int32_t tie_index(Smem &sm, const RowCx &c, uint32_t 
     return (int32_t)lo;
 }
 
-// Sequential walk of the 16-bit top-p chain over runs (one thread).  Returns
-// true when some rank triggers removal; the cut then keeps *t_keep elements of
-// run *run_at (0 = the cut is the previous run).
-__device__ __forceinline__ bool chain_walk(const uint32_t *rcnt, const float *rp, int nruns, float &F, float thr16, int dt,
-                           int *run_at, uint32_t *t_keep)
-{
-    for (int r = 0; r < nruns; ++r) {
-        const float p = rp[r];
-        const uint32_t n = rcnt[r];
-        const float Fend = chain_add_n(F, p, n);
-        if (chain_E(Fend, p, dt) >= thr16) {
-            uint32_t lo = 0, hi = n - 1;
-            while (lo < hi) {
-                const uint32_t mid = lo + (hi - lo) / 2;
-                if (chain_E(chain_add_n(F, p, (uint64_t)mid + 1), p, dt) >= thr16) hi = mid; else lo = mid + 1;
-            }
-            *run_at = r;
-            *t_keep = lo;
-            return true;
-        }
-        F = Fend;
-    }
-    return false;
-}
-
-// chain_walk's result computed by one wave (all 64 lanes call it with the
-// same arguments and receive the same result), 64 runs at a time.
+// The 16-bit top-p chain over runs of equal probabilities, walked by one
+// wave (all 64 lanes call it with the same arguments and receive the same
+// result), 64 runs at a time.  Element by element in rank order F <- fl32(F
+// + p) and the element is removed once chain_E(F, p) >= thr16.  Returns true
+// when some element is removed: the first such is element *t_keep (0-based)
+// of run *run_at, whose earlier elements are kept.
 //
 // Inside one binade of F (ulp u), F + p rounds to F + q*u or F + (q+1)*u with
 // q = floor(p / u): a run of n equal p adds a fixed number of ulps per step,
@@ -499,13 +478,16 @@ __device__ __forceinline__ bool chain_walk(const uint32_t *rcnt, const float *rp
 // in the new binade.  E (chain_E) never decreases along the chain, so the cut
 // is in the first run whose last element reaches thr16, at the element a
 // bisection finds.  run(r, &n, &p) gives the count and probability of run r
-// (every lane asks for its own r); *run_at / *t_keep as chain_walk's.
+// (every lane asks for its own r).  F_io:
+// F before the first run (null: 0), and F after the last one when no run
+// holds the cut.
 template <class RunF>
-__device__ __forceinline__ bool chain_cut_wave(int nr, RunF &&run, float thr16, int dt, int *run_at, uint32_t *t_keep)
+__device__ __forceinline__ bool chain_cut_wave(int nr, RunF &&run, float thr16, int dt, int *run_at, uint32_t *t_keep,
+                                               float *F_io = nullptr)
 {
     constexpr int32_t CAP = 1 << 30;  // ulp counts saturate here (any value past a binade: lim <= 2^24)
     const int l = lane_id();
-    float F = 0.0f;
+    float F = F_io ? *F_io : 0.0f;
     int r0 = 0;        // current run
     uint32_t i0 = 0u;  // its elements already added
     auto sat = [](int64_t v) { return (int32_t)(v < (int64_t)CAP ? v : (int64_t)CAP); };
@@ -551,8 +533,8 @@ __device__ __forceinline__ bool chain_cut_wave(int nr, RunF &&run, float thr16, 
                 const bool hit = m > 0 && chain_E(ldexpf((float)Nend, ef), p, dt) >= thr16;
                 const uint64_t hb = __ballot(hit);
                 if (hb == 0ull) {
-                    if (r0 + 64 >= nr) return false;
                     F = ldexpf((float)__shfl(Nend, 63, 64), ef);
+                    if (r0 + 64 >= nr) break;
                     r0 += 64;
                     i0 = 0u;
                     continue;
@@ -630,8 +612,8 @@ __device__ __forceinline__ bool chain_cut_wave(int nr, RunF &&run, float thr16, 
         const uint64_t out = __ballot(!inside), hb = __ballot(hit);
         const int c = out ? __builtin_ctzll(out) : 64, h = hb ? __builtin_ctzll(hb) : 64;
         if (h == 64 && c == 64) {
-            if (r0 + 64 >= nr) return false;  // the chain never reaches thr16
             F = ldexpf((float)__shfl(Nend, 63, 64), eu);
+            if (r0 + 64 >= nr) break;  // the chain never reaches thr16
             r0 += 64;
             i0 = 0u;
             continue;
@@ -699,6 +681,7 @@ __device__ __forceinline__ bool chain_cut_wave(int nr, RunF &&run, float thr16, 
         i0 = kept0 + (uint32_t)s + 1u;
         if (i0 == wn) { ++r0; i0 = 0u; }
     }
+    if (F_io) *F_io = F;
     return false;
 }
 
@@ -776,20 +759,23 @@ __device__ __forceinline__ void topp_cut_generic(Smem &sm, const RowCx &c, float
             nruns_total += (int)tot;
         }
         __syncthreads();
-        if (threadIdx.x == 0) {
+        if (wave_id() == 0) {
             int run_at = -1;
             uint32_t tk = 0;
             float Fw = F;
-            const bool found = chain_walk(sm.w.r.rcnt, sm.w.r.rp, nruns_total, Fw, thr16, DT, &run_at, &tk);
-            sm.bi[1] = found ? 1 : 0;
-            sm.bu[0] = tk;
-            sm.bf[0] = Fw;
-            sm.bu[1] = nruns_total > 0 ? sm.w.r.rkey[nruns_total - 1] : 0u;
-            if (found) {
-                sm.bu[2] = sm.w.r.rkey[run_at];
-                sm.bu[3] = sm.w.r.rcnt[run_at];
-                sm.bu[4] = run_at > 0 ? sm.w.r.rkey[run_at - 1] : 0u;
-                sm.bi[3] = run_at > 0 ? 1 : 0;
+            auto run = [&](int q, uint32_t *n, float *p) { *n = sm.w.r.rcnt[q]; *p = sm.w.r.rp[q]; };
+            const bool found = chain_cut_wave(nruns_total, run, thr16, DT, &run_at, &tk, &Fw);
+            if (lane_id() == 0) {
+                sm.bi[1] = found ? 1 : 0;
+                sm.bu[0] = tk;
+                sm.bf[0] = Fw;
+                sm.bu[1] = nruns_total > 0 ? sm.w.r.rkey[nruns_total - 1] : 0u;
+                if (found) {
+                    sm.bu[2] = sm.w.r.rkey[run_at];
+                    sm.bu[3] = sm.w.r.rcnt[run_at];
+                    sm.bu[4] = run_at > 0 ? sm.w.r.rkey[run_at - 1] : 0u;
+                    sm.bi[3] = run_at > 0 ? 1 : 0;
+                }
             }
         }
         __syncthreads();
@@ -1238,21 +1224,23 @@ __device__ __forceinline__ bool leader_smallk(Smem &sm, const RowCx &c, const Ro
                 __syncthreads();
             }
             static_assert(PT == 4, "four survivors per thread");
-            if (threadIdx.x == 0) {
+            if (wave_id() == 0) {
                 const float thr16 = rn_dtype(pl.top_p, DT);
-                float F = 0.0f;
                 uint32_t r0 = ns;
                 int run_at = -1;
                 uint32_t tk = 0;
-                const bool found = chain_walk(sm.w.r.rcnt, sm.w.r.rp, (int)sm.bu[2], F, thr16, DT, &run_at, &tk);
+                auto run = [&](int q, uint32_t *n, float *p) { *n = sm.w.r.rcnt[q]; *p = sm.w.r.rp[q]; };
+                const bool found = chain_cut_wave((int)sm.bu[2], run, thr16, DT, &run_at, &tk);
                 if (found) r0 = sm.w.r.rkey[run_at] + tk;
-                sm.bu[0] = r0;
-                sm.bi[1] = found ? 1 : 0;
-                sm.bi[2] = (found && amb <= (uint32_t)run_at) ? 1 : 0;
-                if (r0 > 0) {
-                    const uint64_t q = sm.u.so.k[r0 - 1];
-                    sm.bu[1] = (uint32_t)(q >> 32);
-                    sm.bi[0] = (int32_t)(0xffffffffu - (uint32_t)q);
+                if (lane_id() == 0) {
+                    sm.bu[0] = r0;
+                    sm.bi[1] = found ? 1 : 0;
+                    sm.bi[2] = (found && amb <= (uint32_t)run_at) ? 1 : 0;
+                    if (r0 > 0) {
+                        const uint64_t q = sm.u.so.k[r0 - 1];
+                        sm.bu[1] = (uint32_t)(q >> 32);
+                        sm.bi[0] = (int32_t)(0xffffffffu - (uint32_t)q);
+                    }
                 }
             }
             __syncthreads();
@@ -2052,7 +2040,7 @@ __global__ __launch_bounds__(NTS) void k_rowpass(Args a)
         } else {
             // 16-bit rounding chain in the stable descending order: sort, runs
             // of equal keys with their probabilities in parallel, then one
-            // thread walks the chain over the runs
+            // wave walks the chain over the runs
             const uint64_t kt = i < (int)ns ? (((uint64_t)sm.sv.key[i] << 32) | (uint64_t)(0xffffffffu - (uint32_t)sm.sv.idx[i])) : 0ull;
             const double et = i < (int)ns ? sm.sv.e[i] : 0.0;
             sm.u.so.k[i] = kt;
@@ -2071,18 +2059,20 @@ __global__ __launch_bounds__(NTS) void k_rowpass(Args a)
             if ((uint32_t)i < nr) sm.rcnt[i] = ((uint32_t)i + 1 < nr ? sm.rkey[i + 1] : ns) - sm.rkey[i];
             __syncthreads();
             trace(a.ws, L, row, 24);
-            if (tid == 0) {
+            if (wave_id() == 0) {
                 const float thr16 = rn_dtype(pl.top_p, DT);
-                float F = 0.0f;
                 int run_at = -1;
                 uint32_t tk = 0;
-                const bool found = chain_walk(sm.rcnt, sm.rp, (int)nr, F, thr16, DT, &run_at, &tk);
+                auto run = [&](int q, uint32_t *n, float *p) { *n = sm.rcnt[q]; *p = sm.rp[q]; };
+                const bool found = chain_cut_wave((int)nr, run, thr16, DT, &run_at, &tk);
                 const uint32_t r0 = found ? sm.rkey[run_at] + tk : ns;  // kept: sorted positions < r0
-                sm.bu[0] = r0;
-                if (r0 > 0) {
-                    const uint64_t q = sm.u.so.k[r0 - 1];
-                    sm.bu[1] = (uint32_t)(q >> 32);
-                    sm.bi[0] = (int32_t)(0xffffffffu - (uint32_t)q);
+                if (lane_id() == 0) {
+                    sm.bu[0] = r0;
+                    if (r0 > 0) {
+                        const uint64_t q = sm.u.so.k[r0 - 1];
+                        sm.bu[1] = (uint32_t)(q >> 32);
+                        sm.bi[0] = (int32_t)(0xffffffffu - (uint32_t)q);
+                    }
                 }
             }
             __syncthreads();
