@@ -59,6 +59,9 @@ def parse():
     ap.add_argument("--rotate-gib", type=float, default=1.0, help="distinct input bytes cycled through")
     ap.add_argument("--cpu-rows", type=int, default=32, help="rows in the CPU-baseline sample (0 = skip)")
     ap.add_argument("--cpu-steps", type=int, default=5)
+    ap.add_argument("--row-params", default=None, metavar="T,k,p",
+                    help="give every row this temperature, top_k and top_p (one row mode at a time, for per-mode "
+                         "counters); the default keeps the config's own per-row mix")
     ap.add_argument("--copy-calib-mib", type=int, default=0,
                     help="after the timed steps, run 5 plain device copies of this many MiB (calibrates "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE against known bytes)")
@@ -137,6 +140,11 @@ def main():
     torch.cuda.set_device(dev)
     w = W.make(args.config)
     B, V = w.shape
+    if args.row_params:
+        import numpy as np
+        t_, k_, p_ = args.row_params.split(",")
+        w = W.Workload(w.name, w.dtype, w.logits, np.full(B, float(t_), np.float32), np.full(B, int(k_), np.int32),
+                       np.full(B, float(p_), np.float32), w.uniform)
     esz = 4 if w.dtype == "f32" else 2
     bytes_alg = W.algorithmic_bytes(B, V, w.dtype)
     nbuf = max(1, math.ceil(args.rotate_gib * (1 << 30) / (B * V * esz)))
@@ -201,7 +209,8 @@ def main():
         "dtype": w.dtype,
         "data": "synthetic",
         "config": {"workload": WORKLOAD_DESC[args.config], "B": B, "V": V, "seed": W.SEEDS[args.config],
-                   "rotating_buffers": nbuf, "rotated_bytes": nbuf * B * V * esz},
+                   "rotating_buffers": nbuf, "rotated_bytes": nbuf * B * V * esz,
+                   **({"row_params": args.row_params} if args.row_params else {})},
         "tokens_per_s": round(rows_per_s, 1),
         "p50_us_per_step": round(statistics.median(step_us), 2),
         "p90_us_per_step": round(q[8], 2),
