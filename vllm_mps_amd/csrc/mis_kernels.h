@@ -20,14 +20,20 @@
 //   small top-k  the elements above a floor taken from the per-thread maxima
 //                (closed under the ties the scaling creates) as candidates;
 //   fp32 top-p   float64 sum of exact weights and coarse mass bins;
-//   16-bit top-p the 512 largest values as candidates, float64 sum.
-// k_final (row pass): one workgroup per row merges the summaries: greedy,
-// temperature (chunk holding the draw, then that chunk re-read), small top-k
-// (exact k'-th value over the candidates, top-p over the survivors, draw),
-// the 16-bit top-p probe; the generic path (radix descent over re-reads of
-// the row, the 16-bit rounding chain) serves the rest.
-// k_tp_* (fp32 top-p rows): prep, fine bins, merge, collect and final
-// passes spread each row over the GPU.
+//   16-bit top-p a large batch: the 512 largest values as candidates and a
+//                float64 sum; a small batch: nothing but clearing the row's
+//                key histogram (the t16 passes read the chunk again).
+// Then, by row kind:
+//   k_rowpass    greedy, temperature and small top-k rows (1024 threads per
+//                row): candidates, radix select, top-p over the survivors,
+//                the draw;
+//   k_tp_hist, k_tp_final   fp32 top-p rows spread over the GPU: fine bins
+//                and a stash per chunk, then the exact cut per row;
+//   k_t16_hist, k_t16_walk, k_t16_final   fp16/bf16 top-p rows of small
+//                batches: per-chunk key histograms merged per row, the
+//                rounding chain walked by one wave, the draw;
+//   k_final      everything else (the generic re-read path, the 16-bit probe
+//                of large batches) and the rows the other passes deferred.
 // k_emit: debug probabilities / keep bitmask from each row's cut.
 //
 // Semantics follow model/sampler.py:18-60 per row: greedy argmax (ties ->
@@ -3154,7 +3160,7 @@ static hipError_t launch_chunks(const Args &a, hipStream_t st, int part)
     }
 }
 
-// events (optional, nev = 3 or 4): [0] before the chunk pass, [1] after the
+// events (optional, nev = 3 or 4): [0] before the chunk pass (after k_rows), [1] after the
 // chunk pass on the caller's stream (with the split, its fp32 top-p rows'),
 // [2] after the row pass (before the debug emit), [3] after the side stream's
 // chunk pass (recorded only with the split: one more marker on the caller's
@@ -3170,12 +3176,13 @@ static hipError_t launch_dt(const Args &a, float *probs, uint32_t *keep, hipStre
                             void *const *ev, int nev, const SideStreams *sd)
 {
     hipError_t e;
-    if (ev && (e = hipEventRecord((hipEvent_t)ev[0], st)) != hipSuccess) return e;
     const unsigned B = (unsigned)a.L.B;
     const bool tp32 = DT == F32 && (kinds & MIS_KIND_TOPP32);
     const bool others = (kinds & MIS_KIND_OTHER) != 0u;
     const bool side = tp32 && others && sd != nullptr;
     if (tp32) hipLaunchKernelGGL(k_rows, dim3(1), dim3(NT), 0, st, a);
+    // events[0] opens the chunk pass: after k_rows, which only orders the rows
+    if (ev && (e = hipEventRecord((hipEvent_t)ev[0], st)) != hipSuccess) return e;
     if (side) {
         if ((e = hipEventRecord(sd->fork, st)) != hipSuccess) return e;
         if ((e = hipStreamWaitEvent(sd->s, sd->fork, 0)) != hipSuccess) return e;
