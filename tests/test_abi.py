@@ -11,13 +11,15 @@ import sys
 import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADER = os.path.join(ROOT, "include", "mis_sampler.h")
+HEADERS = [os.path.join(ROOT, "include", h) for h in ("mis_sampler.h", "mis_attention.h")]
 
 
 def declared_functions() -> list[str]:
-    src = open(HEADER).read()
-    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
-    return re.findall(r"\b(mis_\w+)\s*\(", src)
+    names = []
+    for h in HEADERS:
+        src = re.sub(r"/\*.*?\*/", "", open(h).read(), flags=re.S)
+        names += re.findall(r"\b(mis_\w+)\s*\(", src)
+    return names
 
 
 @pytest.fixture(scope="module")
@@ -114,6 +116,22 @@ def test_argument_validation_without_gpu(lib):
     assert lib.mis_fill_uniforms(None, fake, 4, None) == 1
     assert lib.mis_fill_uniforms(fake, None, 4, None) == 1
     assert lib.mis_fill_uniforms(fake, fake, 1 << 31, None) == 4
+    # paged attention: shapes and pointers checked before any launch
+    pa = lambda *a: lib.mis_paged_attention(*a)
+    ok = (vp(0x1000), 64, 16, 4, 64, 2 * 16 * 4 * 64, 16 * 4 * 64, fake, fake, fake, fake, 8, fake, fake, 2, 32,
+          fake, None, 0, None)
+    assert pa(*ok[:14], 0, *ok[15:]) == 0                                  # empty batch
+    assert pa(*ok[:3], 0, *ok[4:]) == 1                                    # n_kv_heads 0
+    assert pa(*ok[:4], 96, *ok[5:]) == 4                                   # d_k 96
+    assert pa(*ok[:15], 30, *ok[16:]) == 4                                 # 30 heads over 4 KV heads
+    assert pa(*ok[:15], 128, *ok[16:]) == 4                                # 32 query heads per KV head
+    assert pa(None, *ok[1:]) == 1
+    assert pa(vp(0x1002), *ok[1:]) == 1                                    # pool not 16-byte aligned
+    long_ctx = (*ok[:11], 64, *ok[12:])                                    # 1024 tokens: splits need a workspace
+    assert pa(*long_ctx) == 2
+    assert lib.mis_paged_attention_workspace_bytes(2, 32, 64, 256) == 256
+    assert lib.mis_paged_attention_workspace_bytes(2, 32, 64, 1024) >= 2 * 32 * 4 * (64 + 2) * 4
+    assert lib.mis_gather_kv(fake, 64, 16, 4, 64, 4096, 2048, fake, 8, fake, 2, 129, fake, fake, None) == 1
 
 
 def test_product_path_fails_loudly_without_library(tmp_path):
