@@ -39,9 +39,11 @@ enum {
     MIS_ATT_ERR_UNSUPPORTED = 4    /* d_k not 64 / 128 / 256, n_heads / n_kv_heads above 16 or not whole */
 };
 
-/* Bytes of device workspace mis_paged_attention() needs (contexts longer than
- * 256 tokens are split over workgroups and merged). */
-size_t mis_paged_attention_workspace_bytes(int64_t B, int n_heads, int d_k, int max_context);
+/* Bytes of device workspace mis_paged_attention() needs for a call of B
+ * sequences and max_context = max_blocks * block_size tokens (contexts are
+ * split over workgroups of 64-256 tokens and merged; one split needs none,
+ * and 256 is returned). */
+size_t mis_paged_attention_workspace_bytes(int64_t B, int n_heads, int n_kv_heads, int d_k, int max_context);
 
 /*
  * One decode step of attention for B sequences: writes new_k / new_v

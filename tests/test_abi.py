@@ -127,11 +127,15 @@ def test_argument_validation_without_gpu(lib):
     assert pa(*ok[:15], 128, *ok[16:]) == 4                                # 32 query heads per KV head
     assert pa(None, *ok[1:]) == 1
     assert pa(vp(0x1002), *ok[1:]) == 1                                    # pool not 16-byte aligned
+    assert pa(*ok[:9], vp(0x1008), *ok[10:]) == 1                          # queries not 16-byte aligned
     long_ctx = (*ok[:11], 64, *ok[12:])                                    # 1024 tokens: splits need a workspace
     assert pa(*long_ctx) == 2
-    assert lib.mis_paged_attention_workspace_bytes(2, 32, 64, 256) == 256
-    assert lib.mis_paged_attention_workspace_bytes(2, 32, 64, 1024) >= 2 * 32 * 4 * (64 + 2) * 4
-    assert lib.mis_gather_kv(fake, 64, 16, 4, 64, 4096, 2048, fake, 8, fake, 2, 129, fake, fake, None) == 1
+    # splits of 64 tokens for a small batch, 256 once the grid is full without them
+    assert lib.mis_paged_attention_workspace_bytes(2, 32, 4, 64, 64) == 256
+    assert lib.mis_paged_attention_workspace_bytes(2, 32, 4, 64, 1024) == 2 * 32 * 16 * (64 + 2) * 4
+    assert lib.mis_paged_attention_workspace_bytes(256, 32, 8, 128, 2048) == 256 * 32 * 8 * (128 + 2) * 4
+    assert lib.mis_gather_kv(fake, 64, 16, 4, 64, 4096, 2048, fake, 8, fake, 2, -1, fake, fake, None) == 1
+    assert lib.mis_gather_kv(fake, 64, 16, 4, 64, 4096, 2048, fake, 8, fake, -2, 16, fake, fake, None) == 1
 
 
 def test_product_path_fails_loudly_without_library(tmp_path):

@@ -24,6 +24,9 @@ SHAPES = {  # (n_heads, n_kv_heads, d_k)
     "llama8b": (32, 8, 128),
     "mha256": (8, 8, 256),
     "gqa16": (16, 1, 64),
+    "g8": (64, 8, 128),
+    "g3": (12, 4, 128),
+    "g16d256": (16, 1, 256),
 }
 
 
@@ -60,6 +63,15 @@ def test_attention_split_contexts(shape, device):
     and the merge; lengths around the split boundaries."""
     n_heads, n_kv, dk = SHAPES[shape]
     _run(shape + " long", device, n_heads, n_kv, dk, [257, 511, 512, 513, 1000, 2048, 3, 4093], seed=2)
+
+
+@pytest.mark.parametrize("B,ctx", [(8, 700), (16, 1500), (64, 1024)])
+def test_attention_split_sizes(B, ctx, device):
+    """Splits of 64, 128 and 256 tokens (the split shrinks while the grid is
+    small): random lengths up to ctx over llama8b's shape."""
+    lens = [int(x) for x in np.random.default_rng(B).integers(1, ctx + 1, B)]
+    lens[0] = ctx
+    _run(f"split B={B} ctx={ctx}", device, 32, 8, 128, lens, seed=B)
 
 
 def test_attention_block_size_and_batch(device):

@@ -63,7 +63,7 @@ def load():
     lib.mis_fill_uniforms.argtypes = [vp, vp, i64, vp]
     lib.mis_fill_uniforms.restype = ctypes.c_int
     ci = ctypes.c_int
-    lib.mis_paged_attention_workspace_bytes.argtypes = [i64, ci, ci, ci]
+    lib.mis_paged_attention_workspace_bytes.argtypes = [i64, ci, ci, ci, ci]
     lib.mis_paged_attention_workspace_bytes.restype = ctypes.c_size_t
     lib.mis_paged_attention.argtypes = [vp, i64, ci, ci, ci, i64, i64, vp, vp, vp, vp, ci, vp, vp, i64, ci, vp, vp,
                                         ctypes.c_size_t, vp]

@@ -60,7 +60,7 @@ def fused_attention_fast(pool: torch.Tensor, new_k: torch.Tensor, new_v: torch.T
         raise ValueError("new_k / new_v must be [B, n_kv_heads, d_k] and queries [B, n_heads, d_k]")
     out = torch.empty((B, n_heads, d_k), dtype=torch.float16, device=dev)
     max_blocks = bt.shape[1]
-    need = int(lib.mis_paged_attention_workspace_bytes(B, n_heads, d_k, max_blocks * block_size))
+    need = int(lib.mis_paged_attention_workspace_bytes(B, n_heads, n_kv_heads, d_k, max_blocks * block_size))
     idx = dev.index if dev.index is not None else torch.cuda.current_device()
     ws = _workspace.get(idx)
     if ws is None or ws.numel() < need:
