@@ -24,6 +24,16 @@ ops (oracle/faithful.py: one call per row, unstable sort, torch.multinomial),
 timed on a bounded sample of the same rows, on this host's cores.
 
 Prints one JSON line.
+
+--op attention measures the paged decode attention instead (config A1: a
+Llama-3-8B-shaped layer, 32 query / 8 KV heads of 128, block size 16, 64
+sequences of 2048 tokens over a 537 MB fp16 pool with scattered blocks, larger
+than the Infinity Cache).  A step is one mis_paged_attention() call: the new
+K / V written, every head's attention over its sequence.  The roofline entry
+covers the call's two launches (the split pass and the merge), whose
+algorithmic bytes are the K and V rows read once plus queries, new K / V and
+outputs.  The CPU baseline is oracle/attention.py (numpy float64) on a sample
+of the sequences.
 """
 from __future__ import annotations
 
@@ -62,6 +72,8 @@ def parse():
     ap.add_argument("--row-params", default=None, metavar="T,k,p",
                     help="give every row this temperature, top_k and top_p (one row mode at a time, for per-mode "
                          "counters); the default keeps the config's own per-row mix")
+    ap.add_argument("--op", default="sample", choices=["sample", "attention"],
+                    help="sample: the sampler (configs C1-C5); attention: the paged decode attention (config A1)")
     ap.add_argument("--copy-calib-mib", type=int, default=0,
                     help="after the timed steps, run 5 plain device copies of this many MiB (calibrates "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE against known bytes)")
@@ -123,6 +135,91 @@ def cpu_baseline(w, nrows: int, steps: int) -> dict:
             "p50_ms_per_sample_step": round(p50 * 1e3, 3), "cpu_model": model}
 
 
+ATT_A1 = {"B": 64, "n_heads": 32, "n_kv_heads": 8, "d_k": 128, "block_size": 16, "context": 2048}
+
+
+def bench_attention(args):
+    """Paged decode attention, config A1 (see the module docstring)."""
+    import numpy as np
+    import torch
+    from vllm_mps_amd import attention as VA
+
+    c = ATT_A1
+    B, H, KV, D, bs, ctx = c["B"], c["n_heads"], c["n_kv_heads"], c["d_k"], c["block_size"], c["context"]
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    mb = ctx // bs
+    nb = B * mb + 1
+    g = torch.Generator(device="cpu").manual_seed(1)
+    pool = torch.randn(nb, 2, bs, KV, D, generator=g).half().to(dev)
+    bt = torch.randperm(nb - 1, generator=g)[:B * mb].view(B, mb).int().to(dev)
+    sl = torch.full((B,), ctx, dtype=torch.int32, device=dev)
+    wi = torch.stack([bt[:, (ctx - 1) // bs], torch.full((B,), (ctx - 1) % bs, dtype=torch.int32, device=dev)],
+                     1).int().contiguous()
+    q = torch.randn(B, H, D, generator=g).half().to(dev)
+    nk = torch.randn(B, KV, D, generator=g).half().to(dev)
+    nv = torch.randn(B, KV, D, generator=g).half().to(dev)
+    call = lambda: VA.fused_attention_fast(pool, nk, nv, q, bt, sl, wi, H, KV, D, bs)
+    for _ in range(args.warmup):
+        call()
+    torch.cuda.synchronize()
+    K = args.steps
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(K)]
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for i in range(K):
+        evs[i][0].record()
+        call()
+        evs[i][1].record()
+    end.record()
+    torch.cuda.synchronize()
+    total_ms = start.elapsed_time(end)
+    call_us = [a.elapsed_time(b) * 1e3 for a, b in evs]
+    mean_us = statistics.mean(call_us)
+    kv_bytes = B * ctx * KV * D * 2 * 2
+    alg = kv_bytes + B * H * D * 2 * 2 + B * KV * D * 2 * 2   # K/V rows read, queries and outputs, new K/V written
+    achieved = alg / (mean_us / 1e6) / 1e9
+    res = {
+        "metric": "paged decode attention: sequences/s per layer + KV GB/s (% of peak)",
+        "value": round(B * K / (total_ms / 1e3), 1),
+        "unit": "sequences/s",
+        "n_gpus": 1, "steps": K, "warmup": args.warmup,
+        "ms_per_step": round(total_ms / K, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f16 (fp32 arithmetic)", "data": "synthetic",
+        "config": {"workload": "A1 Llama-3-8B-shaped decode attention layer, scattered 16-token blocks", **c,
+                   "pool_bytes": pool.numel() * 2},
+        "p50_us_per_step": round(statistics.median(call_us), 2),
+        "roofline": {"bound": "hbm", "kernel": "k_attn_split + k_attn_merge (one call)",
+                     "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "algorithmic_bytes_per_launch": alg, "mean_launch_us": round(mean_us, 2)},
+    }
+    if args.cpu_rows > 0:
+        from oracle import attention as A
+        ns = min(args.cpu_rows, 8, B)
+        sel = np.linspace(0, B - 1, ns).round().astype(int)
+        pool_h = pool.cpu().numpy()
+        bt_h, sl_h, wi_h = bt.cpu().numpy()[sel], sl.cpu().numpy()[sel], wi.cpu().numpy()[sel]
+        q_h, nk_h, nv_h = q.cpu().numpy()[sel], nk.cpu().numpy()[sel], nv.cpu().numpy()[sel]
+        from threadpoolctl import threadpool_limits
+        times = []
+        with threadpool_limits(limits=1):
+            for it in range(1 + args.cpu_steps):
+                t0 = time.perf_counter()
+                A.paged_attention(pool_h, nk_h, nv_h, q_h, bt_h, sl_h, wi_h, H)
+                if it >= 1:
+                    times.append(time.perf_counter() - t0)
+        p50 = statistics.median(times)
+        res["cpu_baseline"] = {"value": round(ns / p50, 2), "unit": "sequences/s", "cores": 1, "kind": "port",
+                               "sample": f"{ns} of {B} A1 sequences (evenly spaced), oracle/attention.py numpy "
+                                         f"float64, p50 of {args.cpu_steps} calls after 1 warmup"}
+    else:
+        res["cpu_baseline"] = None
+    print(json.dumps(res), flush=True)
+
+
 def main():
     args = parse()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -131,6 +228,9 @@ def main():
               "rows are independent, so N GPUs would each run this single-GPU step on B/N rows.",
               file=sys.stderr)
         sys.exit(2)
+    if args.op == "attention":
+        bench_attention(args)
+        return
 
     import torch
     from vllm_mps_amd import workloads as W

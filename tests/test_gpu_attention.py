@@ -74,8 +74,12 @@ def test_attention_split_sizes(B, ctx, device):
     _run(f"split B={B} ctx={ctx}", device, 32, 8, 128, lens, seed=B)
 
 
-def test_attention_block_size_and_batch(device):
-    _run("bs32 B=40", device, 32, 8, 128, list(np.random.default_rng(4).integers(1, 700, 40)), bs=32, seed=4)
+@pytest.mark.parametrize("bs", [32, 8, 24])
+def test_attention_block_size_and_batch(bs, device):
+    """Block sizes: 32 (whole 16-token tiles in a block), 8 and 24 (tiles
+    across blocks; 24 is no power of two)."""
+    lens = [int(x) for x in np.random.default_rng(4).integers(1, 700, 40)]
+    _run(f"bs{bs} B=40", device, 32, 8, 128, lens, bs=bs, seed=4)
 
 
 def test_gather_bit_exact(device):

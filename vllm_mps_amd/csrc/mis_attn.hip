@@ -59,6 +59,7 @@ struct AttnArgs {
     float *part;                     // [B, n_heads, nsplit, D] unnormalised outputs
     float *pm, *pl;                  // [B, n_heads, nsplit] split max and sum
     int nsplit, ts;
+    int bs_shift;                    // log2(block_size) for a power of two, else -1
     float scale;
 };
 
@@ -79,39 +80,50 @@ __device__ __forceinline__ void h8_to_f(const uint4 &r, float *f)
     }
 }
 
-// Physical block of token t (clamped into the pool: an id outside it is the
-// caller's error, never an access outside the buffer).
-__device__ __forceinline__ int block_of(const AttnArgs &a, int b, int t)
-{
-    const int pb = a.block_tables[(int64_t)b * a.max_blocks + t / a.block_size];
-    return pb < 0 ? 0 : (pb >= a.num_blocks ? (int)(a.num_blocks - 1) : pb);
-}
-
-template <int D, int GM>
+template <int D, int GM, bool FAST>
 __global__ __launch_bounds__(ATT_NT) void k_attn_split(AttnArgs a)
 {
     constexpr int NW = ATT_NW;
     constexpr int QV = D / 32;                 // 16-byte K loads per lane per tile (a quarter row)
     constexpr int NM = D / 16;                 // MFMAs per tile
-    constexpr int TPI = D == 256 ? 2 : 4;      // tiles in flight per wave
-    constexpr int DG = D / 8, TSW = 64 / DG;   // values phase: dim groups, tokens per wave step
-    constexpr int U = D == 256 ? 4 : 8;        // values phase: tokens in flight per lane
-    // LDS sized by the call's group G: probabilities [G][ATT_TS], per-wave
-    // reductions [G][NW], split max [G], output sum [G][D], block ids [ATT_TS]
+    constexpr int KT = D == 256 ? 2 : 4;       // tiles per batch of K loads
+    constexpr int DG = D / 8, TSW = 64 / DG;   // values: dim groups of 8, tokens per wave step
+    constexpr int SPT = 16 / TSW;              // value steps per tile
+    constexpr int SMAX = 4 * SPT;              // value steps per wave (at most 4 tiles)
+    constexpr int VR = (D == 256 || GM == 16) ? 8 : 16;  // value loads in flight per lane
+    constexpr int VB = SMAX < VR ? SMAX : VR;
+    // LDS sized by the call's group G: probabilities [NW][G][64] (a wave's own
+    // tokens), wave max and sum [NW][G] each, output sum [G][D], the split's
+    // block ids [ATT_TS + 1]
     extern __shared__ float smem[];
     const int G = a.G;
-    float *const pr = smem;
-    float *const red = pr + G * ATT_TS;
-    float *const mx = red + G * NW;
-    float *const acc = mx + G;
+    float *const pw = smem;
+    float *const wmx = pw + NW * G * 64;
+    float *const wsum = wmx + NW * G;
+    float *const acc = wsum + NW * G;
     int *const pbl = reinterpret_cast<int *>(acc + G * D);
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const int split = blockIdx.x % a.nsplit;
-    const int hk = (blockIdx.x / a.nsplit) % a.n_kv;
+    // the KV heads of one (sequence, split) are neighbours in the grid: they
+    // read the same pool blocks (a token's heads share one contiguous row)
+    const int hk = blockIdx.x % a.n_kv;
+    const int split = (blockIdx.x / a.n_kv) % a.nsplit;
     const int b = blockIdx.x / (a.nsplit * a.n_kv);
+    const int bs = a.block_size, t0 = split * a.ts;
+    // the block ids of the split's whole range, clamped into the pool (an id
+    // outside it is the caller's error, never an access outside the buffer);
+    // loaded before the length is known, so the two loads overlap
+    const int blk0 = a.bs_shift >= 0 ? t0 >> a.bs_shift : t0 / bs;
+    {
+        const int last = t0 + a.ts - 1;
+        const int nblk = min(a.bs_shift >= 0 ? last >> a.bs_shift : last / bs, a.max_blocks - 1) - blk0 + 1;
+        for (int i = tid; i < nblk; i += ATT_NT) {
+            const int pb = a.block_tables[(int64_t)b * a.max_blocks + blk0 + i];
+            pbl[i] = pb < 0 ? 0 : (pb >= a.num_blocks ? (int)(a.num_blocks - 1) : pb);
+        }
+    }
     // lengths beyond the block table are clamped to it
     const int L = min(max(a.seq_lens[b], 0), a.max_blocks * a.block_size);
-    const int t0 = split * a.ts, t1 = min(t0 + a.ts, L), n = t1 - t0;
+    const int t1 = min(t0 + a.ts, L), n = t1 - t0;
     if (n <= 0 && a.nsplit > 1) return;        // past the sequence: the merge reads no such split
     const int64_t hoff = (int64_t)hk * D;      // the KV head within a token's row
     const int64_t rowst = (int64_t)a.n_kv * D; // token stride within a block
@@ -120,12 +132,12 @@ __global__ __launch_bounds__(ATT_NT) void k_attn_split(AttnArgs a)
     const __half *nv = a.new_v + ((int64_t)b * a.n_kv + hk) * D;
     if (n > 0 && L - 1 < t1) {
         const int wb = a.write_info[2 * b], wp = a.write_info[2 * b + 1];
-        if (wb >= 0 && wb < a.num_blocks && wp >= 0 && wp < a.block_size) {
+        if (wb >= 0 && wb < a.num_blocks && wp >= 0 && wp < bs) {
             __half *dk = a.pool + (int64_t)wb * a.s0 + wp * rowst + hoff;
             for (int d = tid; d < D; d += ATT_NT) { dk[d] = nk[d]; dk[a.s1 + d] = nv[d]; }
         }
     }
-    // scores.  Lane l: query head / token column l % 16, quarter l / 16 of the dims.
+    // scores: lane l is query head / token column l % 16 and quarter l / 16 of the dims
     const int col = lane & 15, qd = lane >> 4;
     half4_t qa[NM];
     {
@@ -142,112 +154,145 @@ __global__ __launch_bounds__(ATT_NT) void k_attn_split(AttnArgs a)
         for (int m = 0; m < NM; ++m)
             qa[m] = (m & 1) ? half4_of(r[m >> 1].z, r[m >> 1].w) : half4_of(r[m >> 1].x, r[m >> 1].y);
     }
+    __syncthreads();
+    // wave w owns tiles w, w + NW, w + 2 NW, w + 3 NW of 16 tokens.  A lane
+    // whose token is past the split's end reads the tile's last token instead
+    // (its score is masked and its values zeroed); the newest token is read
+    // from the inputs.
     const int ntiles = (n + 15) >> 4;
-    for (int j0 = w * TPI; j0 < ntiles; j0 += NW * TPI) {
-        uint4 kr[TPI][QV];
+    const int inew = L - 1 >= t0 && L - 1 < t1 ? L - 1 - t0 : -1;
+    const __half *tb[4];                       // FAST: tile j's K rows (the tile lies in one block)
+    if constexpr (FAST) {
 #pragma unroll
-        for (int jj = 0; jj < TPI; ++jj) {
-            const int i = (j0 + jj) * 16 + col, t = t0 + i;
-            if (i < n) {
-                const __half *kp;
-                if (t == L - 1) {
-                    kp = nk;
-                } else {
-                    const int pb = block_of(a, b, t);
-                    kp = a.pool + (int64_t)pb * a.s0 + (t % a.block_size) * rowst + hoff;
-                }
-                if (qd == 0) pbl[i] = t == L - 1 ? -1 : block_of(a, b, t);
-                kp += qd * (D / 4);
-#pragma unroll
-                for (int v = 0; v < QV; ++v) kr[jj][v] = reinterpret_cast<const uint4 *>(kp)[v];
-            } else {
-#pragma unroll
-                for (int v = 0; v < QV; ++v) kr[jj][v] = make_uint4(0u, 0u, 0u, 0u);
-            }
-        }
-#pragma unroll
-        for (int jj = 0; jj < TPI; ++jj) {
-            if (j0 + jj >= ntiles) continue;   // wave-uniform
-            float4_t c = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int m = 0; m < NM; ++m) {
-                const uint4 &r = kr[jj][m >> 1];
-                const half4_t kb = (m & 1) ? half4_of(r.z, r.w) : half4_of(r.x, r.y);
-                c = __builtin_amdgcn_mfma_f32_16x16x16f16(qa[m], kb, c, 0, 0, 0);
-            }
-            // c[r]: query head 4 * qd + r, token (j0 + jj) * 16 + col
-            const int i = (j0 + jj) * 16 + col;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int g = 4 * qd + r;
-                if (g < G) pr[g * ATT_TS + i] = i < n ? c[r] * a.scale : -INFINITY;
-            }
+        for (int q = 0; q < 4; ++q) {
+            const int j = w + NW * q, tok0 = t0 + 16 * j;
+            const int pb = j < ntiles ? __builtin_amdgcn_readfirstlane(pbl[(tok0 >> a.bs_shift) - blk0]) : 0;
+            tb[q] = a.pool + (int64_t)pb * a.s0 + (int64_t)(tok0 & (bs - 1)) * rowst + hoff;
         }
     }
-    __syncthreads();
-    // softmax per query head over the split: max, then exp and sum
-    for (int g = 0; g < G; ++g) {
-        float v = tid < n ? pr[g * ATT_TS + tid] : -INFINITY;
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-        if (lane == 0) red[g * NW + w] = v;
-    }
-    __syncthreads();
-    if (tid < G) {
-        float m = red[tid * NW];
-#pragma unroll
-        for (int i = 1; i < NW; ++i) m = fmaxf(m, red[tid * NW + i]);
-        mx[tid] = m;
-    }
-    __syncthreads();
-    for (int g = 0; g < G; ++g) {
-        const float e = tid < n ? __expf(pr[g * ATT_TS + tid] - mx[g]) : 0.0f;
-        if (tid < n) pr[g * ATT_TS + tid] = e;
-        float v = e;
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-        if (lane == 0) red[g * NW + w] = v;
-    }
-    __syncthreads();
-    // weighted V sum: lane = (token sub, dim group); wave w, step k takes
-    // tokens (k * NW + w) * TSW + sub
+    // the K (kv = 0) or V (kv = 1) row of token 16 j + loc of the wave's tile q
+    auto row_ptr = [&](int q, int loc, int kv) -> const __half * {
+        const int j = w + NW * q;
+        const int c2 = min(loc, n - 16 * j - 1);
+        const __half *p;
+        if constexpr (FAST) {
+            p = tb[q] + c2 * (int)rowst + (kv ? a.s1 : 0);
+        } else {
+            const int t = t0 + 16 * j + c2;
+            const int qb = a.bs_shift >= 0 ? t >> a.bs_shift : t / bs;
+            p = a.pool + (int64_t)pbl[qb - blk0] * a.s0 + (int64_t)(t - qb * bs) * rowst + hoff + (kv ? a.s1 : 0);
+        }
+        if (inew >= 16 * j && inew < 16 * j + 16) {   // wave-uniform
+            if (16 * j + c2 == inew) p = kv ? nv : nk;
+        }
+        return p;
+    };
+    // values: lane = (token sub, dim group); step s of the wave takes token
+    // (s % SPT) TSW + sub of its tile s / SPT
     const int dg = lane % DG, sub = lane / DG;
+    auto load_v = [&](int s) -> uint4 {
+        const int q = s / SPT, j = w + NW * q, loc = (s % SPT) * TSW + sub;
+        if (j >= ntiles) return make_uint4(0u, 0u, 0u, 0u);   // wave-uniform
+        uint4 r = reinterpret_cast<const uint4 *>(row_ptr(q, loc, 1))[dg];
+        if (n - 16 * j < 16) {                 // wave-uniform: the split's last, partial tile
+            if (loc >= n - 16 * j) r = make_uint4(0u, 0u, 0u, 0u);
+        }
+        return r;
+    };
+    float4_t c[4];
+    uint4 vr[VB];
+#pragma unroll
+    for (int kb = 0; kb < 4; kb += KT) {
+        uint4 kr[KT][QV];
+#pragma unroll
+        for (int q = 0; q < KT; ++q) {
+            if (w + NW * (kb + q) < ntiles) {  // wave-uniform
+                const __half *kp = row_ptr(kb + q, col, 0) + qd * (D / 4);
+#pragma unroll
+                for (int v = 0; v < QV; ++v) kr[q][v] = reinterpret_cast<const uint4 *>(kp)[v];
+            }
+        }
+        if (kb == 0) {                         // the first values in flight with the keys
+#pragma unroll
+            for (int u = 0; u < VB; ++u) vr[u] = load_v(u);
+        }
+#pragma unroll
+        for (int q = 0; q < KT; ++q) {
+            float4_t cc = {0.0f, 0.0f, 0.0f, 0.0f};
+            if (w + NW * (kb + q) < ntiles) {  // wave-uniform
+#pragma unroll
+                for (int m = 0; m < NM; ++m) {
+                    const uint4 &r = kr[q][m >> 1];
+                    const half4_t kv = (m & 1) ? half4_of(r.z, r.w) : half4_of(r.x, r.y);
+                    cc = __builtin_amdgcn_mfma_f32_16x16x16f16(qa[m], kv, cc, 0, 0, 0);
+                }
+            }
+            c[kb + q] = cc;
+        }
+    }
+    // the wave's softmax: c[q][r] is query head 4 qd + r, token 16 (w + NW q) + col
+    float mloc[4], lsum[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        float m = -INFINITY;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            if (16 * (w + NW * q) + col < n) m = fmaxf(m, c[q][r] * a.scale);
+#pragma unroll
+        for (int o = 1; o < 16; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+        mloc[r] = m;
+        lsum[r] = 0.0f;
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const bool ok = 16 * (w + NW * q) + col < n;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const float e = ok ? __expf(c[q][r] * a.scale - mloc[r]) : 0.0f;
+            lsum[r] += e;
+            const int g = 4 * qd + r;
+            if (g < G) pw[(w * G + g) * 64 + 16 * q + col] = e;
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+#pragma unroll
+        for (int o = 1; o < 16; o <<= 1) lsum[r] += __shfl_xor(lsum[r], o, 64);
+        const int g = 4 * qd + r;
+        if (col == 0 && g < G) { wmx[w * G + g] = mloc[r]; wsum[w * G + g] = lsum[r]; }
+    }
+    __syncthreads();
+    // weighted V sum of the wave's tokens
     float o[GM][8];
 #pragma unroll
     for (int g = 0; g < GM; ++g)
 #pragma unroll
         for (int e = 0; e < 8; ++e) o[g][e] = 0.0f;
-    for (int i0 = w * TSW + sub; i0 < n; i0 += NW * TSW * U) {
-        uint4 vr[U];
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int i = i0 + u * NW * TSW;
-            if (i < n) {
-                const int pb = pbl[i];
-                const __half *vp = pb < 0 ? nv
-                                          : a.pool + (int64_t)pb * a.s0 + a.s1 + ((t0 + i) % a.block_size) * rowst + hoff;
-                vr[u] = reinterpret_cast<const uint4 *>(vp)[dg];
-            } else {
-                vr[u] = make_uint4(0u, 0u, 0u, 0u);
-            }
+    for (int s0 = 0; s0 < SMAX; s0 += VB) {
+        if (w + NW * (s0 / SPT) >= ntiles) break;   // wave-uniform
+        if (s0 > 0) {
+#pragma unroll
+            for (int u = 0; u < VB; ++u) vr[u] = load_v(s0 + u);
         }
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int i = i0 + u * NW * TSW;
-            if (i < n) {
+        for (int u = 0; u < VB; ++u) {
+            const int s = s0 + u, q = s / SPT, li = 16 * q + (s % SPT) * TSW + sub;
+            if (w + NW * q < ntiles) {         // wave-uniform; tokens past the end carry p = 0, V = 0
                 float v[8];
                 h8_to_f(vr[u], v);
 #pragma unroll
                 for (int g = 0; g < GM; ++g)
                     if (g < G) {
-                        const float pg = pr[g * ATT_TS + i];
+                        const float pg = pw[(w * G + g) * 64 + li];
 #pragma unroll
                         for (int e = 0; e < 8; ++e) o[g][e] = fmaf(pg, v[e], o[g][e]);
                     }
             }
         }
     }
-    // lanes sharing a dim group, then the waves one at a time
+    // lanes sharing a dim group, then the waves one at a time, each rescaled
+    // from its own max to the split's
 #pragma unroll
     for (int sft = DG; sft < 64; sft <<= 1)
 #pragma unroll
@@ -259,50 +304,97 @@ __global__ __launch_bounds__(ATT_NT) void k_attn_split(AttnArgs a)
         if (w == k && sub == 0) {
 #pragma unroll
             for (int g = 0; g < GM; ++g)
-                if (g < G)
+                if (g < G) {
+                    float M = wmx[g];
+#pragma unroll
+                    for (int x = 1; x < NW; ++x) M = fmaxf(M, wmx[x * G + g]);
+                    const float mw = wmx[k * G + g];
+                    const float sc = mw == -INFINITY ? 0.0f : __expf(mw - M);
 #pragma unroll
                     for (int e = 0; e < 8; ++e) {
-                        float *const c = &acc[g * D + dg * 8 + e];
-                        *c = k == 0 ? o[g][e] : *c + o[g][e];
+                        float *const cp = &acc[g * D + dg * 8 + e];
+                        *cp = k == 0 ? sc * o[g][e] : fmaf(sc, o[g][e], *cp);
                     }
+                }
         }
         __syncthreads();
     }
-    // write the split (or, with one split, the output); red holds the per-wave sums
+    // write the split (or, with one split, the output)
     for (int i = tid; i < G * D; i += ATT_NT) {
-        const float v = acc[i];
         const int g = i / D, d = i % D;
+        float M = wmx[g];
+#pragma unroll
+        for (int x = 1; x < NW; ++x) M = fmaxf(M, wmx[x * G + g]);
         float l = 0.0f;
 #pragma unroll
-        for (int k = 0; k < NW; ++k) l += red[g * NW + k];
+        for (int x = 0; x < NW; ++x) {
+            const float mw = wmx[x * G + g];
+            if (mw != -INFINITY) l = fmaf(__expf(mw - M), wsum[x * G + g], l);
+        }
+        const float v = acc[i];
         const int hq = hk * G + g;
         if (a.nsplit == 1) {
             a.out[((int64_t)b * a.n_heads + hq) * D + d] = __float2half(n > 0 ? v / l : 0.0f);
         } else {
             const int64_t ps = ((int64_t)b * a.n_heads + hq) * a.nsplit + split;
             a.part[ps * D + d] = v;
-            if (d == 0) { a.pm[ps] = mx[g]; a.pl[ps] = l; }
+            if (d == 0) { a.pm[ps] = M; a.pl[ps] = l; }
         }
     }
 }
 
-// One workgroup per (sequence, query head): the splits' max-rescaled sum.
+// One wave per (sequence, query head): the splits' max-rescaled sum.  Lanes
+// take splits for the max and the weights exp(m_s - M), which the wave then
+// shares by shuffles while each lane sums its dims over the splits.
 template <int D>
-__global__ __launch_bounds__(ATT_NT) void k_attn_merge(AttnArgs a)
+__global__ __launch_bounds__(ATT_NT) void k_attn_merge(AttnArgs a, int64_t pairs)
 {
-    const int hq = blockIdx.x % a.n_heads, b = blockIdx.x / a.n_heads;
+    constexpr int DPL = D / 64;
+    const int lane = threadIdx.x & 63;
+    const int64_t pair = (int64_t)blockIdx.x * ATT_NW + (threadIdx.x >> 6);
+    if (pair >= pairs) return;                 // whole waves
+    const int64_t b = pair / a.n_heads;
     const int L = min(max(a.seq_lens[b], 0), a.max_blocks * a.block_size);
     const int ns = min(a.nsplit, (L + a.ts - 1) / a.ts);
-    const int64_t base = ((int64_t)b * a.n_heads + hq) * a.nsplit;
+    const int64_t base = pair * a.nsplit;
     float M = -INFINITY;
-    for (int s = 0; s < ns; ++s) M = fmaxf(M, a.pm[base + s]);
-    float Ls = 0.0f;
-    for (int s = 0; s < ns; ++s) Ls += a.pl[base + s] * __expf(a.pm[base + s] - M);
-    for (int d = threadIdx.x; d < D; d += ATT_NT) {
-        float v = 0.0f;
-        for (int s = 0; s < ns; ++s) v += a.part[(base + s) * D + d] * __expf(a.pm[base + s] - M);
-        a.out[((int64_t)b * a.n_heads + hq) * D + d] = __float2half(ns > 0 ? v / Ls : 0.0f);
+    for (int s = lane; s < ns; s += 64) M = fmaxf(M, a.pm[base + s]);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
+    float Ls = 0.0f, v[DPL];
+#pragma unroll
+    for (int j = 0; j < DPL; ++j) v[j] = 0.0f;
+    for (int c0 = 0; c0 < ns; c0 += 64) {
+        const int s = c0 + lane;
+        const float wgt = s < ns ? __expf(a.pm[base + s] - M) : 0.0f;
+        if (s < ns) Ls += wgt * a.pl[base + s];
+        const int nk = min(64, ns - c0);
+        const float *pp = a.part + (base + c0) * D + lane;
+        int k = 0;
+        for (; k + 4 <= nk; k += 4) {
+            float x[4][DPL];
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+#pragma unroll
+                for (int j = 0; j < DPL; ++j) x[u][j] = pp[(int64_t)(k + u) * D + j * 64];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const float wk = __shfl(wgt, k + u, 64);
+#pragma unroll
+                for (int j = 0; j < DPL; ++j) v[j] = fmaf(wk, x[u][j], v[j]);
+            }
+        }
+        for (; k < nk; ++k) {
+            const float wk = __shfl(wgt, k, 64);
+#pragma unroll
+            for (int j = 0; j < DPL; ++j) v[j] = fmaf(wk, pp[(int64_t)k * D + j * 64], v[j]);
+        }
     }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) Ls += __shfl_xor(Ls, o, 64);
+#pragma unroll
+    for (int j = 0; j < DPL; ++j)
+        a.out[pair * D + j * 64 + lane] = __float2half(ns > 0 ? v[j] / Ls : 0.0f);
 }
 
 // The pool gather: one thread per (sequence, token, KV head, dim), zero past
@@ -331,10 +423,19 @@ __global__ __launch_bounds__(ATT_NT) void k_gather(const __half *pool, int64_t n
 template <int D, int GM>
 hipError_t launch_attn(const AttnArgs &a, int64_t B, hipStream_t st)
 {
-    // probabilities, reductions, max, output sum, block ids: at most 34 KiB
-    const size_t lds = ((size_t)a.G * (ATT_TS + ATT_NW + 1 + D) + ATT_TS) * sizeof(float);
-    hipLaunchKernelGGL((k_attn_split<D, GM>), dim3((unsigned)(B * a.n_kv * a.nsplit)), dim3(ATT_NT), lds, st, a);
-    if (a.nsplit > 1) hipLaunchKernelGGL((k_attn_merge<D>), dim3((unsigned)(B * a.n_heads)), dim3(ATT_NT), 0, st, a);
+    // FAST: block sizes that are powers of two from 16 up hold whole 16-token tiles
+    // probabilities, wave max and sum, output sum, block ids: at most 34 KiB
+    const size_t lds = ((size_t)a.G * (ATT_NW * 64 + 2 * ATT_NW + D) + ATT_TS + 1) * sizeof(float);
+    if (a.bs_shift >= 4)
+        hipLaunchKernelGGL((k_attn_split<D, GM, true>), dim3((unsigned)(B * a.n_kv * a.nsplit)), dim3(ATT_NT), lds, st, a);
+    else
+        hipLaunchKernelGGL((k_attn_split<D, GM, false>), dim3((unsigned)(B * a.n_kv * a.nsplit)), dim3(ATT_NT), lds, st,
+                           a);
+    if (a.nsplit > 1) {
+        const int64_t pairs = B * a.n_heads;
+        hipLaunchKernelGGL((k_attn_merge<D>), dim3((unsigned)((pairs + ATT_NW - 1) / ATT_NW)), dim3(ATT_NT), 0, st, a,
+                           pairs);
+    }
     return hipGetLastError();
 }
 
@@ -390,6 +491,7 @@ int mis_paged_attention(void *pool, int64_t num_blocks, int block_size, int n_kv
         return MIS_ATT_ERR_INVALID_ARG;  // 16-byte rows for the vector loads
     const int64_t max_context = (int64_t)max_blocks * block_size;
     if (max_context > (int64_t)1 << 24) return MIS_ATT_ERR_UNSUPPORTED;
+    if ((int64_t)block_size * n_kv_heads * d_k >= (int64_t)1 << 31) return MIS_ATT_ERR_UNSUPPORTED;  // 32-bit offsets in a block
     AttnArgs a;
     a.pool = reinterpret_cast<__half *>(pool);
     a.s0 = pool_stride0; a.s1 = pool_stride1; a.num_blocks = num_blocks;
@@ -403,6 +505,7 @@ int mis_paged_attention(void *pool, int64_t num_blocks, int block_size, int n_kv
     a.ts = split_tokens(B, n_kv_heads, max_context);
     a.nsplit = (int)((max_context + a.ts - 1) / a.ts);
     if (B * n_kv_heads * (int64_t)a.nsplit > 0x7fffffff) return MIS_ATT_ERR_UNSUPPORTED;
+    a.bs_shift = (block_size & (block_size - 1)) == 0 ? __builtin_ctz((unsigned)block_size) : -1;
     a.scale = 1.0f / sqrtf((float)d_k);
     a.part = nullptr; a.pm = nullptr; a.pl = nullptr;
     if (a.nsplit > 1) {
