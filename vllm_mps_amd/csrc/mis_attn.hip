@@ -69,18 +69,16 @@ __device__ __forceinline__ half4_t half4_of(unsigned int lo, unsigned int hi)
     return __builtin_bit_cast(half4_t, v);
 }
 
-__device__ __forceinline__ void h8_to_f(const uint4 &r, float *f)
+// Orders one wave's LDS writes before its later reads (and reads before later
+// writes): a wave's LDS operations complete in order, so a compiler barrier suffices.
+__device__ __forceinline__ void wave_lds_sync()
 {
-    const __half2 *h = reinterpret_cast<const __half2 *>(&r);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const float2 x = __half22float2(h[e]);
-        f[2 * e] = x.x;
-        f[2 * e + 1] = x.y;
-    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-template <int D, int GM, bool FAST>
+template <int D, bool FAST>
 __global__ __launch_bounds__(ATT_NT) void k_attn_split(AttnArgs a)
 {
     constexpr int NW = ATT_NW;
@@ -90,18 +88,22 @@ __global__ __launch_bounds__(ATT_NT) void k_attn_split(AttnArgs a)
     constexpr int DG = D / 8, TSW = 64 / DG;   // values: dim groups of 8, tokens per wave step
     constexpr int SPT = 16 / TSW;              // value steps per tile
     constexpr int SMAX = 4 * SPT;              // value steps per wave (at most 4 tiles)
-    constexpr int VR = (D == 256 || GM == 16) ? 8 : 16;  // value loads in flight per lane
+    constexpr int VR = D == 64 ? 16 : 8;       // value loads in flight per lane
     constexpr int VB = SMAX < VR ? SMAX : VR;
+    constexpr int TPB = VB / SPT;              // tiles per batch of value loads
+    constexpr int VST = D + 4;                 // LDS row stride of a staged V tile, halves (conflict-free reads)
     // LDS sized by the call's group G: probabilities [NW][G][64] (a wave's own
-    // tokens), wave max and sum [NW][G] each, output sum [G][D], the split's
-    // block ids [ATT_TS + 1]
+    // tokens), wave max and sum [NW][G] each, the split's block ids
+    // [ATT_TS + 1], each wave's staged V tile [16][VST] halves (the output sum
+    // [G][D] floats reuses that area once every wave is done with it)
     extern __shared__ float smem[];
     const int G = a.G;
     float *const pw = smem;
     float *const wmx = pw + NW * G * 64;
     float *const wsum = wmx + NW * G;
-    float *const acc = wsum + NW * G;
-    int *const pbl = reinterpret_cast<int *>(acc + G * D);
+    int *const pbl = reinterpret_cast<int *>(wsum + NW * G);
+    _Float16 *const vts = reinterpret_cast<_Float16 *>(pbl + ATT_TS + 4);
+    float *const acc = reinterpret_cast<float *>(vts);
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     // the KV heads of one (sequence, split) are neighbours in the grid: they
     // read the same pool blocks (a token's heads share one contiguous row)
@@ -113,7 +115,16 @@ __global__ __launch_bounds__(ATT_NT) void k_attn_split(AttnArgs a)
     // outside it is the caller's error, never an access outside the buffer);
     // loaded before the length is known, so the two loads overlap
     const int blk0 = a.bs_shift >= 0 ? t0 >> a.bs_shift : t0 / bs;
-    {
+    const int wu = __builtin_amdgcn_readfirstlane(w);
+    int pbt[4];                                // FAST: the block of each of the wave's tiles
+    if constexpr (FAST) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int blk = min((t0 + 16 * (wu + NW * q)) >> a.bs_shift, a.max_blocks - 1);
+            const int pb = a.block_tables[(int64_t)b * a.max_blocks + blk];
+            pbt[q] = pb < 0 ? 0 : (pb >= a.num_blocks ? (int)(a.num_blocks - 1) : pb);
+        }
+    } else {
         const int last = t0 + a.ts - 1;
         const int nblk = min(a.bs_shift >= 0 ? last >> a.bs_shift : last / bs, a.max_blocks - 1) - blk0 + 1;
         for (int i = tid; i < nblk; i += ATT_NT) {
@@ -154,7 +165,7 @@ __global__ __launch_bounds__(ATT_NT) void k_attn_split(AttnArgs a)
         for (int m = 0; m < NM; ++m)
             qa[m] = (m & 1) ? half4_of(r[m >> 1].z, r[m >> 1].w) : half4_of(r[m >> 1].x, r[m >> 1].y);
     }
-    __syncthreads();
+    if constexpr (!FAST) __syncthreads();      // the staged block ids
     // wave w owns tiles w, w + NW, w + 2 NW, w + 3 NW of 16 tokens.  A lane
     // whose token is past the split's end reads the tile's last token instead
     // (its score is masked and its values zeroed); the newest token is read
@@ -165,9 +176,8 @@ __global__ __launch_bounds__(ATT_NT) void k_attn_split(AttnArgs a)
     if constexpr (FAST) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            const int j = w + NW * q, tok0 = t0 + 16 * j;
-            const int pb = j < ntiles ? __builtin_amdgcn_readfirstlane(pbl[(tok0 >> a.bs_shift) - blk0]) : 0;
-            tb[q] = a.pool + (int64_t)pb * a.s0 + (int64_t)(tok0 & (bs - 1)) * rowst + hoff;
+            const int tok0 = t0 + 16 * (wu + NW * q);
+            tb[q] = a.pool + (int64_t)pbt[q] * a.s0 + (int64_t)(tok0 & (bs - 1)) * rowst + hoff;
         }
     }
     // the K (kv = 0) or V (kv = 1) row of token 16 j + loc of the wave's tile q
@@ -230,6 +240,12 @@ __global__ __launch_bounds__(ATT_NT) void k_attn_split(AttnArgs a)
             c[kb + q] = cc;
         }
     }
+    // the second batch of values in flight through the softmax (the keys' registers are free)
+    uint4 vr2[VB];
+    if constexpr (SMAX > VB) {
+#pragma unroll
+        for (int u = 0; u < VB; ++u) vr2[u] = load_v(VB + u);
+    }
     // the wave's softmax: c[q][r] is query head 4 qd + r, token 16 (w + NW q) + col
     float mloc[4], lsum[4];
 #pragma unroll
@@ -262,48 +278,71 @@ __global__ __launch_bounds__(ATT_NT) void k_attn_split(AttnArgs a)
         if (col == 0 && g < G) { wmx[w * G + g] = mloc[r]; wsum[w * G + g] = lsum[r]; }
     }
     __syncthreads();
-    // weighted V sum of the wave's tokens
-    float o[GM][8];
+    // weighted V sum on the matrix cores, one tile at a time: the wave stages
+    // the tile's V rows in LDS, then per 16 dims out[g][d] += P[g][k] V[k][d]
+    // over the 16 tokens k (v_mfma_f32_16x16x16_f16: A = P with the query
+    // heads as rows, B = V read back column-wise).  P is split into fp16
+    // hi + lo parts, both multiplied: hi + lo is within 2^-22 p of p and the
+    // fp16 products are exact, so the sum keeps fp32 accuracy.
+    _Float16 *const vt = vts + w * 16 * VST;
+    float4_t oacc[NM];
 #pragma unroll
-    for (int g = 0; g < GM; ++g)
+    for (int m = 0; m < NM; ++m) oacc[m] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    // one batch of VB value steps (TPB tiles) from registers
+    auto pv_batch = [&](const uint4 *vb_, int s0) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) o[g][e] = 0.0f;
+        for (int t = 0; t < TPB; ++t) {
+            const int q = s0 / SPT + t;
+            if (w + NW * q < ntiles) {         // wave-uniform
 #pragma unroll
-    for (int s0 = 0; s0 < SMAX; s0 += VB) {
-        if (w + NW * (s0 / SPT) >= ntiles) break;   // wave-uniform
-        if (s0 > 0) {
+                for (int k = 0; k < SPT; ++k) {
+                    const uint4 r = vb_[t * SPT + k];
+                    uint2 *dst = reinterpret_cast<uint2 *>(vt + (k * TSW + sub) * VST + dg * 8);
+                    dst[0] = make_uint2(r.x, r.y);
+                    dst[1] = make_uint2(r.z, r.w);
+                }
+                wave_lds_sync();
+                float4 pp = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                if (col < G) pp = *reinterpret_cast<const float4 *>(&pw[(w * G + col) * 64 + 16 * q + 4 * qd]);
+                const half4_t ph = {(_Float16)pp.x, (_Float16)pp.y, (_Float16)pp.z, (_Float16)pp.w};
+                const half4_t pl = {(_Float16)(pp.x - (float)ph[0]), (_Float16)(pp.y - (float)ph[1]),
+                                    (_Float16)(pp.z - (float)ph[2]), (_Float16)(pp.w - (float)ph[3])};
 #pragma unroll
-            for (int u = 0; u < VB; ++u) vr[u] = load_v(s0 + u);
-        }
-#pragma unroll
-        for (int u = 0; u < VB; ++u) {
-            const int s = s0 + u, q = s / SPT, li = 16 * q + (s % SPT) * TSW + sub;
-            if (w + NW * q < ntiles) {         // wave-uniform; tokens past the end carry p = 0, V = 0
-                float v[8];
-                h8_to_f(vr[u], v);
-#pragma unroll
-                for (int g = 0; g < GM; ++g)
-                    if (g < G) {
-                        const float pg = pw[(w * G + g) * 64 + li];
-#pragma unroll
-                        for (int e = 0; e < 8; ++e) o[g][e] = fmaf(pg, v[e], o[g][e]);
-                    }
+                for (int m = 0; m < NM; ++m) {
+                    const _Float16 *src = vt + 4 * qd * VST + 16 * m + col;
+                    const half4_t vb = {src[0], src[VST], src[2 * VST], src[3 * VST]};
+                    oacc[m] = __builtin_amdgcn_mfma_f32_16x16x16f16(ph, vb, oacc[m], 0, 0, 0);
+                    oacc[m] = __builtin_amdgcn_mfma_f32_16x16x16f16(pl, vb, oacc[m], 0, 0, 0);
+                }
+                wave_lds_sync();
             }
         }
+    };
+    // batches alternate between the two register sets; the next load of a
+    // set is issued as soon as it has been consumed
+    pv_batch(vr, 0);
+    if constexpr (SMAX > VB) {
+        if constexpr (SMAX > 2 * VB) {
+#pragma unroll
+            for (int u = 0; u < VB; ++u) vr[u] = load_v(2 * VB + u);
+        }
+        pv_batch(vr2, VB);
+        if constexpr (SMAX > 3 * VB) {
+#pragma unroll
+            for (int u = 0; u < VB; ++u) vr2[u] = load_v(3 * VB + u);
+        }
+        if constexpr (SMAX > 2 * VB) pv_batch(vr, 2 * VB);
+        if constexpr (SMAX > 3 * VB) pv_batch(vr2, 3 * VB);
     }
-    // lanes sharing a dim group, then the waves one at a time, each rescaled
-    // from its own max to the split's
-#pragma unroll
-    for (int sft = DG; sft < 64; sft <<= 1)
-#pragma unroll
-        for (int g = 0; g < GM; ++g)
-            if (g < G)
-#pragma unroll
-                for (int e = 0; e < 8; ++e) o[g][e] += __shfl_xor(o[g][e], sft, 64);
+    static_assert(SMAX <= 4 * VB, "at most four batches of values");
+    // oacc[m][r] is query head 4 qd + r, dim 16 m + col.  The waves add in
+    // turn, each rescaled from its own max to the split's.
+    __syncthreads();                           // every wave is done with the staged tiles
     for (int k = 0; k < NW; ++k) {
-        if (w == k && sub == 0) {
+        if (w == k) {
 #pragma unroll
-            for (int g = 0; g < GM; ++g)
+            for (int r = 0; r < 4; ++r) {
+                const int g = 4 * qd + r;
                 if (g < G) {
                     float M = wmx[g];
 #pragma unroll
@@ -311,11 +350,12 @@ __global__ __launch_bounds__(ATT_NT) void k_attn_split(AttnArgs a)
                     const float mw = wmx[k * G + g];
                     const float sc = mw == -INFINITY ? 0.0f : __expf(mw - M);
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) {
-                        float *const cp = &acc[g * D + dg * 8 + e];
-                        *cp = k == 0 ? sc * o[g][e] : fmaf(sc, o[g][e], *cp);
+                    for (int m = 0; m < NM; ++m) {
+                        float *const cp = &acc[g * D + 16 * m + col];
+                        *cp = k == 0 ? sc * oacc[m][r] : fmaf(sc, oacc[m][r], *cp);
                     }
                 }
+            }
         }
         __syncthreads();
     }
@@ -420,31 +460,24 @@ __global__ __launch_bounds__(ATT_NT) void k_gather(const __half *pool, int64_t n
     out_v[i] = pool[src + s1];
 }
 
-template <int D, int GM>
+template <int D>
 hipError_t launch_attn(const AttnArgs &a, int64_t B, hipStream_t st)
 {
-    // FAST: block sizes that are powers of two from 16 up hold whole 16-token tiles
-    // probabilities, wave max and sum, output sum, block ids: at most 34 KiB
-    const size_t lds = ((size_t)a.G * (ATT_NW * 64 + 2 * ATT_NW + D) + ATT_TS + 1) * sizeof(float);
+    // probabilities, wave max and sum, block ids, staged V tiles (and the
+    // output sum after them): at most 50 KiB
+    const size_t lds = ((size_t)a.G * (ATT_NW * 64 + 2 * ATT_NW) + ATT_TS + 4) * sizeof(float) +
+                       (size_t)ATT_NW * 16 * (D + 4) * sizeof(uint16_t);
+    // block sizes that are powers of two from 16 up hold whole 16-token tiles
     if (a.bs_shift >= 4)
-        hipLaunchKernelGGL((k_attn_split<D, GM, true>), dim3((unsigned)(B * a.n_kv * a.nsplit)), dim3(ATT_NT), lds, st, a);
+        hipLaunchKernelGGL((k_attn_split<D, true>), dim3((unsigned)(B * a.n_kv * a.nsplit)), dim3(ATT_NT), lds, st, a);
     else
-        hipLaunchKernelGGL((k_attn_split<D, GM, false>), dim3((unsigned)(B * a.n_kv * a.nsplit)), dim3(ATT_NT), lds, st,
-                           a);
+        hipLaunchKernelGGL((k_attn_split<D, false>), dim3((unsigned)(B * a.n_kv * a.nsplit)), dim3(ATT_NT), lds, st, a);
     if (a.nsplit > 1) {
         const int64_t pairs = B * a.n_heads;
         hipLaunchKernelGGL((k_attn_merge<D>), dim3((unsigned)((pairs + ATT_NW - 1) / ATT_NW)), dim3(ATT_NT), 0, st, a,
                            pairs);
     }
     return hipGetLastError();
-}
-
-template <int D>
-hipError_t launch_attn_d(const AttnArgs &a, int64_t B, hipStream_t st)
-{
-    if (a.G <= 4) return launch_attn<D, 4>(a, B, st);
-    if (a.G <= 8) return launch_attn<D, 8>(a, B, st);
-    return launch_attn<D, 16>(a, B, st);
 }
 
 // Tokens per split: 256, halved (down to 64) while the grid would hold fewer
@@ -518,9 +551,9 @@ int mis_paged_attention(void *pool, int64_t num_blocks, int block_size, int n_kv
     }
     hipStream_t st = (hipStream_t)stream;
     hipError_t e;
-    if (d_k == 64) e = launch_attn_d<64>(a, B, st);
-    else if (d_k == 128) e = launch_attn_d<128>(a, B, st);
-    else e = launch_attn_d<256>(a, B, st);
+    if (d_k == 64) e = launch_attn<64>(a, B, st);
+    else if (d_k == 128) e = launch_attn<128>(a, B, st);
+    else e = launch_attn<256>(a, B, st);
     return e == hipSuccess ? MIS_ATT_OK : MIS_ATT_ERR_HIP;
 }
 
