@@ -10,8 +10,10 @@ row pass (per-row finalize); the sampled ids stay on the device.
 Inputs are resident in HBM before timing starts.  The batch (131 MB) fits
 the 256 MB Infinity Cache, so the timed loop rotates through >= 1 GiB of
 distinct copies of it.  Timing uses HIP events on the launch stream:
-* whole region: barrier + synchronize, start event, K steps, end event;
-* per pass: mis_sample_ex() records events before the chunk pass, after it
+* whole region (value, ms_per_step): synchronize, start event, K steps with
+  nothing else on the streams, end event;
+* per step and per pass, in a second run of K steps after it:
+  mis_sample_ex() records events before the chunk pass, after it
   on each stream that runs part of it, and after the row pass of every step.
   A batch with fp32 top-p rows and other rows splits the chunk pass into two
   launches on two streams (the top-p rows' on the launch stream, the others'
@@ -164,17 +166,22 @@ def bench_attention(args):
         call()
     torch.cuda.synchronize()
     K = args.steps
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(K)]
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     start.record()
     for i in range(K):
-        evs[i][0].record()
         call()
-        evs[i][1].record()
     end.record()
     torch.cuda.synchronize()
     total_ms = start.elapsed_time(end)
+    # per-call durations from events around each call, in a second run
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(K)]
+    torch.cuda.synchronize()
+    for i in range(K):
+        evs[i][0].record()
+        call()
+        evs[i][1].record()
+    torch.cuda.synchronize()
     call_us = [a.elapsed_time(b) * 1e3 for a, b in evs]
     mean_us = statistics.mean(call_us)
     kv_bytes = B * ctx * KV * D * 2 * 2
@@ -263,18 +270,26 @@ def main():
     torch.cuda.synchronize()
 
     K = args.steps
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(K)]
-    for trio in evs:
-        for e in trio:
-            e.record()
+    # the timed region: K steps with nothing else on the streams
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     start.record()
     for i in range(K):
-        s.sample_packed(bufs[(args.warmup + i) % nbuf], packed, out=out, events=evs[i], kinds=kinds)
+        s.sample_packed(bufs[(args.warmup + i) % nbuf], packed, out=out, kinds=kinds)
     end.record()
     torch.cuda.synchronize()
     total_ms = start.elapsed_time(end)
+    # then K more steps with events inside each, for the per-step and per-pass
+    # durations (the events themselves cost about 13 us per C3 step, so they
+    # stay out of the timed region)
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(K)]
+    for trio in evs:
+        for e in trio:
+            e.record()
+    torch.cuda.synchronize()
+    for i in range(K):
+        s.sample_packed(bufs[(args.warmup + K + i) % nbuf], packed, out=out, events=evs[i], kinds=kinds)
+    torch.cuda.synchronize()
     step_us = [t[0].elapsed_time(t[2]) * 1e3 for t in evs]
     # the chunk pass: from the first event to the later end of its launches
     # (two, and the fourth event recorded, exactly for fp32 with both kinds)
