@@ -11,7 +11,7 @@ import sys
 import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADERS = [os.path.join(ROOT, "include", h) for h in ("mis_sampler.h", "mis_attention.h")]
+HEADERS = [os.path.join(ROOT, "include", h) for h in ("mis_sampler.h", "mis_attention.h", "mis_lmhead.h")]
 
 
 def declared_functions() -> list[str]:
@@ -136,6 +136,18 @@ def test_argument_validation_without_gpu(lib):
     assert lib.mis_paged_attention_workspace_bytes(256, 32, 8, 128, 2048) == 256 * 32 * 8 * (128 + 2) * 4
     assert lib.mis_gather_kv(fake, 64, 16, 4, 64, 4096, 2048, fake, 8, fake, 2, -1, fake, fake, None) == 1
     assert lib.mis_gather_kv(fake, 64, 16, 4, 64, 4096, 2048, fake, 8, fake, -2, 16, fake, fake, None) == 1
+    # fused lm_head + greedy: shapes, dtype, alignment and workspace checked before any launch
+    lh = lambda *a: lib.mis_lm_head_greedy(*a)
+    okh = (fake, 4096, fake, 4096, 4, 4096, 32000, 2, fake, fake, 1 << 20, None)
+    assert lh(*okh[:4], 0, *okh[5:]) == 0                                  # empty batch
+    assert lh(*okh[:4], -1, *okh[5:]) == 1
+    assert lh(*okh[:7], 0, *okh[8:]) == 4                                  # fp32 weights
+    assert lh(*okh[:3], 4000, *okh[4:]) == 1                               # weight rows shorter than H
+    assert lh(fake, 4000, fake, 4000, 4, 4000, 32000, 2, fake, fake, 1 << 20, None) == 4   # H not a multiple of 64
+    assert lh(vp(0x1008), *okh[1:]) == 1                                   # hidden not 16-byte aligned
+    assert lh(*okh[:9], None, 0, None) == 2                                # no workspace
+    assert lh(*okh[:10], 100, None) == 2                                   # too small
+    assert lib.mis_lm_head_greedy_workspace_bytes(4, 32000) == ((250 * 4 * 8 + 255) // 256) * 256
 
 
 def test_product_path_fails_loudly_without_library(tmp_path):

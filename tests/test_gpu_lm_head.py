@@ -1,0 +1,82 @@
+"""GPU: the fused lm_head + greedy kernel (mis_lm_head_greedy) against the CPU
+oracle (oracle/lm_head.py) and against torch's own GEMM + argmax on the GPU.
+
+Bar: the chosen id equals the oracle's, or its exact logit lies within the
+stated tolerance of the exact maximum (twice the worst-case fp32 summation
+error plus one dtype ulp: the kernel's fp32 additions run in another order
+than the oracle's float64 ones, and a near-tie can round either way).  Ties in
+the dtype values (duplicated weight rows) go to the lowest index exactly, and
+NaN logits win at the first NaN."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import lm_head as O
+from tests.test_lm_head_oracle import make
+from vllm_mps_amd import lm_head as LH
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [(1, 64, 1000), (7, 128, 3001), (64, 4096, 32000), (65, 256, 5000), (130, 512, 2049)]
+
+
+def _check(name, x, w, dtype, device):
+    print(f"[lmhead] {name} {dtype} B={x.shape[0]} H={x.shape[1]} V={w.shape[0]}", flush=True)
+    got = LH.lm_head_greedy(x.to(device), w.to(device)).cpu().numpy()
+    xs, ws = x.float().numpy(), w.float().numpy()
+    ids, ex, _ = O.greedy(xs, ws, dtype)
+    tol = O.tolerance(xs, ws, dtype)
+    rows = np.arange(len(ids))
+    assert ((got >= 0) & (got < w.shape[0])).all()
+    ok = (got == ids) | (ex[rows, got] >= ex[rows, ids] - tol)
+    print(f"[lmhead] {name}: {int((got == ids).sum())}/{len(ids)} equal to the oracle", flush=True)
+    assert ok.all(), (np.where(~ok), got[~ok], ids[~ok])
+    return got, ids, ex, tol
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+@pytest.mark.parametrize("B,H,V", SHAPES)
+def test_lm_head_greedy_vs_oracle(B, H, V, dtype, device):
+    x, w = make(B * 7 + V, B, H, V, dtype)
+    got, ids, _, _ = _check(f"shape", x, w, dtype, device)
+    assert (got == ids).mean() >= 0.95
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+def test_lm_head_greedy_vs_torch_gemm(dtype, device):
+    """torch's GEMM in the model dtype (the reference's producer) then argmax."""
+    x, w = make(11, 64, 4096, 32000, dtype)
+    xd, wd = x.to(device), w.to(device)
+    ref = torch.argmax(torch.matmul(xd, wd.t().contiguous()), dim=1).cpu().numpy()
+    got = LH.lm_head_greedy(xd, wd).cpu().numpy()
+    xs, ws = x.float().numpy(), w.float().numpy()
+    ex = O.logits_exact(xs, ws)
+    tol = O.tolerance(xs, ws, dtype)
+    rows = np.arange(64)
+    print(f"[lmhead] vs torch {dtype}: {int((got == ref).sum())}/64 equal", flush=True)
+    assert ((got == ref) | (np.abs(ex[rows, got] - ex[rows, ref]) <= tol)).all()
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+def test_lm_head_greedy_ties_nan_and_strides(dtype, device):
+    x, w = make(5, 9, 192, 4099, dtype)
+    xs, ws = x.float().numpy(), w.float().numpy()
+    ids, _, _ = O.greedy(xs, ws, dtype)
+    w2 = w.clone()
+    w2[3] = w[int(ids[0])]                 # a duplicate of row 0's winner, lower index
+    w2[4098] = w[int(ids[0])]              # and one in the last, partial vocabulary tile
+    got = LH.lm_head_greedy(x.to(device), w2.to(device)).cpu().numpy()
+    assert got[0] == min(3, int(ids[0]))
+    w3 = w.clone()
+    w3[2500, 7] = float("nan")
+    w3[2600, 1] = float("nan")
+    got = LH.lm_head_greedy(x.to(device), w3.to(device)).cpu().numpy()
+    assert (got == 2500).all()
+    # row strides wider than H (a view into a larger buffer)
+    xb = torch.zeros(9, 256, dtype=x.dtype)
+    xb[:, :192] = x
+    wb = torch.zeros(4099, 200, dtype=w.dtype)
+    wb[:, :192] = w
+    got = LH.lm_head_greedy(xb.to(device)[:, :192], wb.to(device)[:, :192]).cpu().numpy()
+    want = LH.lm_head_greedy(x.to(device), w.to(device)).cpu().numpy()
+    assert np.array_equal(got, want)

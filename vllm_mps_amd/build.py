@@ -19,7 +19,7 @@ import sys
 PKG = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(PKG)
 CSRC = os.path.join(PKG, "csrc")
-UNITS = ("mis_api.hip", "mis_f32.hip", "mis_f16.hip", "mis_bf16.hip", "mis_rng.hip", "mis_attn.hip")
+UNITS = ("mis_api.hip", "mis_f32.hip", "mis_f16.hip", "mis_bf16.hip", "mis_rng.hip", "mis_attn.hip", "mis_lmhead.hip")
 OUT_DIR = os.path.join(PKG, "_lib")
 LIB = os.path.join(OUT_DIR, "libmis_sampler.so")
 ARCH = os.environ.get("MIS_OFFLOAD_ARCH", "gfx950")
