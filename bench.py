@@ -74,8 +74,9 @@ def parse():
     ap.add_argument("--row-params", default=None, metavar="T,k,p",
                     help="give every row this temperature, top_k and top_p (one row mode at a time, for per-mode "
                          "counters); the default keeps the config's own per-row mix")
-    ap.add_argument("--op", default="sample", choices=["sample", "attention"],
-                    help="sample: the sampler (configs C1-C5); attention: the paged decode attention (config A1)")
+    ap.add_argument("--op", default="sample", choices=["sample", "attention", "lmhead"],
+                    help="sample: the sampler (configs C1-C5); attention: the paged decode attention (config A1); "
+                         "lmhead: the lm_head GEMM fused with the greedy sampler (config L1)")
     ap.add_argument("--copy-calib-mib", type=int, default=0,
                     help="after the timed steps, run 5 plain device copies of this many MiB (calibrates "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE against known bytes)")
@@ -227,6 +228,95 @@ def bench_attention(args):
     print(json.dumps(res), flush=True)
 
 
+LMH_L1 = {"B": 64, "H": 4096, "V": 128256, "dtype": "bf16"}
+
+
+def bench_lmhead(args):
+    """Fused lm_head + greedy, config L1 (Llama-3-8B's lm_head), against the
+    unfused producer + sampler: torch's GEMM in bf16 (hipBLASLt), then
+    torch.argmax (the reference's pair) or this build's sampler."""
+    import numpy as np
+    import torch
+    from vllm_mps_amd import lm_head as LH
+
+    c = LMH_L1
+    B, H, V = c["B"], c["H"], c["V"]
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    g = torch.Generator(device="cpu").manual_seed(1)
+    x = (torch.randn(B, H, generator=g) * 0.5).to(torch.bfloat16).to(dev)
+    w = (torch.randn(V, H, generator=g) * 0.05).to(torch.bfloat16).to(dev)
+    fused = lambda: LH.lm_head_greedy(x, w)
+    wt = w.t()
+    unfused = lambda: torch.argmax(torch.matmul(x, wt), dim=1)
+    # the same GEMM followed by this build's sampler (greedy rows), as an
+    # engine without the fusion would run it
+    from vllm_mps_amd.sampler import Sampler, pack_params
+    smp = Sampler()
+    zeros = torch.zeros(B, device=dev)
+    packed = pack_params(zeros, torch.zeros(B, dtype=torch.int32, device=dev), torch.ones(B, device=dev), zeros)
+    ids_buf = torch.empty(B, dtype=torch.int64, device=dev)
+    unfused_mis = lambda: smp.sample_packed(torch.matmul(x, wt), packed, out=ids_buf)
+    K = args.steps
+
+    def timed(fn):
+        for _ in range(args.warmup):
+            fn()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        start.record()
+        for _ in range(K):
+            fn()
+        end.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) / K
+
+    ms = timed(fused)
+    ms_unfused = timed(unfused)
+    ms_unfused_mis = timed(unfused_mis)
+    same = bool(torch.equal(fused(), unfused())) and bool(torch.equal(fused(), unfused_mis().clone()))
+    alg = V * H * 2 + B * H * 2 + B * 8           # the weight read once, the hidden states, the ids
+    achieved = alg / (ms / 1e3) / 1e9
+    flops = 2.0 * B * H * V
+    res = {
+        "metric": "fused lm_head + greedy: sequences/s per decode step + weight GB/s (% of peak)",
+        "value": round(B / (ms / 1e3), 1), "unit": "sequences/s",
+        "n_gpus": 1, "steps": K, "warmup": args.warmup, "ms_per_step": round(ms, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16 (fp32 accumulation)", "data": "synthetic",
+        "config": {"workload": "L1 Llama-3-8B lm_head [4096 -> 128256] bf16, greedy", **c},
+        "unfused_ms_per_step": round(ms_unfused, 5),
+        "speedup_vs_unfused": round(ms_unfused / ms, 3),
+        "unfused_mis_sampler_ms_per_step": round(ms_unfused_mis, 5),
+        "speedup_vs_unfused_mis_sampler": round(ms_unfused_mis / ms, 3),
+        "ids_equal_unfused": same,
+        "tflops": round(flops / (ms / 1e3) / 1e12, 1),
+        "roofline": {"bound": "hbm", "kernel": "k_lmh_tile + k_lmh_merge (one call)", "achieved": round(achieved, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "algorithmic_bytes_per_launch": alg, "mean_launch_us": round(ms * 1e3, 2)},
+    }
+    if args.cpu_rows > 0:
+        from oracle import lm_head as O
+        from threadpoolctl import threadpool_limits
+        ns = 2
+        xs = x[:ns].float().cpu().numpy()
+        ws = w.float().cpu().numpy()
+        times = []
+        with threadpool_limits(limits=1):
+            for it in range(1 + min(args.cpu_steps, 3)):
+                t0 = time.perf_counter()
+                O.greedy(xs, ws, "bf16")
+                if it >= 1:
+                    times.append(time.perf_counter() - t0)
+        p50 = statistics.median(times)
+        res["cpu_baseline"] = {"value": round(ns / p50, 3), "unit": "sequences/s", "cores": 1, "kind": "port",
+                               "sample": f"{ns} of {B} L1 sequences, oracle/lm_head.py numpy float64 GEMM + argmax, "
+                                         f"p50 of {len(times)} calls after 1 warmup"}
+    else:
+        res["cpu_baseline"] = None
+    print(json.dumps(res), flush=True)
+
+
 def main():
     args = parse()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -237,6 +327,9 @@ def main():
         sys.exit(2)
     if args.op == "attention":
         bench_attention(args)
+        return
+    if args.op == "lmhead":
+        bench_lmhead(args)
         return
 
     import torch
