@@ -8,8 +8,8 @@
 // from HBM, 32 contiguous bytes per lane per block of 64 hidden dims) and the
 // hidden states as B (the block staged in LDS once per workgroup, double
 // buffered).  The products of two 16-bit values are exact in fp32; the sums
-// are fp32.  The next block's weight and hidden loads are issued before the
-// current block's MFMAs.  The epilogue rounds each logit to the model dtype
+// are fp32.  The weight blocks two ahead and the next hidden block are
+// loaded while the current block's MFMAs run.  The epilogue rounds each logit to the model dtype
 // and keeps, per sequence, the tile's best (dtype value, lowest index): a
 // 64-bit key, larger is better.  k_lmh_merge takes the maximum key over the
 // tiles of each sequence.
@@ -121,7 +121,7 @@ __global__ __launch_bounds__(LMH_NT) void k_lmh_tile(const uint16_t *__restrict_
             *reinterpret_cast<uint4 *>(&xs[buf][row * LMH_XST + seg * 8]) = xr[u];
         }
     };
-    auto load_w = [&](int kb, uint4 (*wr)[2]) {
+    auto load_w = [&](int kb, uint4 (*wr)[2]) {   // this lane's 32 bytes of each of its rows
 #pragma unroll
         for (int rt = 0; rt < LMH_RT; ++rt) {
             const uint4 *p = reinterpret_cast<const uint4 *>(wrow[rt] + (int64_t)kb * LMH_KB);
@@ -134,14 +134,19 @@ __global__ __launch_bounds__(LMH_NT) void k_lmh_tile(const uint16_t *__restrict_
     for (int rt = 0; rt < LMH_RT; ++rt)
 #pragma unroll
         for (int ct = 0; ct < LMH_BG / 16; ++ct) acc[rt][ct] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
-    uint4 xr[2], wr[LMH_RT][2], wn[LMH_RT][2];
+    // three register sets of weight blocks: block k + 2 is issued as block k's
+    // MFMAs start, so each block has two iterations to arrive
+    uint4 xr[2], w0[LMH_RT][2], w1[LMH_RT][2], w2[LMH_RT][2];
     load_x(0, xr);
-    load_w(0, wr);
+    load_w(0, w0);
+    if (nkb > 1) load_w(1, w1);
     store_x(0, xr);
-    for (int kb = 0; kb < nkb; ++kb) {
+    // iteration kb: weights in `cur`, block kb + 2 into `fut` (the set block
+    // kb - 1 used), hidden block kb in LDS buffer kb & 1
+    auto step = [&](int kb, uint4 (*cur)[2], uint4 (*fut)[2]) {
         __syncthreads();                       // block kb staged; the other buffer free
-        const bool more = kb + 1 < nkb;
-        if (more) { load_x(kb + 1, xr); load_w(kb + 1, wn); }
+        if (kb + 1 < nkb) load_x(kb + 1, xr);
+        if (kb + 2 < nkb) load_w(kb + 2, fut);
         const uint16_t *xb = xs[kb & 1];
         // step s uses dims 4 s .. 4 s + 3 of each lane's 16 (the same
         // permutation of the block's dims for both operands)
@@ -153,18 +158,19 @@ __global__ __launch_bounds__(LMH_NT) void k_lmh_tile(const uint16_t *__restrict_
                 bx[ct] = *reinterpret_cast<const u32x2_t *>(&xb[(16 * ct + col) * LMH_XST + 16 * qd + 4 * s]);
 #pragma unroll
             for (int rt = 0; rt < LMH_RT; ++rt) {
-                const uint4 &r = wr[rt][s >> 1];
+                const uint4 &r = cur[rt][s >> 1];
                 const u32x2_t a = (s & 1) ? u32x2_t{r.z, r.w} : u32x2_t{r.x, r.y};
 #pragma unroll
                 for (int ct = 0; ct < LMH_BG / 16; ++ct)
                     if (ct < nct) acc[rt][ct] = mfma16<DT>(a, bx[ct], acc[rt][ct]);  // nct is workgroup-uniform
             }
         }
-        if (more) {
-            store_x((kb + 1) & 1, xr);
-#pragma unroll
-            for (int rt = 0; rt < LMH_RT; ++rt) { wr[rt][0] = wn[rt][0]; wr[rt][1] = wn[rt][1]; }
-        }
+        if (kb + 1 < nkb) store_x((kb + 1) & 1, xr);
+    };
+    for (int kb = 0; kb < nkb; kb += 3) {      // the sets rotate with period three
+        step(kb, w0, w2);
+        if (kb + 1 < nkb) step(kb + 1, w1, w0);
+        if (kb + 2 < nkb) step(kb + 2, w2, w1);
     }
     // epilogue: acc[rt][ct][r] is vocabulary row v0 + 32 w + 16 rt + 4 qd + r,
     // sequence b0 + 16 ct + col
