@@ -71,6 +71,20 @@ template <int DT> __device__ __forceinline__ float scale_r(float x, float T, flo
 template <int DT, int N> __device__ __forceinline__ void scale_all(float (&x)[N], float T, float r)
 {
     static_assert(N <= 64, "one mask bit per element");
+    if (T == 1.0f) {
+        // x / 1 == x exactly, and x (a value of the row's dtype) rounds to
+        // itself: only NaN elements, which the division quiets, take the
+        // general formula
+        uint64_t nan = 0ull;
+#pragma unroll
+        for (int i = 0; i < N; ++i) nan |= x[i] != x[i] ? (1ull << i) : 0ull;
+        if (__ballot(nan != 0ull) != 0ull) {
+#pragma unroll
+            for (int i = 0; i < N; ++i)
+                if (nan & (1ull << i)) x[i] = DT == F32 ? x[i] / T : rn_dtype(x[i] / T, DT);
+        }
+        return;
+    }
     uint64_t slow = 0ull;
 #pragma unroll
     for (int i = 0; i < N; ++i) {

@@ -1634,8 +1634,13 @@ __global__ __launch_bounds__(NT) void k_sample(Args a, int part)
         uint32_t ncand = 0u, kc = 0u, trunc = 0u;
         if (live && pl.mode == M_TEMP) {
             double s = 0.0;
+            if (T == 1.0f) {  // y = x exactly (a live chunk holds no NaN)
 #pragma unroll
-            for (int i = 0; i < EPT; ++i) s += (double)wexp(scale_r<DT>(x[i], T, rT), ymax);
+                for (int i = 0; i < EPT; ++i) s += (double)wexp(x[i], ymax);
+            } else {
+#pragma unroll
+                for (int i = 0; i < EPT; ++i) s += (double)wexp(scale_r<DT>(x[i], T, rT), ymax);
+            }
             Sc = block_sum<double>(s, sm.red);
         } else if (live && topp32) {
             // weights exp(y - ymax) in float64 (dexp: relative error below
@@ -1671,8 +1676,13 @@ __global__ __launch_bounds__(NT) void k_sample(Args a, int part)
                 // dtype and takes an exact S only for a row where one of
                 // them could change within that bound
                 double s = 0.0;
+                if (T == 1.0f) {  // y = x exactly (a live chunk holds no NaN)
 #pragma unroll
-                for (int i = 0; i < EPT; ++i) s += (double)wexp(scale_r<DT>(x[i], T, rT), ymax);
+                    for (int i = 0; i < EPT; ++i) s += (double)wexp(x[i], ymax);
+                } else {
+#pragma unroll
+                    for (int i = 0; i < EPT; ++i) s += (double)wexp(scale_r<DT>(x[i], T, rT), ymax);
+                }
                 Sc = block_sum<double>(s, sm.red);
             }
             // ---- candidates: every finite x whose scaled key reaches a threshold
