@@ -83,6 +83,30 @@ def parse():
     return ap.parse_args()
 
 
+def copy_calibration(mib: int, dev) -> None:
+    """Five plain device copies of `mib` MiB (rocprofv3 FETCH_SIZE / WRITE_SIZE calibration)."""
+    if mib <= 0:
+        return
+    import torch
+    src = torch.empty(mib << 20, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+
+
+def traffic_from_file(name: str, key: str):
+    """HBM bytes per call from a committed rocprofv3 traffic summary under profiles/, or None."""
+    try:
+        with open(os.path.join(ROOT, "profiles", name)) as f:
+            for line in f:
+                if line.startswith(key + ":"):
+                    return int(float(line.split(":", 1)[1]))
+    except OSError:
+        pass
+    return None
+
+
 def traffic_from_profile(config: str):
     """HBM bytes per chunk pass (its one or two launches of a step) measured by rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE,
     each scaled by the same counter's reading for a copy of known size), from the committed
@@ -184,6 +208,7 @@ def bench_attention(args):
         evs[i][1].record()
     torch.cuda.synchronize()
     call_us = [a.elapsed_time(b) * 1e3 for a, b in evs]
+    copy_calibration(args.copy_calib_mib, dev)
     mean_us = statistics.mean(call_us)
     kv_bytes = B * ctx * KV * D * 2 * 2
     alg = kv_bytes + B * H * D * 2 * 2 + B * KV * D * 2 * 2   # K/V rows read, queries and outputs, new K/V written
@@ -201,7 +226,8 @@ def bench_attention(args):
         "p50_us_per_step": round(statistics.median(call_us), 2),
         "roofline": {"bound": "hbm", "kernel": "k_attn_split + k_attn_merge (one call)",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": traffic_from_file("paged_attention_A1_traffic.md", "traffic_bytes_per_call"),
                      "algorithmic_bytes_per_launch": alg, "mean_launch_us": round(mean_us, 2)},
     }
     if args.cpu_rows > 0:
@@ -275,6 +301,7 @@ def bench_lmhead(args):
     ms_unfused = timed(unfused)
     ms_unfused_mis = timed(unfused_mis)
     same = bool(torch.equal(fused(), unfused())) and bool(torch.equal(fused(), unfused_mis().clone()))
+    copy_calibration(args.copy_calib_mib, dev)
     alg = V * H * 2 + B * H * 2 + B * 8           # the weight read once, the hidden states, the ids
     achieved = alg / (ms / 1e3) / 1e9
     flops = 2.0 * B * H * V
@@ -292,7 +319,8 @@ def bench_lmhead(args):
         "ids_equal_unfused": same,
         "tflops": round(flops / (ms / 1e3) / 1e12, 1),
         "roofline": {"bound": "hbm", "kernel": "k_lmh_tile + k_lmh_merge (one call)", "achieved": round(achieved, 1),
-                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": traffic_from_file("lm_head_greedy_L1_traffic.md", "traffic_bytes_per_call"),
                      "algorithmic_bytes_per_launch": alg, "mean_launch_us": round(ms * 1e3, 2)},
     }
     if args.cpu_rows > 0:
@@ -433,14 +461,7 @@ def main():
                      "chunk_pass_launches": 2 if split else 1,
                      "row_pass_us": round(k2_mean, 2)},
     }
-    if args.copy_calib_mib > 0:
-        n = args.copy_calib_mib << 20
-        src = torch.empty(n, dtype=torch.uint8, device=dev)
-        dst = torch.empty_like(src)
-        for _ in range(5):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        del src, dst
+    copy_calibration(args.copy_calib_mib, dev)
     if args.cpu_rows > 0:
         res["cpu_baseline"] = cpu_baseline(w, args.cpu_rows, args.cpu_steps)
     else:
