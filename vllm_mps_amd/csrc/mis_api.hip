@@ -94,6 +94,7 @@ static int sample_impl(const void *logits, int dtype, int64_t B, int64_t V, int6
     a.ws = (char *)workspace;
     a.out_ids = out_ids;
     a.out_status = out_status;
+    a.emit = (out_probs || out_keep) ? 1 : 0;
     hipStream_t st = (hipStream_t)stream;
     hipError_t e;
     const SideStreams *sd = nullptr;

@@ -3035,13 +3035,21 @@ __global__ __launch_bounds__(NTF) void k_t16_final(Args a)
     const int gb = sm.bi[2];
     const uint32_t tb = sm.bu[2], cb = sm.bu[3];
     const uint32_t rk = ck << 16;  // the cut key as a row key
-    int32_t cut_i = IDX_ALL;
-    if (gb >= 0 && tb < cb) cut_i = (int32_t)nth_key_in_chunk<DT, NTF>(sm, c, gb, rk, tb);
-    else if (gb >= 0 && tot > t) cut_i = (int32_t)((int64_t)(gb + 1) * c.CH - 1);  // every tie up to chunk gb's end
-    trace(a.ws, L, row, 12);
+    // the chunk first: the per-chunk kept masses do not depend on the tie index
     int gsel;
     double resid, SK;
     pick_chunk(sm, G, pl.u, &gsel, &resid, &SK);
+    int32_t cut_i = IDX_ALL;
+    if (gb >= 0 && tb < cb) {
+        // the last kept tie lies inside chunk gb: its index matters to a draw
+        // in that chunk and to the emitted keep masks; a draw in another chunk
+        // keeps every tie before chunk gb and none after it, as gb * CH - 1 does
+        if (gsel == gb || a.emit) cut_i = (int32_t)nth_key_in_chunk<DT, NTF>(sm, c, gb, rk, tb);
+        else cut_i = (int32_t)((int64_t)gb * c.CH - 1);
+    } else if (gb >= 0 && tot > t) {
+        cut_i = (int32_t)((int64_t)(gb + 1) * c.CH - 1);  // every tie up to chunk gb's end
+    }
+    trace(a.ws, L, row, 12);
     int64_t id = -1;
     if (gsel >= 0) {
         const float T = pl.T, rT = 1.0f / pl.T;

@@ -191,6 +191,7 @@ struct Args {
     char *ws;
     int64_t *out_ids;
     int32_t *out_status;
+    int emit;                   // probabilities or keep masks requested (k_emit reads every row's exact cut)
 };
 
 }  // namespace mis
