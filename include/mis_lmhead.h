@@ -26,6 +26,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include "mis_sampler.h"   /* mis_rng_row */
+
 #ifdef __cplusplus
 extern "C" {
 #endif
@@ -49,6 +51,30 @@ size_t mis_lm_head_greedy_workspace_bytes(int64_t B, int64_t V);
  */
 int mis_lm_head_greedy(const void *hidden, int64_t ldx, const void *weight, int64_t ldw, int64_t B, int64_t H,
                        int64_t V, int dtype, int64_t *ids, void *workspace, size_t workspace_bytes, void *stream);
+
+/*
+ * The same GEMM with a sampling epilogue, for batches mixing greedy rows and
+ * temperature-only rows (top-k 0, top-p 1: the engine's default parameters):
+ *   temperature [B] (device f32): 0 = greedy (as mis_lm_head_greedy);
+ *     T > 0: ids[b] = argmax_v (y[b, v] + g[b, v]), y = dtype(logit / T) (the
+ *     quotient in fp32, rounded once to the dtype), g the Gumbel noise below:
+ *     an exact draw from softmax(y) (the Gumbel-max theorem), replacing
+ *     model/sampler.py:37 and :57-59 for such rows (torch.multinomial's generator
+ *     becomes a per-request counter-based one);
+ *     T < 0 or NaN: ids[b] = -1 (the reference's ValueError);
+ *   rng [B] (device): the draw's key and counter, as mis_fill_uniforms:
+ *     vocabulary rows v .. v + 3 (v a multiple of 4) take Philox4x32-10 with
+ *     key (seed low, seed high ^ step high) and counter (v / 4, step low,
+ *     request low, request high); output word i gives u = (w >> 8) * 2^-24 and
+ *     g = -log(-log(u)) (u = 0: -inf).
+ * A sampled row whose scaled logits hold NaN or +inf, or are all -inf, gets
+ * id -1 (the reference's torch.multinomial RuntimeError).  Top-k and top-p
+ * rows are not served here (their cuts need the whole row): run the GEMM and
+ * mis_sample.  The workspace is mis_lm_head_greedy_workspace_bytes(B, V).
+ */
+int mis_lm_head_sample(const void *hidden, int64_t ldx, const void *weight, int64_t ldw, int64_t B, int64_t H,
+                       int64_t V, int dtype, const float *temperature, const mis_rng_row *rng, int64_t *ids,
+                       void *workspace, size_t workspace_bytes, void *stream);
 
 #ifdef __cplusplus
 }

@@ -80,3 +80,64 @@ def test_lm_head_greedy_ties_nan_and_strides(dtype, device):
     got = LH.lm_head_greedy(xb.to(device)[:, :192], wb.to(device)[:, :192]).cpu().numpy()
     want = LH.lm_head_greedy(x.to(device), w.to(device)).cpu().numpy()
     assert np.array_equal(got, want)
+
+
+def _check_sample(name, x, w, dtype, T, seed, req, stp, device):
+    print(f"[lmhead-sample] {name} {dtype} B={x.shape[0]} H={x.shape[1]} V={w.shape[0]}", flush=True)
+    got = LH.lm_head_sample(x.to(device), w.to(device), torch.from_numpy(T), (seed, req, stp)).cpu().numpy()
+    xs, ws = x.float().numpy(), w.float().numpy()
+    ids, z, y = O.sample(xs, ws, dtype, T, seed, req, stp)
+    same = got == ids
+    print(f"[lmhead-sample] {name}: {int(same.sum())}/{len(ids)} equal to the oracle", flush=True)
+    bad = ids < 0
+    assert np.array_equal(got[bad], ids[bad])
+    # elsewhere a different id must be a near-tie of the oracle's maximum:
+    # fp32 noise and sums, and a dtype rounding of y the GEMM's order can flip
+    ymax = np.nanmax(np.abs(np.where(np.isfinite(y), y, 0)), axis=1)
+    ulp = np.ldexp(1.0, np.floor(np.log2(np.maximum(ymax, 1e-30))).astype(int) - (10 if dtype == "f16" else 7))
+    zmax = np.nanmax(np.where(np.isfinite(z), np.abs(z), 0), axis=1)
+    for b in np.where(~same & ~bad)[0]:
+        assert got[b] >= 0 and z[b, got[b]] >= z[b, ids[b]] - (1e-5 * (1 + zmax[b]) + 2 * ulp[b]), b
+    return same.mean()
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+@pytest.mark.parametrize("B,H,V", [(7, 256, 3001), (64, 4096, 32000), (130, 512, 2049)])
+def test_lm_head_sample_vs_oracle(B, H, V, dtype, device):
+    x, w = make(B + V, B, H, V, dtype)
+    rng = np.random.default_rng(B)
+    T = rng.choice(np.array([0.0, 0.7, 1.0, 1.3], np.float32), B)
+    req = rng.integers(0, 1 << 40, B)
+    stp = rng.integers(0, 1000, B)
+    assert _check_sample("mixed", x, w, dtype, T, 12345, req, stp, device) >= 0.95
+
+
+def test_lm_head_sample_greedy_rows_and_invalid(device):
+    x, w = make(31, 6, 256, 4099, "bf16")
+    T = np.array([0.0, 0.0, 1.0, -1.0, np.nan, 0.9], np.float32)
+    got = LH.lm_head_sample(x.to(device), w.to(device), torch.from_numpy(T), (5, np.arange(6), np.zeros(6))).cpu().numpy()
+    greedy = LH.lm_head_greedy(x.to(device), w.to(device)).cpu().numpy()
+    assert got[0] == greedy[0] and got[1] == greedy[1]
+    assert got[3] == -1 and got[4] == -1 and got[2] >= 0 and got[5] >= 0
+    w2 = w.clone()
+    w2[100, 3] = float("nan")                        # a NaN logit: the sampled rows are invalid
+    got = LH.lm_head_sample(x.to(device), w2.to(device), torch.from_numpy(T), (5, np.arange(6), np.zeros(6))).cpu().numpy()
+    assert got[2] == -1 and got[5] == -1 and got[0] == 100
+
+
+def test_lm_head_sample_follows_softmax(device):
+    """4096 draws of one request (steps 0..4095) over 8 tokens: the frequencies
+    are softmax(y) (chi-square), and every draw equals the oracle's."""
+    from scipy import stats
+    x, w = make(41, 1, 128, 8, "bf16")
+    w = (w.float() * 20).to(torch.bfloat16)
+    n = 4096
+    xb = x.repeat(n, 1)
+    T = np.full(n, 1.0, np.float32)
+    got = LH.lm_head_sample(xb.to(device), w.to(device), torch.from_numpy(T), (99, np.zeros(n), np.arange(n))).cpu().numpy()
+    ids, _, y = O.sample(xb.float().numpy(), w.float().numpy(), "bf16", T, 99, np.zeros(n, np.int64), np.arange(n))
+    assert (got == ids).mean() >= 0.999
+    p = np.exp(y[0].astype(np.float64) - y[0].max())
+    p /= p.sum()
+    print(f"[lmhead-sample] frequencies {np.bincount(got, minlength=8)} expected {np.round(p * n).astype(int)}", flush=True)
+    assert stats.chisquare(np.bincount(got, minlength=8), p * n).pvalue > 1e-4

@@ -75,3 +75,40 @@ def test_tolerance_covers_fp32_reordering():
         for h in perm[:4096]:
             f32 = (f32 + (xs[:, h:h + 1] * ws[:, h][None, :]).astype(np.float32)).astype(np.float32)
         assert (np.abs(f32 - ex) <= tol[:, None] / 2).all()
+
+
+def test_philox_words_match_c_oracle():
+    """The vectorised Philox the sampling oracle uses equals the C oracle's
+    function (itself checked against the Random123 known answers)."""
+    from oracle import oracle as OR
+    rng = np.random.default_rng(0)
+    ctr = rng.integers(0, 2 ** 32, (64, 4), dtype=np.uint64).astype(np.uint32)
+    key = rng.integers(0, 2 ** 32, (64, 2), dtype=np.uint64).astype(np.uint32)
+    got = O.philox_words(ctr, key[:, 0], key[:, 1])
+    want = np.stack([OR.philox4x32_10(ctr[i], key[i]) for i in range(64)])
+    assert np.array_equal(got, want)
+
+
+def test_gumbel_max_draws_follow_softmax():
+    """The oracle's Gumbel-max draws (many steps of one request) have the
+    softmax frequencies of the scaled logits: a chi-square test over 6 tokens."""
+    from scipy import stats
+    x, w = make(21, 1, 64, 6, "bf16")
+    xs, ws = x.float().numpy(), w.float().numpy() * 20
+    n = 20000
+    T = np.full(n, 0.8, np.float32)
+    ids, _, y = O.sample(np.repeat(xs, n, 0), ws, "bf16", T, 7, np.zeros(n, np.int64), np.arange(n))
+    p = np.exp(y[0].astype(np.float64) - y[0].max())
+    p /= p.sum()
+    counts = np.bincount(ids, minlength=6)
+    assert stats.chisquare(counts, p * n).pvalue > 1e-4, (counts, p * n)
+
+
+def test_sample_rows_and_invalid():
+    x, w = make(22, 5, 128, 300, "f16")
+    xs, ws = x.float().numpy(), w.float().numpy()
+    T = np.array([0.0, 1.0, -1.0, np.nan, 0.5], np.float32)
+    ids, z, _ = O.sample(xs, ws, "f16", T, 3, np.arange(5), np.zeros(5, np.int64))
+    g, _, _ = O.greedy(xs, ws, "f16")
+    assert ids[0] == g[0] and ids[2] == -1 and ids[3] == -1
+    assert ids[1] == int(np.argmax(z[1])) and ids[4] == int(np.argmax(z[4]))

@@ -23,7 +23,7 @@ KIND_ALL = 7     # MIS_KIND_ALL
 EXPORTED = ("mis_workspace_bytes", "mis_workspace_init", "mis_sample", "mis_sample_profiled", "mis_sample_ex",
             "mis_sample_noalloc", "mis_fill_uniforms", "mis_context_create",
             "mis_paged_attention_workspace_bytes", "mis_paged_attention", "mis_gather_kv",
-            "mis_lm_head_greedy_workspace_bytes", "mis_lm_head_greedy", "mis_context_destroy", "mis_strerror", "mis_last_hip_error", "mis_abi_version")
+            "mis_lm_head_greedy_workspace_bytes", "mis_lm_head_greedy", "mis_lm_head_sample", "mis_context_destroy", "mis_strerror", "mis_last_hip_error", "mis_abi_version")
 
 _lib = None
 
@@ -75,6 +75,8 @@ def load():
     lib.mis_lm_head_greedy_workspace_bytes.restype = ctypes.c_size_t
     lib.mis_lm_head_greedy.argtypes = [vp, i64, vp, i64, i64, i64, i64, ci, vp, vp, ctypes.c_size_t, vp]
     lib.mis_lm_head_greedy.restype = ci
+    lib.mis_lm_head_sample.argtypes = [vp, i64, vp, i64, i64, i64, i64, ci, vp, vp, vp, vp, ctypes.c_size_t, vp]
+    lib.mis_lm_head_sample.restype = ci
     lib.mis_context_create.argtypes = [ctypes.POINTER(vp)]
     lib.mis_context_create.restype = ctypes.c_int
     lib.mis_context_destroy.argtypes = [vp]

@@ -22,7 +22,9 @@
 #include <math.h>
 #include <stdint.h>
 
+#include "mis_common.h"
 #include "mis_lmhead.h"
+#include "mis_sampler.h"
 
 namespace mis {
 namespace {
@@ -81,10 +83,29 @@ __device__ __forceinline__ uint64_t pack(uint32_t k, int64_t v)
     return ((uint64_t)k << 32) | (uint64_t)(0xffffffffu - (uint32_t)v);
 }
 
-template <int DT>
+// The Gumbel noise of vocabulary rows v .. v + 3 (v a multiple of 4) for one
+// draw: Philox4x32-10 with key (seed low, seed high ^ step high) and counter
+// (v / 4, step low, request low, request high); word i gives u = (w >> 8) 2^-24
+// in [0, 1) and g = -log(-log(u)) (u = 0 gives -inf, never the maximum).
+__device__ __forceinline__ void gumbel4(const mis_rng_row &q, int64_t v, float *g)
+{
+    uint32_t c[4] = {(uint32_t)(v >> 2), (uint32_t)q.step, (uint32_t)q.request, (uint32_t)(q.request >> 32)};
+    philox4x32_10(c, (uint32_t)q.seed, (uint32_t)(q.seed >> 32) ^ (uint32_t)(q.step >> 32));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float u = (float)(c[i] >> 8) * 5.9604644775390625e-08f;
+        g[i] = -logf(-logf(u));
+    }
+}
+
+// SAMPLE: rows with temperature T > 0 take argmax(y + g) (the Gumbel-max draw
+// from softmax(y)), y = dtype(logit / T); rows with T = 0 the greedy key.  A
+// NaN or +inf y marks the row invalid (key 0xffffffff, k_lmh_merge gives -1).
+template <int DT, bool SAMPLE>
 __global__ __launch_bounds__(LMH_NT) void k_lmh_tile(const uint16_t *__restrict__ X, int64_t ldx,
                                                      const uint16_t *__restrict__ W, int64_t ldw, int64_t B, int64_t H,
-                                                     int64_t V, uint64_t *__restrict__ part)
+                                                     int64_t V, uint64_t *__restrict__ part, const float *__restrict__ temp,
+                                                     const mis_rng_row *__restrict__ rng)
 {
     __shared__ uint16_t xs[2][LMH_BG * LMH_XST];
     __shared__ uint64_t red[LMH_NW][LMH_BG];
@@ -177,16 +198,36 @@ __global__ __launch_bounds__(LMH_NT) void k_lmh_tile(const uint16_t *__restrict_
 #pragma unroll
     for (int ct = 0; ct < LMH_BG / 16; ++ct) {
         uint64_t best = 0ull;
+        float T = 0.0f;
+        mis_rng_row q = {0ull, 0ull, 0ull};
+        if constexpr (SAMPLE) {
+            const int64_t b = b0 + 16 * ct + col;
+            if (ct < nct && b < B) { T = temp[b]; q = rng[b]; }
+        }
 #pragma unroll
-        for (int rt = 0; rt < LMH_RT; ++rt)
+        for (int rt = 0; rt < LMH_RT; ++rt) {
+            float g[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            const int64_t vq = v0 + 32 * w + 16 * rt + 4 * qd;
+            if constexpr (SAMPLE) {
+                if (T > 0.0f) gumbel4(q, vq, g);
+            }
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int64_t v = v0 + 32 * w + 16 * rt + 4 * qd + r;
+                const int64_t v = vq + r;
                 if (v < V) {
-                    const uint64_t k = pack(val_key(round_dt<DT>(acc[rt][ct][r])), v);
+                    const float x = round_dt<DT>(acc[rt][ct][r]);
+                    uint32_t key;
+                    if (SAMPLE && T > 0.0f) {
+                        const float y = round_dt<DT>(x / T);
+                        key = (y != y || y == INFINITY) ? 0xffffffffu : val_key(y + g[r]);
+                    } else {
+                        key = val_key(x);
+                    }
+                    const uint64_t k = pack(key, v);
                     best = k > best ? k : best;
                 }
             }
+        }
 #pragma unroll
         for (int o = 16; o < 64; o <<= 1) {
             const uint64_t other = __shfl_xor(best, o, 64);
@@ -205,7 +246,7 @@ __global__ __launch_bounds__(LMH_NT) void k_lmh_tile(const uint16_t *__restrict_
 
 // One wave per sequence: the best key over the vocabulary tiles.
 __global__ __launch_bounds__(LMH_NT) void k_lmh_merge(const uint64_t *__restrict__ part, int64_t ntiles, int64_t B,
-                                                      int64_t *__restrict__ ids)
+                                                      int64_t *__restrict__ ids, const float *__restrict__ temp)
 {
     const int lane = threadIdx.x & 63;
     const int64_t b = (int64_t)blockIdx.x * LMH_NW + (threadIdx.x >> 6);
@@ -220,7 +261,14 @@ __global__ __launch_bounds__(LMH_NT) void k_lmh_merge(const uint64_t *__restrict
         const uint64_t other = __shfl_xor(best, o, 64);
         best = other > best ? other : best;
     }
-    if (lane == 0) ids[b] = (int64_t)(0xffffffffu - (uint32_t)(best & 0xffffffffu));
+    if (lane == 0) {
+        const float T = temp ? temp[b] : 0.0f;
+        const uint32_t k = (uint32_t)(best >> 32);
+        // a sampled row is invalid when a scaled logit is NaN or +inf, or when
+        // every one is -inf (nothing to sample); T < 0 or NaN is a bad parameter
+        const bool bad = temp && (!(T >= 0.0f) || (T > 0.0f && (k == 0xffffffffu || k <= 0x007fffffu)));
+        ids[b] = bad ? -1 : (int64_t)(0xffffffffu - (uint32_t)(best & 0xffffffffu));
+    }
 }
 
 }  // namespace
@@ -257,10 +305,46 @@ int mis_lm_head_greedy(const void *hidden, int64_t ldx, const void *weight, int6
     const uint16_t *x = reinterpret_cast<const uint16_t *>(hidden);
     const uint16_t *wt = reinterpret_cast<const uint16_t *>(weight);
     if (dtype == 1)
-        hipLaunchKernelGGL((k_lmh_tile<1>), grid, dim3(LMH_NT), 0, st, x, ldx, wt, ldw, B, H, V, part);
+        hipLaunchKernelGGL((k_lmh_tile<1, false>), grid, dim3(LMH_NT), 0, st, x, ldx, wt, ldw, B, H, V, part, nullptr,
+                           nullptr);
     else
-        hipLaunchKernelGGL((k_lmh_tile<2>), grid, dim3(LMH_NT), 0, st, x, ldx, wt, ldw, B, H, V, part);
-    hipLaunchKernelGGL(k_lmh_merge, dim3((unsigned)((B + LMH_NW - 1) / LMH_NW)), dim3(LMH_NT), 0, st, part, nt, B, ids);
+        hipLaunchKernelGGL((k_lmh_tile<2, false>), grid, dim3(LMH_NT), 0, st, x, ldx, wt, ldw, B, H, V, part, nullptr,
+                           nullptr);
+    hipLaunchKernelGGL(k_lmh_merge, dim3((unsigned)((B + LMH_NW - 1) / LMH_NW)), dim3(LMH_NT), 0, st, part, nt, B, ids,
+                       nullptr);
+    return hipGetLastError() == hipSuccess ? MIS_LMH_OK : MIS_LMH_ERR_HIP;
+}
+
+int mis_lm_head_sample(const void *hidden, int64_t ldx, const void *weight, int64_t ldw, int64_t B, int64_t H,
+                       int64_t V, int dtype, const float *temperature, const mis_rng_row *rng, int64_t *ids,
+                       void *workspace, size_t workspace_bytes, void *stream)
+{
+    using namespace mis;
+    if (B < 0 || H <= 0 || V <= 0 || ldx < H || ldw < H) return MIS_LMH_ERR_INVALID_ARG;
+    if (B == 0) return MIS_LMH_OK;
+    if (!hidden || !weight || !ids || !temperature || !rng) return MIS_LMH_ERR_INVALID_ARG;
+    if (dtype != 1 && dtype != 2) return MIS_LMH_ERR_UNSUPPORTED;
+    if (H % LMH_KB != 0) return MIS_LMH_ERR_UNSUPPORTED;
+    if (V >= ((int64_t)1 << 31) || B > 65535 * (int64_t)LMH_BG) return MIS_LMH_ERR_UNSUPPORTED;
+    if (((uintptr_t)hidden & 15u) || ((uintptr_t)weight & 15u) || (ldx & 7) || (ldw & 7))
+        return MIS_LMH_ERR_INVALID_ARG;
+    const int64_t nt = (V + LMH_VT - 1) / LMH_VT;
+    if (nt > 0x7fffffff) return MIS_LMH_ERR_UNSUPPORTED;
+    const size_t need = mis_lm_head_greedy_workspace_bytes(B, V);
+    if (!workspace || workspace_bytes < need || ((uintptr_t)workspace & 255u)) return MIS_LMH_ERR_WORKSPACE;
+    hipStream_t st = (hipStream_t)stream;
+    uint64_t *part = reinterpret_cast<uint64_t *>(workspace);
+    const dim3 grid((unsigned)nt, (unsigned)((B + LMH_BG - 1) / LMH_BG));
+    const uint16_t *x = reinterpret_cast<const uint16_t *>(hidden);
+    const uint16_t *wt = reinterpret_cast<const uint16_t *>(weight);
+    if (dtype == 1)
+        hipLaunchKernelGGL((k_lmh_tile<1, true>), grid, dim3(LMH_NT), 0, st, x, ldx, wt, ldw, B, H, V, part,
+                           temperature, rng);
+    else
+        hipLaunchKernelGGL((k_lmh_tile<2, true>), grid, dim3(LMH_NT), 0, st, x, ldx, wt, ldw, B, H, V, part,
+                           temperature, rng);
+    hipLaunchKernelGGL(k_lmh_merge, dim3((unsigned)((B + LMH_NW - 1) / LMH_NW)), dim3(LMH_NT), 0, st, part, nt, B, ids,
+                       temperature);
     return hipGetLastError() == hipSuccess ? MIS_LMH_OK : MIS_LMH_ERR_HIP;
 }
 

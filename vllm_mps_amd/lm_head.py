@@ -1,4 +1,4 @@
-"""The lm_head GEMM fused with the greedy sampler on the MI355X (HIP kernel
+"""The lm_head GEMM fused with the greedy / temperature sampler on the MI355X (HIP kernel
 ``mis_lmhead.hip``, C ABI ``include/mis_lmhead.h``).
 
 Replaces, for greedy rows, the producer of the decode step's logits (the
@@ -6,8 +6,11 @@ model's lm_head, ``models/llama_adapter.py:198-207``) together with the
 sampler's greedy branch (``torch.argmax(logits)``, ``model/sampler.py:32-34``):
 the logits are never written to HBM.  ``lm_head_greedy(hidden, weight)``
 returns ``argmax(dtype(hidden @ weight.T), dim=-1)`` with the sum in fp32 and
-one rounding to the model dtype, ties to the lowest index, NaN first.  There
-is no CPU path.
+one rounding to the model dtype, ties to the lowest index, NaN first.
+``lm_head_sample(hidden, weight, temperature, rng)`` also serves temperature-only
+rows (``model/sampler.py:37, :57-59`` with top-k 0 and top-p 1, the default
+parameters): the Gumbel-max draw argmax(dtype(logit / T) + g) from softmax,
+with g from a per-request counter-based generator.  There is no CPU path.
 """
 from __future__ import annotations
 
@@ -44,7 +47,57 @@ def lm_head_greedy(hidden: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
     rc = lib.mis_lm_head_greedy(hidden.data_ptr(), hidden.stride(0), weight.data_ptr(), weight.stride(0), B, H, V,
                                 _DT[hidden.dtype], ids.data_ptr(), ws.data_ptr(), ws.numel(),
                                 torch.cuda.current_stream(dev).cuda_stream)
+    _check(rc, "mis_lm_head_greedy")
+    return ids
+
+
+def _check(rc: int, what: str) -> None:
     if rc != 0:
         names = {1: "invalid argument", 2: "workspace", 3: "HIP launch failed", 4: "unsupported shape"}
-        raise _native.MisError(f"mis_lm_head_greedy failed: {names.get(rc, rc)}")
+        raise _native.MisError(f"{what} failed: {names.get(rc, rc)}")
+
+
+def lm_head_sample(hidden: torch.Tensor, weight: torch.Tensor, temperature, rng) -> torch.Tensor:
+    """Greedy and temperature-only rows in one fused call (``mis_lm_head_sample``):
+    temperature [B] (0 = greedy), rng = (seed, requests [B], steps [B]) keying
+    each row's Gumbel noise (a request's token depends only on its logits and
+    (seed, request, step)).  int64 ids [B] on the device; -1 for an invalid
+    row.  Top-k / top-p rows need the unfused path."""
+    if hidden.device.type != "cuda" or weight.device != hidden.device:
+        raise _native.MisError("lm_head_sample needs hidden and weight on one ROCm device; there is no CPU path")
+    if hidden.dtype not in _DT or weight.dtype != hidden.dtype:
+        raise ValueError("hidden and weight must both be float16 or both bfloat16")
+    if hidden.dim() != 2 or weight.dim() != 2 or hidden.shape[1] != weight.shape[1]:
+        raise ValueError("hidden must be [B, H] and weight [V, H]")
+    if hidden.stride(1) != 1 or weight.stride(1) != 1:
+        raise ValueError("hidden and weight rows must be contiguous")
+    lib = _native.load()
+    B, H = hidden.shape
+    V = weight.shape[0]
+    dev = hidden.device
+    t = torch.as_tensor(temperature, dtype=torch.float32).to(dev).reshape(-1).contiguous()
+    seed, requests, steps = rng
+    req = torch.as_tensor(requests, dtype=torch.int64).reshape(-1)
+    stp = torch.as_tensor(steps, dtype=torch.int64).reshape(-1)
+    if t.numel() != B or req.numel() != B or stp.numel() != B:
+        raise ValueError("temperature, requests and steps need one entry per row")
+    rows = torch.stack([torch.full((B,), _i64(seed), dtype=torch.int64), req, stp], dim=1)   # mis_rng_row
+    rows = rows.contiguous().to(dev)
+    ids = torch.empty(B, dtype=torch.int64, device=dev)
+    need = int(lib.mis_lm_head_greedy_workspace_bytes(B, V))
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    ws = _workspace.get(idx)
+    if ws is None or ws.numel() < need:
+        ws = torch.empty(need, dtype=torch.uint8, device=dev)
+        _workspace[idx] = ws
+    rc = lib.mis_lm_head_sample(hidden.data_ptr(), hidden.stride(0), weight.data_ptr(), weight.stride(0), B, H, V,
+                                _DT[hidden.dtype], t.data_ptr(), rows.data_ptr(), ids.data_ptr(), ws.data_ptr(),
+                                ws.numel(), torch.cuda.current_stream(dev).cuda_stream)
+    _check(rc, "mis_lm_head_sample")
     return ids
+
+
+def _i64(x: int) -> int:
+    """A 64-bit unsigned value as the int64 with the same bits."""
+    x = int(x) & 0xFFFFFFFFFFFFFFFF
+    return x - (1 << 64) if x >= 1 << 63 else x
