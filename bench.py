@@ -297,9 +297,18 @@ def bench_lmhead(args):
         torch.cuda.synchronize()
         return start.elapsed_time(end) / K
 
+    # temperature-only rows (T = 1, the default parameters): the fused Gumbel-max
+    # draw against the GEMM + this build's sampler with the same rows
+    ones = torch.ones(B, device=dev)
+    rng_rows = (1234, np.arange(B), np.zeros(B, dtype=np.int64))
+    fused_t1 = lambda: LH.lm_head_sample(x, w, ones, rng_rows)
+    packed_t1 = pack_params(ones, torch.zeros(B, dtype=torch.int32, device=dev), ones, torch.rand(B, device=dev))
+    unfused_t1 = lambda: smp.sample_packed(torch.matmul(x, wt), packed_t1, out=ids_buf)
     ms = timed(fused)
     ms_unfused = timed(unfused)
     ms_unfused_mis = timed(unfused_mis)
+    ms_t1 = timed(fused_t1)
+    ms_unfused_t1 = timed(unfused_t1)
     same = bool(torch.equal(fused(), unfused())) and bool(torch.equal(fused(), unfused_mis().clone()))
     copy_calibration(args.copy_calib_mib, dev)
     alg = V * H * 2 + B * H * 2 + B * 8           # the weight read once, the hidden states, the ids
@@ -316,6 +325,8 @@ def bench_lmhead(args):
         "speedup_vs_unfused": round(ms_unfused / ms, 3),
         "unfused_mis_sampler_ms_per_step": round(ms_unfused_mis, 5),
         "speedup_vs_unfused_mis_sampler": round(ms_unfused_mis / ms, 3),
+        "temperature_rows": {"fused_ms_per_step": round(ms_t1, 5), "unfused_mis_sampler_ms_per_step": round(ms_unfused_t1, 5),
+                             "speedup": round(ms_unfused_t1 / ms_t1, 3)},
         "ids_equal_unfused": same,
         "tflops": round(flops / (ms / 1e3) / 1e12, 1),
         "roofline": {"bound": "hbm", "kernel": "k_lmh_tile + k_lmh_merge (one call)", "achieved": round(achieved, 1),
