@@ -300,8 +300,8 @@ def bench_lmhead(args):
     # temperature-only rows (T = 1, the default parameters): the fused Gumbel-max
     # draw against the GEMM + this build's sampler with the same rows
     ones = torch.ones(B, device=dev)
-    rng_rows = (1234, np.arange(B), np.zeros(B, dtype=np.int64))
-    fused_t1 = lambda: LH.lm_head_sample(x, w, ones, rng_rows)
+    rows_dev = LH.rng_rows((1234, np.arange(B), np.zeros(B, dtype=np.int64)), B, dev)
+    fused_t1 = lambda: LH.lm_head_sample(x, w, ones, rows_dev)
     packed_t1 = pack_params(ones, torch.zeros(B, dtype=torch.int32, device=dev), ones, torch.rand(B, device=dev))
     unfused_t1 = lambda: smp.sample_packed(torch.matmul(x, wt), packed_t1, out=ids_buf)
     ms = timed(fused)

@@ -141,3 +141,13 @@ def test_lm_head_sample_follows_softmax(device):
     p /= p.sum()
     print(f"[lmhead-sample] frequencies {np.bincount(got, minlength=8)} expected {np.round(p * n).astype(int)}", flush=True)
     assert stats.chisquare(np.bincount(got, minlength=8), p * n).pvalue > 1e-4
+
+
+def test_lm_head_sample_device_rng_rows(device):
+    """Records built once on the device (rng_rows) give the same draws as the tuple form."""
+    x, w = make(51, 9, 256, 3000, "f16")
+    T = torch.full((9,), 0.9)
+    rng = (77, np.arange(9) * 1000, np.full(9, 5))
+    a = LH.lm_head_sample(x.to(device), w.to(device), T, rng)
+    b = LH.lm_head_sample(x.to(device), w.to(device), T.to(device), LH.rng_rows(rng, 9, device))
+    assert torch.equal(a, b)

@@ -61,8 +61,9 @@ def lm_head_sample(hidden: torch.Tensor, weight: torch.Tensor, temperature, rng)
     """Greedy and temperature-only rows in one fused call (``mis_lm_head_sample``):
     temperature [B] (0 = greedy), rng = (seed, requests [B], steps [B]) keying
     each row's Gumbel noise (a request's token depends only on its logits and
-    (seed, request, step)).  int64 ids [B] on the device; -1 for an invalid
-    row.  Top-k / top-p rows need the unfused path."""
+    (seed, request, step)), or those records already on the device
+    (``rng_rows``).  int64 ids [B] on the device; -1 for an invalid row.
+    Top-k / top-p rows need the unfused path."""
     if hidden.device.type != "cuda" or weight.device != hidden.device:
         raise _native.MisError("lm_head_sample needs hidden and weight on one ROCm device; there is no CPU path")
     if hidden.dtype not in _DT or weight.dtype != hidden.dtype:
@@ -76,13 +77,13 @@ def lm_head_sample(hidden: torch.Tensor, weight: torch.Tensor, temperature, rng)
     V = weight.shape[0]
     dev = hidden.device
     t = torch.as_tensor(temperature, dtype=torch.float32).to(dev).reshape(-1).contiguous()
-    seed, requests, steps = rng
-    req = torch.as_tensor(requests, dtype=torch.int64).reshape(-1)
-    stp = torch.as_tensor(steps, dtype=torch.int64).reshape(-1)
-    if t.numel() != B or req.numel() != B or stp.numel() != B:
-        raise ValueError("temperature, requests and steps need one entry per row")
-    rows = torch.stack([torch.full((B,), _i64(seed), dtype=torch.int64), req, stp], dim=1)   # mis_rng_row
-    rows = rows.contiguous().to(dev)
+    if isinstance(rng, torch.Tensor):
+        rows = rng                             # already [B, 3] int64 (mis_rng_row) on the device
+    else:
+        rows = rng_rows(rng, B, dev)
+    if t.numel() != B or rows.shape != (B, 3) or rows.dtype != torch.int64 or rows.device != dev \
+            or not rows.is_contiguous():
+        raise ValueError("temperature needs one entry per row and rng (seed, requests, steps) one per row")
     ids = torch.empty(B, dtype=torch.int64, device=dev)
     need = int(lib.mis_lm_head_greedy_workspace_bytes(B, V))
     idx = dev.index if dev.index is not None else torch.cuda.current_device()
@@ -95,6 +96,19 @@ def lm_head_sample(hidden: torch.Tensor, weight: torch.Tensor, temperature, rng)
                                 ws.numel(), torch.cuda.current_stream(dev).cuda_stream)
     _check(rc, "mis_lm_head_sample")
     return ids
+
+
+def rng_rows(rng, B: int, device) -> torch.Tensor:
+    """(seed, requests [B], steps [B]) -> the [B, 3] int64 mis_rng_row records on `device`;
+    build them once per step and pass the tensor to lm_head_sample to keep the
+    host-to-device copy out of the call."""
+    seed, requests, steps = rng
+    req = torch.as_tensor(requests, dtype=torch.int64).reshape(-1)
+    stp = torch.as_tensor(steps, dtype=torch.int64).reshape(-1)
+    if req.numel() != B or stp.numel() != B:
+        raise ValueError("requests and steps need one entry per row")
+    rows = torch.stack([torch.full((B,), _i64(seed), dtype=torch.int64), req, stp], dim=1)
+    return rows.contiguous().to(device)
 
 
 def _i64(x: int) -> int:
