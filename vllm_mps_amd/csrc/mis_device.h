@@ -386,21 +386,42 @@ __device__ __forceinline__ int wave_find_asc(const double *v, int n, double targ
     return sel;
 }
 
-// Bitonic sort, descending, of n <= cap (u64 key, f64 value) pairs in LDS by
-// all threads of the block; entries n .. pow2(n)-1 are padded with key 0, so
-// the arrays must hold pow2(n) entries.
-// Bitonic sort, descending, of k[0..n) with payload e (n <= CAP; CAP and the
-// block size NTH powers of two).  Padding keys are 0, so every real key must
-// be > 0.  Element i sits in thread i / PT (PT = CAP / NTH, at most 4) at
-// register slot i % PT: compare-exchanges between slots of one thread work on
-// registers, between lanes of one wave on shuffles, and only partners in
-// other waves go through LDS (k and e, CAP entries each).
+// Sort, descending, of k[0..n) with payload e (n <= CAP; CAP and the block
+// size NTH powers of two), by all threads of the block; afterwards entries
+// n .. CAP-1 hold key 0 and payload 0, and every real key must be > 0.
+// Up to RANK_N entries: each of the first n threads counts the keys above
+// its own (equal keys ordered by position) and writes its pair to that rank.
+// Beyond: a bitonic sort, element i in thread i / PT (PT = CAP / NTH, at most
+// 4) at register slot i % PT: compare-exchanges between slots of one thread
+// work on registers, between lanes of one wave on shuffles, and only partners
+// in other waves go through LDS (k and e, CAP entries each).
+constexpr int RANK_N = 256;
 template <int NTH, int CAP>
 __device__ __forceinline__ void block_sort_desc(uint64_t *k, double *e, int n)
 {
     constexpr int PT = CAP / NTH;
     static_assert(PT == 1 || PT == 2 || PT == 4, "1, 2 or 4 elements per thread");
+    static_assert(RANK_N <= NTH, "one element per thread in the rank sort");
     const int tid = threadIdx.x;
+    if (n <= RANK_N) {
+        __syncthreads();
+        uint64_t kt = 0ull;
+        double et = 0.0;
+        int rank = 0;
+        if (tid < n) {
+            kt = k[tid];
+            et = e[tid];
+            for (int j = 0; j < n; ++j) {
+                const uint64_t kj = k[j];
+                rank += (kj > kt || (kj == kt && j < tid)) ? 1 : 0;
+            }
+        }
+        __syncthreads();
+        if (tid < n) { k[rank] = kt; e[rank] = et; }
+        for (int i = n + tid; i < CAP; i += NTH) { k[i] = 0ull; e[i] = 0.0; }
+        __syncthreads();
+        return;
+    }
     int npow = 1;
     while (npow < n) npow <<= 1;
     uint64_t kv[PT];
