@@ -304,11 +304,11 @@ def bench_lmhead(args):
     fused_t1 = lambda: LH.lm_head_sample(x, w, ones, rows_dev)
     packed_t1 = pack_params(ones, torch.zeros(B, dtype=torch.int32, device=dev), ones, torch.rand(B, device=dev))
     unfused_t1 = lambda: smp.sample_packed(torch.matmul(x, wt), packed_t1, out=ids_buf)
-    ms = timed(fused)
-    ms_unfused = timed(unfused)
-    ms_unfused_mis = timed(unfused_mis)
-    ms_t1 = timed(fused_t1)
-    ms_unfused_t1 = timed(unfused_t1)
+    # every pipeline twice, round robin; the second round is reported (the
+    # first one also brings the clocks up to speed for the pipeline timed first)
+    for _ in range(2):
+        ms, ms_unfused, ms_unfused_mis, ms_t1, ms_unfused_t1 = (
+            timed(f) for f in (fused, unfused, unfused_mis, fused_t1, unfused_t1))
     same = bool(torch.equal(fused(), unfused())) and bool(torch.equal(fused(), unfused_mis().clone()))
     copy_calibration(args.copy_calib_mib, dev)
     alg = V * H * 2 + B * H * 2 + B * 8           # the weight read once, the hidden states, the ids

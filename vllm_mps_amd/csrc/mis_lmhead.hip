@@ -7,9 +7,10 @@
 // v_mfma_f32_16x16x16 (f16 or bf16) with the weight rows as A (read straight
 // from HBM, 32 contiguous bytes per lane per block of 64 hidden dims) and the
 // hidden states as B (the block staged in LDS once per workgroup, double
-// buffered).  The products of two 16-bit values are exact in fp32; the sums
-// are fp32.  The weight blocks two ahead and the next hidden block are
-// loaded while the current block's MFMAs run.  The epilogue rounds each logit to the model dtype
+// buffered); each tile walks the hidden blocks from its own starting block.
+// The products of two 16-bit values are exact in fp32; the sums are fp32.
+// The weight blocks two ahead and the next hidden block are loaded while the
+// current block's MFMAs run.  The epilogue rounds each logit to the model dtype
 // and keeps, per sequence, the tile's best (dtype value, lowest index): a
 // 64-bit key, larger is better.  k_lmh_merge takes the maximum key over the
 // tiles of each sequence.
@@ -158,16 +159,21 @@ __global__ __launch_bounds__(LMH_NT) void k_lmh_tile(const uint16_t *__restrict_
     // three register sets of weight blocks: block k + 2 is issued as block k's
     // MFMAs start, so each block has two iterations to arrive
     uint4 xr[2], w0[LMH_RT][2], w1[LMH_RT][2], w2[LMH_RT][2];
-    load_x(0, xr);
-    load_w(0, w0);
-    if (nkb > 1) load_w(1, w1);
+    // this tile walks the hidden blocks from block vt mod nkb, wrapping: the
+    // tiles in flight then read different column ranges of their rows instead
+    // of all sweeping one 128-byte column of rows 8 KB apart
+    const int koff = (int)(vt % (int64_t)nkb);
+    auto blk = [&](int kb) { const int k = kb + koff; return k >= nkb ? k - nkb : k; };
+    load_x(blk(0), xr);
+    load_w(blk(0), w0);
+    if (nkb > 1) load_w(blk(1), w1);
     store_x(0, xr);
     // iteration kb: weights in `cur`, block kb + 2 into `fut` (the set block
     // kb - 1 used), hidden block kb in LDS buffer kb & 1
     auto step = [&](int kb, uint4 (*cur)[2], uint4 (*fut)[2]) {
         __syncthreads();                       // block kb staged; the other buffer free
-        if (kb + 1 < nkb) load_x(kb + 1, xr);
-        if (kb + 2 < nkb) load_w(kb + 2, fut);
+        if (kb + 1 < nkb) load_x(blk(kb + 1), xr);
+        if (kb + 2 < nkb) load_w(blk(kb + 2), fut);
         const uint16_t *xb = xs[kb & 1];
         // step s uses dims 4 s .. 4 s + 3 of each lane's 16 (the same
         // permutation of the block's dims for both operands)
