@@ -1534,22 +1534,16 @@ __global__ __launch_bounds__(NT) void k_sample(Args a, int part)
     const int G = L.G;
     const uint32_t task = blockIdx.x;  // a row's chunks have consecutive indices
     const int chunk = (int)(task % (uint32_t)G);
-    int row = (int)(task / (uint32_t)G);
-    if (part != K1_ALL) {
-        // the split halves take their rows from the launch order k_rows wrote
-        // (fp32 top-p rows first), so a half's working workgroups lead its grid
-        const int32_t *perm = reinterpret_cast<const int32_t *>(a.ws + L.perm);
-        const int ntp = uni(ldp(&perm[L.B]));
-        const int r = part == K1_TOPP32 ? row : ntp + row;
-        if ((part == K1_TOPP32 && row >= ntp) || r >= (int)L.B) return;
-        row = uni(ldp(&perm[r]));
-    }
+    const int row = (int)(task / (uint32_t)G);
     const int64_t V = a.V;
     const int64_t base = (int64_t)chunk * CH;
     const char *rowp = a.logits + (int64_t)row * a.stride_bytes;
     mis_row_params P = a.params[row];
     P.temperature = uni(P.temperature); P.top_k = uni(P.top_k); P.top_p = uni(P.top_p); P.uniform = uni(P.uniform);
     const RowPlan pl = plan_row(P, V);
+    // the split halves: each launch covers every (row, chunk) and keeps its
+    // own rows (the fp32 top-p rows, or the others)
+    if (part != K1_ALL && (part == K1_TOPP32) != (DT == F32 && pl.mode == M_TOPP)) return;
     ChunkSum *csr = reinterpret_cast<ChunkSum *>(a.ws + L.chunks) + (size_t)row * G;
     ChunkSum *cs = csr + chunk;
     RoundBuf *rb = reinterpret_cast<RoundBuf *>(a.ws + L.rbuf) + (size_t)row * G + chunk;
@@ -2156,35 +2150,6 @@ __device__ __forceinline__ int fine_bin(float y, float lo, float scf)
     return (int)fminf(fmaxf(floorf((y - lo) * scf), 0.0f), (float)(FH - 1));
 }
 
-// The launch order of an fp32 batch split between the top-p passes and the
-// rest: perm[0, n) = the fp32 top-p rows in row order, perm[n, B) = the
-// others, perm[B] = n.  One workgroup at the start of the step.
-__global__ __launch_bounds__(NT) void k_rows(Args a)
-{
-    __shared__ Red red;
-    int32_t *perm = reinterpret_cast<int32_t *>(a.ws + a.L.perm);
-    const int tid = threadIdx.x, B = (int)a.L.B;
-    uint32_t ntp = 0u;
-    for (int r0 = 0; r0 < B; r0 += NT) {  // top-p rows: their rank in row order
-        const int row = r0 + tid;
-        const bool t = row < B && plan_row(a.params[row], a.V).mode == M_TOPP;
-        uint32_t tot;
-        const uint32_t ex = block_excl_scan<uint32_t>(t ? 1u : 0u, red, &tot);
-        if (t) perm[ntp + ex] = row;
-        ntp += tot;
-    }
-    uint32_t nother = 0u;
-    for (int r0 = 0; r0 < B; r0 += NT) {  // the others after them
-        const int row = r0 + tid;
-        const bool o = row < B && plan_row(a.params[row], a.V).mode != M_TOPP;
-        uint32_t tot;
-        const uint32_t ex = block_excl_scan<uint32_t>(o ? 1u : 0u, red, &tot);
-        if (o) perm[ntp + nother + ex] = row;
-        nother += tot;
-    }
-    if (tid == 0) perm[B] = (int32_t)ntp;
-}
-
 // LDS of k_tp_hist
 constexpr int LCAP = 4096;          // band elements of a chunk binned from a dense LDS list
 struct HistSmem {
@@ -2209,12 +2174,9 @@ __global__ __launch_bounds__(NT) void k_tp_hist(Args a)
     constexpr int VEC = Traits<F32>::VEC;
     const Layout &L = a.L;
     const int tid = threadIdx.x, G = L.G;
-    // workgroup i serves chunk i % G of the (i / G)-th fp32 top-p row (k_rows)
+    // workgroup i serves chunk i % G of row i / G, if an fp32 top-p row
     const int g = (int)(blockIdx.x % (unsigned)G);
-    const int32_t *perm = reinterpret_cast<const int32_t *>(a.ws + L.perm);
-    const int rk = (int)(blockIdx.x / (unsigned)G);
-    if (rk >= uni(ldp(&perm[L.B]))) return;
-    const int row = uni(ldp(&perm[rk]));
+    const int row = (int)(blockIdx.x / (unsigned)G);
     mis_row_params P = a.params[row];
     P.temperature = uni(P.temperature); P.top_k = uni(P.top_k); P.top_p = uni(P.top_p); P.uniform = uni(P.uniform);
     const RowPlan pl = plan_row(P, a.V);
@@ -3178,7 +3140,7 @@ static hipError_t launch_chunks(const Args &a, hipStream_t st, int part)
     }
 }
 
-// events (optional, nev = 3 or 4): [0] before the chunk pass (after k_rows), [1] after the
+// events (optional, nev = 3 or 4): [0] before the chunk pass, [1] after the
 // chunk pass on the caller's stream (with the split, its fp32 top-p rows'),
 // [2] after the row pass (before the debug emit), [3] after the side stream's
 // chunk pass (recorded only with the split: one more marker on the caller's
@@ -3187,8 +3149,8 @@ static hipError_t launch_chunks(const Args &a, hipStream_t st, int part)
 // stream from the caller, the other rows' chunk pass and row pass run on the
 // side stream beside the top-p rows' chunk pass and top-p passes; the rows
 // either deferred follow once both are done.  Without a side stream the same
-// kernels run in one stream.  k_rows first writes the launch order the split
-// chunk-pass halves and k_tp_hist read.
+// kernels run in one stream.  Each chunk-pass half covers every (row, chunk)
+// and keeps the workgroups of its own rows.
 template <int DT>
 static hipError_t launch_dt(const Args &a, float *probs, uint32_t *keep, hipStream_t st, unsigned kinds,
                             void *const *ev, int nev, const SideStreams *sd)
@@ -3198,8 +3160,7 @@ static hipError_t launch_dt(const Args &a, float *probs, uint32_t *keep, hipStre
     const bool tp32 = DT == F32 && (kinds & MIS_KIND_TOPP32);
     const bool others = (kinds & MIS_KIND_OTHER) != 0u;
     const bool side = tp32 && others && sd != nullptr;
-    if (tp32) hipLaunchKernelGGL(k_rows, dim3(1), dim3(NT), 0, st, a);
-    // events[0] opens the chunk pass: after k_rows, which only orders the rows
+    // events[0] opens the chunk pass
     if (ev && (e = hipEventRecord((hipEvent_t)ev[0], st)) != hipSuccess) return e;
     if (side) {
         if ((e = hipEventRecord(sd->fork, st)) != hipSuccess) return e;

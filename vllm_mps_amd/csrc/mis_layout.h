@@ -132,7 +132,7 @@ struct Layout {
     int ept, G;
     int ccap;                       // candidate slots per (row, chunk)
     int t16;                        // fp16/bf16 and B < T16_ROWS: the t16 passes serve the top-p rows
-    size_t rowout, chunks, rbuf, cand, topc, topr, stash, perm, t16h, t16c, t16r, total;
+    size_t rowout, chunks, rbuf, cand, topc, topr, stash, t16h, t16c, t16r, total;
 };
 
 inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -168,8 +168,6 @@ inline Layout make_layout(int64_t B, int64_t V, int dtype)
     L.topc = off;   off = align256(off + (f32 ? sizeof(TopChunk) * BG : 0));
     L.topr = off;   off = align256(off + (f32 ? sizeof(TopRow) * (size_t)B : 0));
     L.stash = off;  off = align256(off + (f32 ? sizeof(Cand) * (size_t)STASH_CAP * BG : 0));
-    // fp32: the rows in launch order (top-p rows first) and their count
-    L.perm = off;   off = align256(off + (f32 ? sizeof(int32_t) * ((size_t)B + 1) : 0));
     // fp16/bf16 top-p of a small batch: per-row key histograms, per-chunk
     // masses, per-row cuts
     L.t16 = (!f32 && B < T16_ROWS) ? 1 : 0;
