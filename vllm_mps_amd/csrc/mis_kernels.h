@@ -133,7 +133,7 @@ struct Smem {
     double cw[G_MAX];          // per-chunk kept weight
     double etab[ETAB_N];       // 2^(j/64) for dexp
     union {
-        Cand cc[CCAP];         // a small-k row's candidates
+        Cand cc[CCAP_FIN];     // a small-k row's candidates
         struct { uint32_t cnt[RUN_CAP]; uint32_t rkey[RUN_CAP]; uint32_t rcnt[RUN_CAP]; float rp[RUN_CAP]; } r;  // 16-bit chain runs
     } w;
     double chs[G_MAX];         // per-chunk rescale to the row max
@@ -1001,7 +1001,7 @@ __device__ __forceinline__ bool leader_smallk(Smem &sm, const RowCx &c, const Ro
     };
     constexpr int BATCH = 8;  // candidate loads in flight per thread
     // the row's candidates, copied once into LDS when they fit
-    const bool cached = ntot <= (uint32_t)CCAP;
+    const bool cached = ntot <= (uint32_t)CCAP_FIN;
     if (cached) {
         for (uint32_t f0 = 0; f0 < ntot; f0 += NT * BATCH) {
             const Cand *cp[BATCH];

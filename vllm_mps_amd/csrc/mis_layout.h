@@ -18,11 +18,12 @@ constexpr int SURV_CAP = 1024;     // top-k survivors / top-p window held in LDS
 constexpr int K_PROBE = 512;       // fp16/bf16 top-p rows look for their cut among this many largest values
                                    // first (ties at the last one stay within SURV_CAP)
 constexpr int EPT_DEFAULT = 32;    // elements per thread of the chunk pass (64 when G would exceed G_MAX)
-constexpr int CCAP = 8192;         // small-k candidates of a row cached in LDS (64 KB)
+constexpr int CCAP = 8192;         // small-k candidates of a row cached in LDS by k_rowpass (64 KB)
+constexpr int CCAP_FIN = 4096;     // k_final's LDS cache of a row's candidates (32 KB; more are read from the workspace)
 constexpr int G_MAX = 256;         // chunks per row
 constexpr int CB_N = 128;          // coarse top-p bins below a chunk's max (float64, per wave)
 constexpr float CB_SCALE = 4.0f;   // coarse bin = floor(y * CB_SCALE): 1/4 unit of y, 32 units in all
-constexpr int REGION_MAX = 16;     // L1 bins per 16-bit chain pass at most (re-read path)
+constexpr int REGION_MAX = 8;      // L1 bins per 16-bit chain pass at most (re-read path)
 constexpr int RUN_CAP = REGION_MAX * 256;
 constexpr int TIE_CAP = 1024;
 constexpr uint32_t NCAND_OVERFLOW = 0xffffffffu;
